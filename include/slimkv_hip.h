@@ -1,0 +1,185 @@
+/*
+ * slimkv_hip.h -- C ABI of the MI355X (gfx950) compressed-cache attention library.
+ *
+ * Every entry point enqueues work on the caller's HIP stream (passed as `void*`,
+ * a hipStream_t), allocates nothing, never synchronises the host, and returns 0 on
+ * success or a negative error code; `slimkv_last_error()` then holds a message
+ * for the calling thread.  Tensors are device pointers.  bf16 data is passed as
+ * its 16-bit pattern.  Strides are in elements, the last dimension of every
+ * tensor is contiguous, and bf16 rows must start on 16-byte boundaries
+ * (strides and widths are multiples of 8 elements).  Workspaces are owned by the
+ * caller and sized by the matching `*_workspace` query; they need no clearing.
+ */
+#ifndef SLIMKV_HIP_H
+#define SLIMKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SLIMKV_OK 0
+#define SLIMKV_EINVAL (-1)   /* invalid shape, stride or argument */
+#define SLIMKV_EUNSUP (-2)   /* supported by the reference, not by this build */
+#define SLIMKV_EWORKSPACE (-3) /* workspace too small */
+#define SLIMKV_EHIP (-4)     /* HIP runtime error */
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* slimkv_last_error(void);
+
+/* ABI version of this header (bumped on any struct change). */
+int slimkv_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Split-K decode attention with GQA, bottom-right causality and LSE.
+ *
+ * Replaces the native forward of the reference decode extension,
+ *   slimkv_fa2_decode_320.forward(q, k, v, softmax_scale, causal, num_splits,
+ *                                 pack_q, cache_seqlens)
+ *   (kernels/fa2_decode/binding.cpp:35-121, exported at :123-130), and the
+ *   flash_attn call inside flash_forward (slimkv/llama3/fa2_decode.py:15-38).
+ * Semantics follow the reference eager attention
+ *   (slimkv/llama3/latent_decode.py:16-41): query head j uses KV head
+ *   j / (heads / kv_heads); with `causal` query i sees keys
+ *   [0, keys_b - queries + i]; a row that sees no key gets output 0 and
+ *   LSE -inf.  K and V widths may differ; no padding is needed.
+ * q   [B, Lq, Hq, Wk]  k [B, N, Hk, Wk]  v [B, N, Hk, Wv]  (BSHD, bf16)
+ * out [B, Lq, Hq, Wv]  bf16;  lse [B, Hq, Lq] fp32 contiguous (may be NULL)
+ * seqlens: optional device int32 [B] key counts (each <= keys).
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_attention_args {
+    const void* q;  int64_t q_sb, q_sl, q_sh;
+    const void* k;  int64_t k_sb, k_sn, k_sh;
+    const void* v;  int64_t v_sb, v_sn, v_sh;
+    void* out;      int64_t o_sb, o_sl, o_sh;
+    float* lse;
+    const int32_t* seqlens;
+    int64_t batch, queries, heads, kv_heads, keys, width_k, width_v;
+    double scale;
+    int32_t causal;
+    int32_t splits; /* 0 = automatic */
+} slimkv_attention_args;
+
+size_t slimkv_attention_workspace(const slimkv_attention_args* a);
+int slimkv_attention_forward(const slimkv_attention_args* a, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused reconstruction-free latent beacon decode for one attention layer.
+ *
+ * Replaces the attention core of slimkv.llama3.fa2_decode.decode
+ *   (slimkv/llama3/fa2_decode.py:143-164): query RoPE (optional, bf16-exact as
+ *   decode_kernels.py:44-51), raw branch over RoPE'd full-dim K/V
+ *   (:146-148), query absorption into U_K (project_query :41-46), latent branch
+ *   over un-RoPE'd beacon latents (:152-154), V lift through U_V
+ *   (project_value :49-54), bias folding (:157-163) and the LSE merge
+ *   (merge_attention :57-66) -- all under one online softmax.
+ * q       [B, Lq, Hq, D] bf16; rotated in-kernel at q_positions [B, Lq] when
+ *         `cos`/`sin` ([rope_rows, D] fp32) are given, else already rotated.
+ * raw_k/v [B, Nr, Hkv, D] bf16, K already rotated (sinks, tail, current token).
+ * lat_k   [B, Nl, Rk] bf16 and lat_v [B, Nl, Rv] bf16: global latent rows.
+ * up_k    [Hkv*D, Rk], up_v [Hkv*D, Rv]: nn.Linear weights of the beacon
+ *         up-projections, optional biases [Hkv*D].
+ * block_diagonal = 1 asserts that every off-diagonal (D x Rk/Hkv) block of
+ *         up_k and (D x Rv/Hkv) block of up_v is zero (per-KV-head bases); the
+ *         latent branch then reads only each head's own latent slice.
+ * lat_causal: bottom-right causal latent branch (the beacon-insertion step).
+ * out [B, Lq, Hq, D] bf16; lse [B, Hq, Lq] fp32 (may be NULL).
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_latent_decode_args {
+    const void* q;  int64_t q_sb, q_sl, q_sh;
+    const int64_t* q_positions; int64_t pos_sb;
+    const float* cos; const float* sin; int64_t rope_rows;
+    const void* raw_k; int64_t rk_sb, rk_sn, rk_sh;
+    const void* raw_v; int64_t rv_sb, rv_sn, rv_sh;
+    const int32_t* raw_lengths;
+    int64_t raw_keys;
+    const void* lat_k; int64_t lk_sb, lk_sn;
+    const void* lat_v; int64_t lv_sb, lv_sn;
+    const int32_t* lat_lengths;
+    int64_t lat_keys;
+    int32_t lat_causal;
+    int32_t block_diagonal;
+    const void* up_k; const void* up_k_bias;
+    const void* up_v; const void* up_v_bias;
+    int64_t batch, queries, heads, kv_heads, head_dim, rank_k, rank_v;
+    double scale;
+    void* out; int64_t o_sb, o_sl, o_sh;
+    float* lse;
+    int32_t raw_splits, lat_splits; /* 0 = automatic */
+} slimkv_latent_decode_args;
+
+size_t slimkv_latent_decode_workspace(const slimkv_latent_decode_args* a);
+int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decode RoPE of the query and the raw K cache, bf16-exact.
+ * Replaces decode_ops.fused_rope (slimkv/llama3/decode_ops.py:14-31) and its
+ * kernel (slimkv/llama3/decode_kernels.py:7-51).
+ * q [B, Hq, Lq, D], k [B, Hk, Nk, D] (BHSD, strided); outputs contiguous.
+ * Query position: q_positions[b*pos_sb + s].  Key position of slot s:
+ * s < sink -> s; s == Nk-1 -> q_positions[b*pos_sb]; else
+ * raw_indices[s - sink] + sink + history.
+ * out = bf16(bf16(x*bf16(cos)) + bf16(rotate_half(x)*bf16(sin))).
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_rope_decode_args {
+    const void* q; int64_t q_sb, q_sh, q_ss;
+    const void* k; int64_t k_sb, k_sh, k_ss;
+    void* out_q; void* out_k;
+    const float* cos; const float* sin; int64_t rope_rows;
+    const int64_t* q_positions; int64_t pos_sb;
+    const int64_t* raw_indices; /* may be NULL when no slot needs it */
+    int64_t raw_index_count;
+    int64_t batch, heads, kv_heads, queries, keys, dim, sink, history;
+} slimkv_rope_decode_args;
+
+int slimkv_rope_decode(const slimkv_rope_decode_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Prefill RoPE that leaves beacon K unrotated.
+ * Replaces prefill_ops.fused_prefill_rope (slimkv/llama3/prefill_ops.py:48-73)
+ * and prefill_rope_kernel (slimkv/llama3/prefill_kernels.py:7-53).
+ * Query slot s uses positions[b*pos_sb + Nk - Lq + s]; key slot s uses
+ * positions[b*pos_sb + s] unless it is a beacon: s in [sink, Nk-role_len) or
+ * roles[s - (Nk-role_len)] in {1, 2}, which is copied unchanged.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_prefill_rope_args {
+    const void* q; int64_t q_sb, q_sh, q_ss;
+    const void* k; int64_t k_sb, k_sh, k_ss;
+    void* out_q; int64_t oq_sb, oq_sh, oq_ss;
+    void* out_k; int64_t ok_sb, ok_sh, ok_ss;
+    const float* cos; const float* sin; int64_t rope_rows;
+    const int64_t* positions; int64_t pos_sb;
+    const int64_t* roles; int64_t role_len;
+    int64_t batch, heads, kv_heads, queries, keys, dim, sink;
+} slimkv_prefill_rope_args;
+
+int slimkv_prefill_rope(const slimkv_prefill_rope_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * LSE merge of two attention branches.
+ * Replaces decode_ops.fused_merge (slimkv/llama3/decode_ops.py:34-48) and
+ * merge_kernel (slimkv/llama3/decode_kernels.py:53-75):
+ * t = max(r,l) + log1p(exp(-|r-l|)); out = exp(r-t)*raw + exp(l-t)*latent.
+ * raw/latent [B, H, L, D] bf16 (strided), lse [B, H, L] fp32 (strided);
+ * out contiguous [B, H, L, D] bf16.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_merge_args {
+    const void* raw; int64_t r_sb, r_sh, r_sl;
+    const void* latent; int64_t l_sb, l_sh, l_sl;
+    const float* raw_lse; int64_t rl_sb, rl_sh, rl_sl;
+    const float* latent_lse; int64_t ll_sb, ll_sh, ll_sl;
+    void* out;
+    int64_t batch, heads, length, dim;
+} slimkv_merge_args;
+
+int slimkv_merge(const slimkv_merge_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLIMKV_HIP_H */

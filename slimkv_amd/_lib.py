@@ -1,0 +1,139 @@
+"""ctypes binding of the C ABI in include/slimkv_hip.h.
+
+The shared library is the only compute path.  Loading fails loudly when it is
+missing: there is no CPU or PyTorch fallback behind any entry point.
+"""
+import ctypes
+import os
+from functools import lru_cache
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().parent / 'libslimkv_hip.so'
+
+c_i64 = ctypes.c_int64
+c_i32 = ctypes.c_int32
+c_ptr = ctypes.c_void_p
+c_f64 = ctypes.c_double
+
+
+def _struct(name, fields):
+    return type(name, (ctypes.Structure,), {'_fields_': fields})
+
+
+def _i64s(*names):
+    return [(n, c_i64) for n in names]
+
+
+AttentionArgs = _struct('slimkv_attention_args', [
+    ('q', c_ptr), *_i64s('q_sb', 'q_sl', 'q_sh'),
+    ('k', c_ptr), *_i64s('k_sb', 'k_sn', 'k_sh'),
+    ('v', c_ptr), *_i64s('v_sb', 'v_sn', 'v_sh'),
+    ('out', c_ptr), *_i64s('o_sb', 'o_sl', 'o_sh'),
+    ('lse', c_ptr),
+    ('seqlens', c_ptr),
+    *_i64s('batch', 'queries', 'heads', 'kv_heads', 'keys', 'width_k', 'width_v'),
+    ('scale', c_f64),
+    ('causal', c_i32),
+    ('splits', c_i32),
+])
+
+LatentDecodeArgs = _struct('slimkv_latent_decode_args', [
+    ('q', c_ptr), *_i64s('q_sb', 'q_sl', 'q_sh'),
+    ('q_positions', c_ptr), ('pos_sb', c_i64),
+    ('cos', c_ptr), ('sin', c_ptr), ('rope_rows', c_i64),
+    ('raw_k', c_ptr), *_i64s('rk_sb', 'rk_sn', 'rk_sh'),
+    ('raw_v', c_ptr), *_i64s('rv_sb', 'rv_sn', 'rv_sh'),
+    ('raw_lengths', c_ptr),
+    ('raw_keys', c_i64),
+    ('lat_k', c_ptr), *_i64s('lk_sb', 'lk_sn'),
+    ('lat_v', c_ptr), *_i64s('lv_sb', 'lv_sn'),
+    ('lat_lengths', c_ptr),
+    ('lat_keys', c_i64),
+    ('lat_causal', c_i32),
+    ('block_diagonal', c_i32),
+    ('up_k', c_ptr), ('up_k_bias', c_ptr),
+    ('up_v', c_ptr), ('up_v_bias', c_ptr),
+    *_i64s('batch', 'queries', 'heads', 'kv_heads', 'head_dim', 'rank_k', 'rank_v'),
+    ('scale', c_f64),
+    ('out', c_ptr), *_i64s('o_sb', 'o_sl', 'o_sh'),
+    ('lse', c_ptr),
+    ('raw_splits', c_i32), ('lat_splits', c_i32),
+])
+
+RopeDecodeArgs = _struct('slimkv_rope_decode_args', [
+    ('q', c_ptr), *_i64s('q_sb', 'q_sh', 'q_ss'),
+    ('k', c_ptr), *_i64s('k_sb', 'k_sh', 'k_ss'),
+    ('out_q', c_ptr), ('out_k', c_ptr),
+    ('cos', c_ptr), ('sin', c_ptr), ('rope_rows', c_i64),
+    ('q_positions', c_ptr), ('pos_sb', c_i64),
+    ('raw_indices', c_ptr), ('raw_index_count', c_i64),
+    *_i64s('batch', 'heads', 'kv_heads', 'queries', 'keys', 'dim', 'sink', 'history'),
+])
+
+PrefillRopeArgs = _struct('slimkv_prefill_rope_args', [
+    ('q', c_ptr), *_i64s('q_sb', 'q_sh', 'q_ss'),
+    ('k', c_ptr), *_i64s('k_sb', 'k_sh', 'k_ss'),
+    ('out_q', c_ptr), *_i64s('oq_sb', 'oq_sh', 'oq_ss'),
+    ('out_k', c_ptr), *_i64s('ok_sb', 'ok_sh', 'ok_ss'),
+    ('cos', c_ptr), ('sin', c_ptr), ('rope_rows', c_i64),
+    ('positions', c_ptr), ('pos_sb', c_i64),
+    ('roles', c_ptr), ('role_len', c_i64),
+    *_i64s('batch', 'heads', 'kv_heads', 'queries', 'keys', 'dim', 'sink'),
+])
+
+MergeArgs = _struct('slimkv_merge_args', [
+    ('raw', c_ptr), *_i64s('r_sb', 'r_sh', 'r_sl'),
+    ('latent', c_ptr), *_i64s('l_sb', 'l_sh', 'l_sl'),
+    ('raw_lse', c_ptr), *_i64s('rl_sb', 'rl_sh', 'rl_sl'),
+    ('latent_lse', c_ptr), *_i64s('ll_sb', 'll_sh', 'll_sl'),
+    ('out', c_ptr),
+    *_i64s('batch', 'heads', 'length', 'dim'),
+])
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    'slimkv_last_error': (ctypes.c_char_p, []),
+    'slimkv_abi_version': (ctypes.c_int, []),
+    'slimkv_attention_workspace': (ctypes.c_size_t, [ctypes.POINTER(AttentionArgs)]),
+    'slimkv_attention_forward': (ctypes.c_int, [ctypes.POINTER(AttentionArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(LatentDecodeArgs)]),
+    'slimkv_latent_decode': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_rope_decode': (ctypes.c_int, [ctypes.POINTER(RopeDecodeArgs), c_ptr]),
+    'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
+    'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),
+}
+
+ABI_VERSION = 1
+
+
+class SlimKVError(RuntimeError):
+    """A native entry point rejected its arguments or failed to launch."""
+
+
+@lru_cache(None)
+def lib():
+    path = Path(os.environ.get('SLIMKV_HIP_LIBRARY', LIBRARY))
+    if not path.exists():
+        raise ImportError(f'{path} is missing: build it with `python -m slimkv_amd.build` '
+                          '(slimkv_amd has no fallback compute path)')
+    handle = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if handle.slimkv_abi_version() != ABI_VERSION:
+        raise ImportError(f'{path} has ABI {handle.slimkv_abi_version()}, expected {ABI_VERSION}')
+    return handle
+
+
+def check(code):
+    if code != 0:
+        message = lib().slimkv_last_error().decode(errors='replace')
+        if code == -1:
+            raise ValueError(message)
+        raise SlimKVError(f'slimkv_hip error {code}: {message}')
+
+
+def stream_handle(device):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,69 @@
+// Shared device helpers for the gfx950 kernels: bf16 bit conversions, 16-byte
+// vector types, the bf16 MFMA tile, wavefront reductions and error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/slimkv_hip.h"
+
+namespace slimkv {
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
+    return __uint_as_float(bits << 16);
+}
+
+// Round-to-nearest-even to bf16; NaN maps to the canonical quiet NaN 0x7fc0,
+// as torch's float -> bfloat16 conversion does.
+__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float x) {
+    return bf16_to_f32(f32_to_bf16(x));
+}
+
+// Four bf16 held in two dwords, as the MFMA operand wants them.
+__device__ __forceinline__ v4s as_v4s(uint32_t lo, uint32_t hi) {
+    u32x2 t = {lo, hi};
+    return __builtin_bit_cast(v4s, t);
+}
+
+// D = A(16x16) * B(16x16) + C, bf16 inputs, fp32 accumulate.  Lane l holds
+// A[l%16][4*(l/16)+i], B[4*(l/16)+i][l%16], and D[4*(l/16)+i][l%16], i = 0..3.
+__device__ __forceinline__ v4f mfma16(v4s a, v4s b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+    return __builtin_amdgcn_exp2f(x);
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+__device__ __forceinline__ int64_t clamp_i64(int64_t x, int64_t lo, int64_t hi) {
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// Thread-local message behind slimkv_last_error().
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_hip(hipError_t err, const char* what);
+int device_cu_count();
+
+}  // namespace slimkv

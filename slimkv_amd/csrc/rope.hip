@@ -1,0 +1,246 @@
+// Elementwise decode/prefill RoPE (bf16-exact operation boundaries) and the
+// two-branch LSE merge.  Each thread handles 8 consecutive features of one row
+// with 128-bit loads/stores; the rotate-half partner is read from the same row.
+
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace slimkv {
+
+struct RopeRow {
+    const uint16_t* src;
+    uint16_t* dst;
+    int64_t pos;        // table row, or -1 to copy unchanged
+};
+
+// out = bf16(bf16(x*bf16(cos)) + bf16(rotate_half(x)*bf16(sin))) for 8 lanes of a row.
+__device__ __forceinline__ void rope8(const uint16_t* src, uint16_t* dst, int dd, int D,
+                                      const float* cos, const float* sin, int64_t pos) {
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(src + dd);
+    if (pos < 0) {
+        *reinterpret_cast<u32x4*>(dst + dd) = xv;
+        return;
+    }
+    const int half = D / 2;
+    const int pd = dd < half ? dd + half : dd - half;
+    const u32x4 pv = *reinterpret_cast<const u32x4*>(src + pd);
+    const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t ps[4] = {pv.x, pv.y, pv.z, pv.w};
+    const float* cr = cos + pos * D + dd;
+    const float* sr = sin + pos * D + dd;
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int hbit = 0; hbit < 2; ++hbit) {
+            const int idx = 2 * e + hbit;
+            const float x = bf16_to_f32(hbit ? (xs[e] >> 16) : (xs[e] & 0xffffu));
+            float pt = bf16_to_f32(hbit ? (ps[e] >> 16) : (ps[e] & 0xffffu));
+            if (dd < half) pt = -pt;
+            const float c = round_bf16(cr[idx]);
+            const float s = round_bf16(sr[idx]);
+            const float first = round_bf16(x * c);
+            const float second = round_bf16(pt * s);
+            pair |= f32_to_bf16(first + second) << (16 * hbit);
+        }
+        o[e] = pair;
+    }
+    *reinterpret_cast<u32x4*>(dst + dd) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
+struct RopeDecodeParams {
+    slimkv_rope_decode_args a;
+    int64_t q_rows, k_rows;     // rows of q and k (B*H*L)
+};
+
+__global__ void __launch_bounds__(256)
+rope_decode_kernel(RopeDecodeParams p) {
+    const slimkv_rope_decode_args& a = p.a;
+    const int per_row = (int)(a.dim / 8);
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t qitems = p.q_rows * per_row;
+    const int64_t kitems = p.k_rows * per_row;
+    if (gid >= qitems + kitems) return;
+    const int D = (int)a.dim;
+    if (gid < qitems) {
+        const int64_t row = gid / per_row;
+        const int dd = (int)(gid % per_row) * 8;
+        const int64_t s = row % a.queries;
+        const int64_t hh = (row / a.queries) % a.heads;
+        const int64_t b = row / (a.queries * a.heads);
+        const uint16_t* src = static_cast<const uint16_t*>(a.q) + b * a.q_sb + hh * a.q_sh + s * a.q_ss;
+        uint16_t* dst = static_cast<uint16_t*>(a.out_q) + row * D;
+        const int64_t pos = clamp_i64(a.q_positions[b * a.pos_sb + s], 0, a.rope_rows - 1);
+        rope8(src, dst, dd, D, a.cos, a.sin, pos);
+    } else {
+        const int64_t kg = gid - qitems;
+        const int64_t row = kg / per_row;
+        const int dd = (int)(kg % per_row) * 8;
+        const int64_t s = row % a.keys;
+        const int64_t hh = (row / a.keys) % a.kv_heads;
+        const int64_t b = row / (a.keys * a.kv_heads);
+        const uint16_t* src = static_cast<const uint16_t*>(a.k) + b * a.k_sb + hh * a.k_sh + s * a.k_ss;
+        uint16_t* dst = static_cast<uint16_t*>(a.out_k) + row * D;
+        int64_t pos;
+        if (s < a.sink) {
+            pos = s;
+        } else if (s == a.keys - 1) {
+            pos = a.q_positions[b * a.pos_sb];
+        } else {
+            const int64_t ri = clamp_i64(s - a.sink, 0, a.raw_index_count - 1);
+            pos = a.raw_indices[ri] + a.sink + a.history;
+        }
+        pos = clamp_i64(pos, 0, a.rope_rows - 1);
+        rope8(src, dst, dd, D, a.cos, a.sin, pos);
+    }
+}
+
+struct PrefillRopeParams {
+    slimkv_prefill_rope_args a;
+    int64_t q_rows, k_rows;
+};
+
+__global__ void __launch_bounds__(256)
+prefill_rope_kernel(PrefillRopeParams p) {
+    const slimkv_prefill_rope_args& a = p.a;
+    const int per_row = (int)(a.dim / 8);
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t qitems = p.q_rows * per_row;
+    const int64_t kitems = p.k_rows * per_row;
+    if (gid >= qitems + kitems) return;
+    const int D = (int)a.dim;
+    if (gid < qitems) {
+        const int64_t row = gid / per_row;
+        const int dd = (int)(gid % per_row) * 8;
+        const int64_t s = row % a.queries;
+        const int64_t hh = (row / a.queries) % a.heads;
+        const int64_t b = row / (a.queries * a.heads);
+        const uint16_t* src = static_cast<const uint16_t*>(a.q) + b * a.q_sb + hh * a.q_sh + s * a.q_ss;
+        uint16_t* dst = static_cast<uint16_t*>(a.out_q) + b * a.oq_sb + hh * a.oq_sh + s * a.oq_ss;
+        const int64_t pos = clamp_i64(a.positions[b * a.pos_sb + a.keys - a.queries + s], 0, a.rope_rows - 1);
+        rope8(src, dst, dd, D, a.cos, a.sin, pos);
+    } else {
+        const int64_t kg = gid - qitems;
+        const int64_t row = kg / per_row;
+        const int dd = (int)(kg % per_row) * 8;
+        const int64_t s = row % a.keys;
+        const int64_t hh = (row / a.keys) % a.kv_heads;
+        const int64_t b = row / (a.keys * a.kv_heads);
+        const uint16_t* src = static_cast<const uint16_t*>(a.k) + b * a.k_sb + hh * a.k_sh + s * a.k_ss;
+        uint16_t* dst = static_cast<uint16_t*>(a.out_k) + b * a.ok_sb + hh * a.ok_sh + s * a.ok_ss;
+        const int64_t prefix = a.keys - a.role_len;
+        bool beacon = s < prefix && s >= a.sink;
+        if (s >= prefix) {
+            const int64_t role = a.roles[s - prefix];
+            beacon = beacon || role == 1 || role == 2;
+        }
+        const int64_t pos = beacon ? -1 : clamp_i64(a.positions[b * a.pos_sb + s], 0, a.rope_rows - 1);
+        rope8(src, dst, dd, D, a.cos, a.sin, pos);
+    }
+}
+
+__global__ void __launch_bounds__(256)
+merge_kernel(slimkv_merge_args a) {
+    const int per_row = (int)(a.dim / 8);
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t rows = a.batch * a.heads * a.length;
+    if (gid >= rows * per_row) return;
+    const int64_t row = gid / per_row;
+    const int dd = (int)(gid % per_row) * 8;
+    const int64_t q = row % a.length;
+    const int64_t hh = (row / a.length) % a.heads;
+    const int64_t b = row / (a.length * a.heads);
+    const float r = a.raw_lse[b * a.rl_sb + hh * a.rl_sh + q * a.rl_sl];
+    const float l = a.latent_lse[b * a.ll_sb + hh * a.ll_sh + q * a.ll_sl];
+    const float m = fmaxf(r, l);
+    const float total = m + log1pf(expf(-fabsf(r - l)));
+    const float rw = expf(r - total);
+    const float lw = expf(l - total);
+    const u32x4 rv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.raw) + b * a.r_sb + hh * a.r_sh + q * a.r_sl + dd);
+    const u32x4 lv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.latent) + b * a.l_sb + hh * a.l_sh + q * a.l_sl + dd);
+    const uint32_t rs[4] = {rv.x, rv.y, rv.z, rv.w};
+    const uint32_t ls[4] = {lv.x, lv.y, lv.z, lv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float r0 = bf16_to_f32(rs[e] & 0xffffu), r1 = bf16_to_f32(rs[e] >> 16);
+        const float l0 = bf16_to_f32(ls[e] & 0xffffu), l1 = bf16_to_f32(ls[e] >> 16);
+        o[e] = f32_to_bf16(rw * r0 + lw * l0) | (f32_to_bf16(rw * r1 + lw * l1) << 16);
+    }
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + row * a.dim + dd) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
+namespace {
+bool al8(int64_t x) { return (x & 7) == 0; }
+bool pal16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+}  // namespace
+
+}  // namespace slimkv
+
+using namespace slimkv;
+
+extern "C" int slimkv_rope_decode(const slimkv_rope_decode_args* a, void* stream) {
+    if (!a || !a->q || !a->k || !a->out_q || !a->out_k || !a->cos || !a->sin || !a->q_positions)
+        return fail(SLIMKV_EINVAL, "null pointer");
+    if (a->dim <= 0 || a->dim % 16 || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->queries <= 0 ||
+        a->keys < 0 || a->rope_rows <= 0 || a->sink < 0 || a->history < 0)
+        return fail(SLIMKV_EINVAL, "invalid RoPE sizes (dim must be a multiple of 16)");
+    const int64_t strides[] = {a->q_sb, a->q_sh, a->q_ss, a->k_sb, a->k_sh, a->k_ss};
+    for (int64_t st : strides)
+        if (!al8(st)) return fail(SLIMKV_EINVAL, "strides must be multiples of 8 elements");
+    if (!pal16(a->q) || !pal16(a->k) || !pal16(a->out_q) || !pal16(a->out_k))
+        return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
+    const int64_t middle = a->keys > 0 ? std::max<int64_t>(0, a->keys - 1 - a->sink) : 0;
+    if (middle > 0 && (!a->raw_indices || a->raw_index_count < middle))
+        return fail(SLIMKV_EINVAL, "raw indices must cover every tail slot");
+    RopeDecodeParams p{};
+    p.a = *a;
+    if (p.a.raw_index_count <= 0) p.a.raw_index_count = 1;
+    p.q_rows = a->batch * a->heads * a->queries;
+    p.k_rows = a->batch * a->kv_heads * a->keys;
+    const int64_t items = (p.q_rows + p.k_rows) * (a->dim / 8);
+    if (items == 0) return SLIMKV_OK;
+    const int64_t blocks = (items + 255) / 256;
+    hipLaunchKernelGGL(rope_decode_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+    return check_hip(hipGetLastError(), "rope kernel launch");
+}
+
+extern "C" int slimkv_prefill_rope(const slimkv_prefill_rope_args* a, void* stream) {
+    if (!a || !a->q || !a->k || !a->out_q || !a->out_k || !a->cos || !a->sin || !a->positions || !a->roles)
+        return fail(SLIMKV_EINVAL, "null pointer");
+    if (a->dim <= 0 || a->dim % 16 || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->queries <= 0 ||
+        a->keys < a->queries || a->role_len < 0 || a->role_len > a->keys || a->rope_rows <= 0 || a->sink < 0)
+        return fail(SLIMKV_EINVAL, "invalid prefill RoPE sizes");
+    const int64_t strides[] = {a->q_sb, a->q_sh, a->q_ss, a->k_sb, a->k_sh, a->k_ss,
+                               a->oq_sb, a->oq_sh, a->oq_ss, a->ok_sb, a->ok_sh, a->ok_ss};
+    for (int64_t st : strides)
+        if (!al8(st)) return fail(SLIMKV_EINVAL, "strides must be multiples of 8 elements");
+    if (!pal16(a->q) || !pal16(a->k) || !pal16(a->out_q) || !pal16(a->out_k))
+        return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
+    PrefillRopeParams p{};
+    p.a = *a;
+    p.q_rows = a->batch * a->heads * a->queries;
+    p.k_rows = a->batch * a->kv_heads * a->keys;
+    const int64_t items = (p.q_rows + p.k_rows) * (a->dim / 8);
+    const int64_t blocks = (items + 255) / 256;
+    hipLaunchKernelGGL(prefill_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+    return check_hip(hipGetLastError(), "prefill rope kernel launch");
+}
+
+extern "C" int slimkv_merge(const slimkv_merge_args* a, void* stream) {
+    if (!a || !a->raw || !a->latent || !a->raw_lse || !a->latent_lse || !a->out)
+        return fail(SLIMKV_EINVAL, "null pointer");
+    if (a->batch <= 0 || a->heads <= 0 || a->length <= 0 || a->dim <= 0 || a->dim % 8)
+        return fail(SLIMKV_EINVAL, "invalid merge sizes (dim must be a multiple of 8)");
+    const int64_t strides[] = {a->r_sb, a->r_sh, a->r_sl, a->l_sb, a->l_sh, a->l_sl};
+    for (int64_t st : strides)
+        if (!al8(st)) return fail(SLIMKV_EINVAL, "strides must be multiples of 8 elements");
+    if (!pal16(a->raw) || !pal16(a->latent) || !pal16(a->out))
+        return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
+    const int64_t items = a->batch * a->heads * a->length * (a->dim / 8);
+    const int64_t blocks = (items + 255) / 256;
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), *a);
+    return check_hip(hipGetLastError(), "merge kernel launch");
+}

@@ -1,0 +1,197 @@
+"""Tensor-level calls into the HIP library (device memory and streams via torch).
+
+Each function validates its tensors, allocates outputs and the workspace from
+torch's caching allocator (so the calls are HIP-graph capturable), fills the C
+argument struct and enqueues on torch's current stream.  Nothing here computes
+on the CPU.
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+BF16 = torch.bfloat16
+
+
+def _ptr(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _need_device(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != 'cuda':
+            raise ValueError('slimkv_amd kernels need device tensors (no CPU path)')
+
+
+def _need_bf16(*tensors):
+    for t in tensors:
+        if t is not None and t.dtype != BF16:
+            raise ValueError(f'expected bfloat16, found {t.dtype}')
+
+
+def _last_contiguous(t):
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def attention_forward(q, k, v, scale, causal=False, splits=0, seqlens=None, out=None, lse=None):
+    """BSHD split-K attention.  q [B,Lq,Hq,Wk], k [B,N,Hk,Wk], v [B,N,Hk,Wv].
+
+    Returns (out [B,Lq,Hq,Wv] bf16, lse [B,Hq,Lq] fp32).
+    """
+    _need_device(q, k, v, seqlens)
+    _need_bf16(q, k, v)
+    q, k, v = (_last_contiguous(x) for x in (q, k, v))
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError('BSHD tensors required')
+    B, Lq, Hq, Wk = q.shape
+    _, N, Hk, _ = k.shape
+    Wv = v.shape[-1]
+    if k.shape[0] != B or k.shape[-1] != Wk or v.shape[:3] != k.shape[:3]:
+        raise ValueError('invalid K/V shapes')
+    if out is None:
+        out = torch.empty(B, Lq, Hq, Wv, dtype=BF16, device=q.device)
+    if lse is None:
+        lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device)
+    if seqlens is not None:
+        if seqlens.dtype != torch.int32 or not seqlens.is_contiguous() or seqlens.numel() != B:
+            raise ValueError('One int32 cache length per sequence required')
+    a = _lib.AttentionArgs(
+        _ptr(q), *q.stride()[:3], _ptr(k), *k.stride()[:3], _ptr(v), *v.stride()[:3],
+        _ptr(out), *out.stride()[:3], _ptr(lse), _ptr(seqlens),
+        B, Lq, Hq, Hk, N, Wk, Wv, float(scale), int(bool(causal)), int(splits))
+    nbytes = lib().slimkv_attention_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    ws = _workspace(nbytes, q.device)
+    check(lib().slimkv_attention_forward(ctypes.byref(a), _ptr(ws), nbytes, _lib.stream_handle(q.device)))
+    return out, lse
+
+
+def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias=None, up_v_bias=None,
+                  block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
+                  raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None,
+                  workspace=None):
+    """Fused latent beacon decode for one layer.
+
+    q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given),
+    raw_k/raw_v [B,Nr,Hkv,D] with RoPE'd K, lat_k [B,Nl,Rk], lat_v [B,Nl,Rv],
+    up_k [Hkv*D,Rk], up_v [Hkv*D,Rv].  Returns (out [B,Lq,Hq,D] bf16, lse [B,Hq,Lq]).
+    """
+    _need_device(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v)
+    _need_bf16(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, up_k_bias, up_v_bias)
+    B, Lq, Hq, D = q.shape
+    Nr, Hkv = raw_k.shape[1], raw_k.shape[2]
+    Rk, Rv = up_k.shape[1], up_v.shape[1]
+    Nl = 0 if lat_k is None else lat_k.shape[1]
+    q, raw_k, raw_v = (_last_contiguous(x) for x in (q, raw_k, raw_v))
+    if lat_k is not None:
+        lat_k, lat_v = _last_contiguous(lat_k), _last_contiguous(lat_v)
+        if lat_k.dim() == 4:
+            lat_k, lat_v = lat_k.squeeze(2), lat_v.squeeze(2)
+        if lat_k.shape[-1] != Rk or lat_v.shape[-1] != Rv:
+            raise ValueError('latent widths differ from the up-projection ranks')
+    up_k, up_v = up_k.contiguous(), up_v.contiguous()
+    if out is None:
+        out = torch.empty(B, Lq, Hq, D, dtype=BF16, device=q.device)
+    if lse is None:
+        lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device)
+    if cos is not None:
+        if cos.dtype != torch.float32 or sin.dtype != torch.float32 or q_positions is None:
+            raise ValueError('RoPE tables must be fp32 with int64 query positions')
+        cos, sin = cos.contiguous(), sin.contiguous()
+        q_positions = q_positions.to(torch.int64)
+        if q_positions.stride(-1) != 1:
+            q_positions = q_positions.contiguous()
+    a = _lib.LatentDecodeArgs(
+        _ptr(q), *q.stride()[:3],
+        _ptr(q_positions), 0 if q_positions is None else q_positions.stride(0),
+        _ptr(cos), _ptr(sin), 0 if cos is None else cos.shape[0],
+        _ptr(raw_k), *raw_k.stride()[:3], _ptr(raw_v), *raw_v.stride()[:3],
+        _ptr(raw_lengths), Nr,
+        _ptr(lat_k), *(lat_k.stride()[:2] if lat_k is not None else (0, 0)),
+        _ptr(lat_v), *(lat_v.stride()[:2] if lat_v is not None else (0, 0)),
+        _ptr(lat_lengths), Nl, int(bool(lat_causal)), int(bool(block_diagonal)),
+        _ptr(up_k), _ptr(up_k_bias), _ptr(up_v), _ptr(up_v_bias),
+        B, Lq, Hq, Hkv, D, Rk, Rv, float(scale),
+        _ptr(out), *out.stride()[:3], _ptr(lse), int(raw_splits), int(lat_splits))
+    nbytes = lib().slimkv_latent_decode_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = _workspace(nbytes, q.device)
+    check(lib().slimkv_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    return out, lse
+
+
+def latent_decode_workspace_bytes(**shape):
+    """Workspace size for a latent decode of the given sizes (no tensors needed)."""
+    a = _lib.LatentDecodeArgs()
+    for key, value in shape.items():
+        setattr(a, key, value)
+    return lib().slimkv_latent_decode_workspace(ctypes.byref(a))
+
+
+def rope_decode(q, k, cos, sin, query_positions, raw_indices, sink, history):
+    """q [B,Hq,Lq,D], k [B,Hk,Nk,D] (BHSD); returns new contiguous (oq, ok)."""
+    _need_device(q, k, cos, sin, query_positions)
+    _need_bf16(q, k)
+    q, k = _last_contiguous(q), _last_contiguous(k)
+    oq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    ok = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    pos = query_positions if query_positions.dtype == torch.int64 else query_positions.long()
+    if pos.stride(-1) != 1:
+        pos = pos.contiguous()
+    idx = None
+    if raw_indices is not None:
+        idx = raw_indices.to(device=q.device, dtype=torch.int64).contiguous()
+    a = _lib.RopeDecodeArgs(
+        _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(oq), _ptr(ok), _ptr(cos), _ptr(sin), cos.shape[0],
+        _ptr(pos), pos.stride(0), _ptr(idx), 0 if idx is None else idx.numel(),
+        q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3], int(sink), int(history))
+    check(lib().slimkv_rope_decode(ctypes.byref(a), _lib.stream_handle(q.device)))
+    return oq, ok
+
+
+def prefill_rope(q, k, cos, sin, positions, roles, sink):
+    """q [B,Hq,Lq,D], k [B,Hk,Nk,D]; outputs keep the input strides (empty_like)."""
+    _need_device(q, k, cos, sin, positions, roles)
+    _need_bf16(q, k)
+    oq, ok = torch.empty_like(q), torch.empty_like(k)
+    pos = positions if positions.stride(-1) == 1 else positions.contiguous()
+    roles = roles.to(device=q.device, dtype=torch.int64).contiguous()
+    a = _lib.PrefillRopeArgs(
+        _ptr(q), *q.stride()[:3], _ptr(k), *k.stride()[:3],
+        _ptr(oq), *oq.stride()[:3], _ptr(ok), *ok.stride()[:3],
+        _ptr(cos), _ptr(sin), cos.shape[0], _ptr(pos), pos.stride(0),
+        _ptr(roles), roles.numel(),
+        q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3], int(sink))
+    check(lib().slimkv_prefill_rope(ctypes.byref(a), _lib.stream_handle(q.device)))
+    return oq, ok
+
+
+def merge(raw, raw_lse, latent, latent_lse):
+    """raw/latent [B,H,L,D] bf16, LSEs [B,H,L] fp32 -> contiguous [B,H,L,D] bf16."""
+    _need_device(raw, latent, raw_lse, latent_lse)
+    _need_bf16(raw, latent)
+    raw, latent = _last_contiguous(raw), _last_contiguous(latent)
+    raw_lse, latent_lse = raw_lse.float(), latent_lse.float()
+    out = torch.empty(raw.shape, dtype=raw.dtype, device=raw.device)
+    a = _lib.MergeArgs(
+        _ptr(raw), *raw.stride()[:3], _ptr(latent), *latent.stride()[:3],
+        _ptr(raw_lse), *raw_lse.stride(), _ptr(latent_lse), *latent_lse.stride(),
+        _ptr(out), *raw.shape)
+    check(lib().slimkv_merge(ctypes.byref(a), _lib.stream_handle(raw.device)))
+    return out
+
+
+def default_scale(head_dim):
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,144 @@
+"""Fused latent beacon decode (one layer) against the oracle's restatement of
+the reference bf16 decode path, slimkv/llama3/fa2_decode.py:143-164.
+
+Inputs are the seeded synthetic Llama-3.1-8B decode layer: sinks and a raw
+tail with RoPE'd full-dim K, beacon latents without RoPE, per-KV-head
+orthonormal bases assembled into block-diagonal global weights.  Bar: max abs
+2e-2, mean abs 2e-3 on the bf16 output; decode RoPE of q and raw K bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import rope as orope
+from slimkv_amd.workloads import decode_rope_layout, latent_case, rope_tables
+from tests.helpers import assert_close, assert_lse_close, bits, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _rotated(case):
+    """Rotate q and raw K with the HIP decode RoPE (BHSD views) and check the
+    bits against the oracle rotation."""
+    from slimkv_amd import kernels
+    raw_idx, history = decode_rope_layout(case)
+    q_bhsd = case.q.transpose(1, 2)
+    k_bhsd = case.raw_k.transpose(1, 2)
+    oq, ok = kernels.rope_decode(q_bhsd, k_bhsd, case.cos, case.sin, case.q_positions, raw_idx,
+                                 case.sinks, history)
+    torch.cuda.synchronize()
+    eq, ek = orope.rope_decode(to_np(q_bhsd).astype(np.float32), to_np(k_bhsd).astype(np.float32),
+                               to_np(case.cos).astype(np.float32), to_np(case.sin).astype(np.float32),
+                               case.q_positions.cpu().numpy(), raw_idx.cpu().numpy(), case.sinks, history)
+    from oracle.bf16 import to_bits
+    assert (bits(oq) == to_bits(eq)).all(), 'decode RoPE of q is not bit-exact'
+    assert (bits(ok) == to_bits(ek)).all(), 'decode RoPE of raw K is not bit-exact'
+    return oq, ok      # BHSD contiguous
+
+
+def _oracle(case, q_rot_bhsd, k_rot_bhsd, lat_causal=False, up_k_bias=None, up_v_bias=None,
+            lat_k=None, lat_v=None):
+    lat_k = case.lat_k if lat_k is None else lat_k
+    lat_v = case.lat_v if lat_v is None else lat_v
+    return oa.latent_layer(
+        to_np(q_rot_bhsd), to_np(k_rot_bhsd), to_np(case.raw_v.transpose(1, 2)),
+        to_np(lat_k)[:, None], to_np(lat_v)[:, None], to_np(case.up_k), to_np(case.up_v),
+        case.scale, case.kv_heads, None if up_k_bias is None else to_np(up_k_bias),
+        None if up_v_bias is None else to_np(up_v_bias), lat_causal)
+
+
+def _run(case, k_rot_bhsd, block_diagonal=True, rope_in_kernel=True, q_rot=None, **kw):
+    from slimkv_amd import kernels
+    raw_k = k_rot_bhsd.transpose(1, 2)
+    if rope_in_kernel:
+        q, extra = case.q, dict(q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    else:
+        q, extra = q_rot, {}
+    out, lse = kernels.latent_decode(q, raw_k, case.raw_v, kw.pop('lat_k', case.lat_k),
+                                     kw.pop('lat_v', case.lat_v), case.up_k, case.up_v, case.scale,
+                                     block_diagonal=block_diagonal, **extra, **kw)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+@pytest.mark.parametrize('block_diagonal', [True, False])
+def test_config0_shape(device, block_diagonal):
+    """B1, 32/8 heads, d 128, context 4096, t4, 4 sinks + 124 tail, r 32."""
+    case = latent_case(batch=1, context=4096, tail=124, seed=0, device=device)
+    q_rot, k_rot = _rotated(case)
+    out, lse = _run(case, k_rot, block_diagonal)
+    eo, el = _oracle(case, q_rot, k_rot)
+    assert_close(to_np(out.transpose(1, 2)), eo, what='out')
+    assert_lse_close(to_np(lse), el, what='lse')
+
+
+@pytest.mark.parametrize('rk,rv', [(16, 16), (32, 32), (48, 48), (16, 48), (48, 32)])
+def test_layer_adaptive_ranks(device, rk, rv):
+    case = latent_case(batch=3, context=2048, tail=128, rank_k=rk, rank_v=rv, seed=rk * 100 + rv,
+                       device=device)
+    q_rot, k_rot = _rotated(case)
+    eo, el = _oracle(case, q_rot, k_rot)
+    for bd in (True, False):
+        out, lse = _run(case, k_rot, bd)
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd}')
+        assert_lse_close(to_np(lse), el, what=f'lse bd={bd}')
+
+
+def test_prerotated_query_and_biases(device):
+    """q given already rotated; U_K / U_V biases fold into the LSE and output
+    (fa2_decode.py:157-163)."""
+    case = latent_case(batch=2, context=1500, tail=100, seed=11, device=device)
+    q_rot, k_rot = _rotated(case)
+    gen = torch.Generator(device=device).manual_seed(4)
+    bk = (0.5 * torch.randn(case.up_k.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+    bv = (0.5 * torch.randn(case.up_v.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+    eo, el = _oracle(case, q_rot, k_rot, up_k_bias=bk, up_v_bias=bv)
+    for bd in (True, False):
+        out, lse = _run(case, k_rot, bd, rope_in_kernel=False, q_rot=q_rot.transpose(1, 2),
+                        up_k_bias=bk, up_v_bias=bv)
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd}')
+        assert_lse_close(to_np(lse), el, what=f'lse bd={bd}')
+
+
+def test_insertion_step_two_queries(device):
+    """Raw token + its new beacon (Q2): the raw query sees N-1 latents, the
+    beacon query sees N (fa2_decode.py:153-154; paired_decode.py:30-43)."""
+    case = latent_case(batch=2, context=1000, tail=60, seed=21, device=device)
+    gen = torch.Generator(device=device).manual_seed(22)
+    q2 = torch.randn(2, 2, 32, 128, generator=gen, device=device).to(torch.bfloat16)
+    case.q = q2
+    case.q_positions = torch.tensor([[1000, 1001]] * 2, device=device)
+    case.cos, case.sin = rope_tables(1002, 128, 500000.0, device)
+    q_rot, k_rot = _rotated(case)
+    eo, el = _oracle(case, q_rot, k_rot, lat_causal=True)
+    for bd in (True, False):
+        out, lse = _run(case, k_rot, bd, lat_causal=True)
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd}')
+        assert_lse_close(to_np(lse), el, what=f'lse bd={bd}')
+
+
+def test_empty_latent_branch(device):
+    """No history yet: the output is the raw branch alone (fa2_decode.py:149-150)."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=2, context=200, tail=120, seed=3, device=device)
+    q_rot, k_rot = _rotated(case)
+    out, lse = kernels.latent_decode(case.q, k_rot.transpose(1, 2), case.raw_v, None, None, case.up_k,
+                                     case.up_v, case.scale, block_diagonal=True,
+                                     q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    torch.cuda.synchronize()
+    eo, el = oa.eager_forward(to_np(q_rot.transpose(1, 2)), to_np(k_rot.transpose(1, 2)),
+                              to_np(case.raw_v), case.scale)
+    assert_close(to_np(out), eo)
+    assert_lse_close(to_np(lse), el)
+
+
+def test_batch16_config1_shape_reduced_context(device):
+    """The batch-16 t4f4 geometry (32/8 heads, 4 sinks, 128 tail, r 32) at an
+    8K context so the oracle finishes in seconds."""
+    case = latent_case(batch=16, context=8192 + 132, tail=128, seed=7, device=device)
+    q_rot, k_rot = _rotated(case)
+    out, lse = _run(case, k_rot, True)
+    eo, el = _oracle(case, q_rot, k_rot)
+    assert_close(to_np(out.transpose(1, 2)), eo)
+    assert_lse_close(to_np(lse), el)

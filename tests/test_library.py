@@ -1,0 +1,51 @@
+"""The C-ABI library builds, loads and exports every entry point the header
+declares (no GPU needed: nothing here launches a kernel)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    names = set()
+    for header in (ROOT / 'include').glob('*.h'):
+        text = re.sub(r'/\*.*?\*/', '', header.read_text(), flags=re.S)
+        names.update(re.findall(r'\b(slimkv_[a-z0-9_]+)\s*\(', text))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert 'slimkv_latent_decode' in names and 'slimkv_attention_forward' in names
+
+
+def test_library_exports_every_declared_symbol():
+    from slimkv_amd import _lib
+    handle = _lib.lib()
+    for name in declared_symbols():
+        assert hasattr(handle, name), name
+        assert name in _lib.SIGNATURES, f'{name} has no ctypes signature'
+
+
+def test_struct_layouts_match_header_field_order():
+    """ctypes mirrors list the header's fields in order with matching widths."""
+    from slimkv_amd import _lib
+    header = (ROOT / 'include' / 'slimkv_hip.h').read_text()
+    for struct in (_lib.AttentionArgs, _lib.LatentDecodeArgs, _lib.RopeDecodeArgs,
+                   _lib.PrefillRopeArgs, _lib.MergeArgs):
+        body = re.search(r'typedef struct %s \{(.*?)\}' % struct.__name__, header, re.S).group(1)
+        body = re.sub(r'/\*.*?\*/', '', body)
+        fields = re.findall(r'\*?\s*([a-z_][a-z0-9_]*)\s*(?=[,;])', body)
+        assert fields == [f[0] for f in struct._fields_], struct.__name__
+
+
+def test_errors_are_reported_without_a_gpu():
+    from slimkv_amd import _lib
+    a = _lib.AttentionArgs()
+    assert _lib.lib().slimkv_attention_workspace(ctypes.byref(a)) == 0
+    assert b'null' in _lib.lib().slimkv_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(-1)
