@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Latent beacon decode attention benchmark on one MI355X.
+
+Workload: Llama-3.1-8B attention layer shape, t4f4 -- batch 16, 32 query / 8 KV
+heads, head_dim 128, context 32768 per sequence: 8192 beacon latent rows per
+sequence, 4 sinks + a 128-token raw tail + the current token with full-dim
+RoPE'd K/V.  One step is a sweep over 32 layers, each with its own buffers
+(~4.6 GB, far beyond the 256 MB MALL) and a latent rank drawn per layer by seed
+from {16, 32, 48} (K and V rank equal).  Each layer runs the fused decode:
+query RoPE + absorption, split-K attention over raw and latent rows, combine +
+V lift.  The 32-layer sweep is captured once in a HIP graph and replayed.
+
+value  = algorithmic bytes of the sweep / sweep time (GB/s), inputs resident in HBM.
+roofline = the split-K attention kernel alone: its algorithmic bytes per launch
+           / its average duration measured with HIP events on the launch stream.
+cpu_baseline = the reference eager fp32 path restated in torch, one full-shape
+           rank-32 layer repeated for ~10-30 s on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = 'decode attn GB/s and % HBM peak, Llama-3.1-8B t4f4 b16 ctx32K; decode tokens/s'
+HBM_PEAK_GBPS = 8000.0
+
+B, HQ, HKV, D = 16, 32, 8, 128
+CONTEXT, RATIO, SINKS, TAIL = 32768, 4, 4, 128
+BEACONS = CONTEXT // RATIO          # 8192 latent rows
+RAW = SINKS + TAIL + 1              # sinks + tail + current token
+RANKS = (16, 32, 48)
+
+
+def layer_bytes(rk, rv):
+    """Algorithmic bytes of one layer step: latent rows, raw rows, q in, out,
+    and the two up-projection weights once."""
+    rows = B * (BEACONS * HKV * (rk + rv) * 2 + RAW * HKV * D * 2 * 2)
+    return rows + B * 2 * HQ * D * 2 + HKV * D * (rk + rv) * 2
+
+
+def split_kernel_bytes(rk, rv):
+    """Bytes the split-K kernel must read: latent rows, raw rows and q once."""
+    return B * (BEACONS * HKV * (rk + rv) * 2 + RAW * HKV * D * 2 * 2 + HQ * D * 2)
+
+
+def draw_ranks(layers, seed):
+    import random
+    rng = random.Random(seed)
+    return [rng.choice(RANKS) for _ in range(layers)]
+
+
+def make_layer(torch, device, rank, seed, cos, sin):
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cpu_gen = torch.Generator().manual_seed(seed + 1)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+
+    lat_k = randn(B, BEACONS, HKV * rank)
+    lat_v = randn(B, BEACONS, HKV * rank)
+    raw_k = randn(B, RAW, HKV, D)
+    raw_v = randn(B, RAW, HKV, D)
+    q = randn(B, 1, HQ, D)
+    up_k = block_diagonal([orthonormal_columns(D, rank, cpu_gen) for _ in range(HKV)]).to(device, torch.bfloat16)
+    up_v = block_diagonal([orthonormal_columns(D, rank, cpu_gen) for _ in range(HKV)]).to(device, torch.bfloat16)
+    q_pos = torch.full((B, 1), CONTEXT, dtype=torch.int64, device=device)
+    # Raw K is kept rotated in the cache (rotated once when appended): sinks at
+    # 0..3, tail at CONTEXT-TAIL.., current token at CONTEXT.
+    raw_idx = torch.arange(TAIL, device=device)
+    history = CONTEXT - TAIL - SINKS
+    _, k_rot = kernels.rope_decode(q.transpose(1, 2), raw_k.transpose(1, 2), cos, sin, q_pos, raw_idx,
+                                   SINKS, history)
+    raw_k = k_rot.transpose(1, 2).contiguous()
+    return dict(rank=rank, q=q, q_pos=q_pos, raw_k=raw_k, raw_v=raw_v, lat_k=lat_k, lat_v=lat_v,
+                up_k=up_k, up_v=up_v,
+                out=torch.empty(B, 1, HQ, D, dtype=torch.bfloat16, device=device),
+                lse=torch.empty(B, HQ, 1, dtype=torch.float32, device=device))
+
+
+def run_layer(kernels, L, cos, sin, scale, workspace):
+    kernels.latent_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'], scale,
+                          block_diagonal=True, q_positions=L['q_pos'], cos=cos, sin=sin,
+                          out=L['out'], lse=L['lse'], workspace=workspace)
+
+
+def cpu_baseline(torch, layer, cos, sin, scale, budget_s=(10.0, 30.0)):
+    """Time the torch fp32 eager restatement of the reference path on the host."""
+    from oracle import eager_torch
+    threads = int(os.environ.get('OMP_NUM_THREADS', '0')) or len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    from slimkv_amd import kernels
+    q_rot, _ = kernels.rope_decode(layer['q'].transpose(1, 2), layer['raw_k'].transpose(1, 2)[:, :, :1].contiguous(),
+                                   cos, sin, layer['q_pos'], None, 0, 0)
+    cpu = {k: layer[k].float().cpu() for k in ('raw_k', 'raw_v', 'lat_k', 'lat_v', 'up_k', 'up_v')}
+    q_cpu = q_rot.float().cpu()
+    lat_k, lat_v = cpu['lat_k'][:, :, None], cpu['lat_v'][:, :, None]
+
+    def once():
+        return eager_torch.latent_layer(q_cpu, cpu['raw_k'], cpu['raw_v'], lat_k, lat_v, cpu['up_k'], cpu['up_v'],
+                                        scale, HKV)
+
+    once()
+    times = []
+    start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+        elapsed = time.perf_counter() - start
+        if (elapsed >= budget_s[0] and len(times) >= 5) or elapsed >= budget_s[1]:
+            break
+    times.sort()
+    median = times[len(times) // 2]
+    rk = layer['rank']
+    return {'value': round(layer_bytes(rk, rk) / median / 1e9, 3), 'unit': 'GB/s', 'cores': threads,
+            'kind': 'port', 'ms_per_layer': round(median * 1e3, 2),
+            'sample': f'one full-shape rank-{rk} layer (B16, 8192 beacons, 133 raw), torch fp32 eager '
+                      f'restatement, {len(times)} runs in {elapsed:.1f}s, median'}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--layers', type=int, default=32)
+    ap.add_argument('--seed', type=int, default=0)
+    ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    ap.add_argument('--no-graph', action='store_true', help='time eager launches instead of graph replay')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
+        print('bench.py measures one GPU: the decode path shards by sequence with no exchange, '
+              'so multi-GPU runs are not part of this build (use --gpus 1).', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from slimkv_amd import _lib, kernels
+    from slimkv_amd.workloads import rope_tables
+
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    scale = 1.0 / D ** 0.5
+    cos, sin = rope_tables(CONTEXT + 1, D, 500000.0, device)
+    ranks = draw_ranks(args.layers, args.seed)
+    print(f'bench: building {args.layers} layers, ranks {ranks}', file=sys.stderr, flush=True)
+    layers = [make_layer(torch, device, r, args.seed * 1000 + i, cos, sin) for i, r in enumerate(ranks)]
+    ws_bytes = max(kernels.latent_decode_workspace_bytes(
+        L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'], block_diagonal=True,
+        q_positions=L['q_pos'], cos=cos, sin=sin) for L in layers)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    torch.cuda.synchronize()
+
+    def sweep():
+        for L in layers:
+            run_layer(kernels, L, cos, sin, scale, workspace)
+
+    sweep()
+    torch.cuda.synchronize()
+    if args.no_graph:
+        step = sweep
+    else:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            sweep()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            sweep()
+        step = graph.replay
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+    sweep_bytes = sum(layer_bytes(r, r) for r in ranks)
+    gbps = sweep_bytes / (elapsed / args.steps) / 1e9
+    print(f'bench: sweep {ms_per_step:.3f} ms, {gbps:.1f} GB/s', file=sys.stderr, flush=True)
+
+    # Split-K kernel alone: HIP events recorded by the library around each launch.
+    lib = _lib.lib()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in layers]
+    for a, b in events:
+        a.record()
+        b.record()
+    torch.cuda.synchronize()
+    durations = {r: [] for r in set(ranks)}
+    for _ in range(max(3, min(args.steps, 10))):
+        for L, (a, b) in zip(layers, events):
+            _lib.check(lib.slimkv_set_profile_events(a.cuda_event, b.cuda_event))
+            run_layer(kernels, L, cos, sin, scale, workspace)
+        _lib.check(lib.slimkv_set_profile_events(None, None))
+        torch.cuda.synchronize()
+        for L, (a, b) in zip(layers, events):
+            durations[L['rank']].append(a.elapsed_time(b) * 1e-3)
+    dom = 32 if 32 in durations else max(durations, key=lambda r: len(durations[r]))
+    dur = sorted(durations[dom])
+    dur_avg = sum(dur) / len(dur)
+    achieved = split_kernel_bytes(dom, dom) / dur_avg / 1e9
+    all_split = sum(sum(v) / len(v) * ranks.count(r) for r, v in durations.items())
+    roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+                'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
+                'kernel': f'split_kernel<8,{8 if dom == 32 else (4 if dom == 16 else 12)}> (rank {dom} layers)',
+                'avg_us': round(dur_avg * 1e6, 2),
+                'split_kernel_sweep_frac': round(all_split / (elapsed / args.steps), 3)}
+
+    result = {
+        'metric': METRIC, 'value': round(gbps, 1), 'unit': 'GB/s', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': round(ms_per_step, 4), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
+        'config': {'workload': 'latent beacon decode, 32-layer sweep, Llama-3.1-8B layer shape t4f4',
+                   'batch': B, 'context': CONTEXT, 'beacons': BEACONS, 'raw_tokens': RAW,
+                   'q_heads': HQ, 'kv_heads': HKV, 'head_dim': D, 'layer_ranks': ranks,
+                   'graph': not args.no_graph},
+        'hbm_frac': round(gbps / HBM_PEAK_GBPS, 4),
+        'tokens_per_s': round(B / (elapsed / args.steps), 1),
+        'us_per_layer': round(ms_per_step * 1e3 / len(layers), 2),
+        'roofline': roofline,
+    }
+    if not args.no_cpu:
+        rank32 = next((L for L in layers if L['rank'] == 32), layers[0])
+        print('bench: CPU baseline leg', file=sys.stderr, flush=True)
+        result['cpu_baseline'] = cpu_baseline(torch, rank32, cos, sin, scale)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -32,6 +32,14 @@ const char* slimkv_last_error(void);
 /* ABI version of this header (bumped on any struct change). */
 int slimkv_abi_version(void);
 
+/* Measurement hook (no counterpart in the reference, whose benchmark attributes
+ * kernels with torch.profiler scopes, tools/benchmark/benchmark_context_decode.py:186-289).
+ * While set on the calling thread, every entry point records `before` (a
+ * hipEvent_t) on its stream immediately before its split-K attention kernel and
+ * `after` immediately after it, so a caller can time that kernel alone with
+ * HIP events.  Pass NULL, NULL to clear. */
+int slimkv_set_profile_events(void* before, void* after);
+
 /* ------------------------------------------------------------------------
  * Split-K decode attention with GQA, bottom-right causality and LSE.
  *

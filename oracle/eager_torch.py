@@ -1,0 +1,53 @@
+"""The reference's eager latent decode path restated in torch fp32 on the CPU.
+
+Used only as the CPU baseline leg of bench.py (timed on the host cores) and as a
+second, independent restatement checked against the numpy oracle in tests.
+Follows slimkv/llama3/latent_decode.py:16-41 (eager_forward),
+slimkv/llama3/fa2_decode.py:41-54 (project_query / project_value),
+:57-66 (merge) and :145-164 (the branch structure of decode), in fp32 as the
+reference eager path computes (latent_decode.py:26-28).
+"""
+import math
+
+import torch
+
+
+def eager_forward(q, k, v, scale, causal=False):
+    batch, queries, heads, rank = q.shape
+    keys, kv_heads = k.shape[1:3]
+    groups = heads // kv_heads
+    grouped_q = q.transpose(1, 2).reshape(batch, kv_heads, groups * queries, rank)
+    scores = (grouped_q.float() @ k.transpose(1, 2).transpose(-1, -2).float()) * scale
+    scores = scores.reshape(batch, heads, queries, keys)
+    if causal:
+        qpos = torch.arange(queries) + keys - queries
+        scores = scores.masked_fill(torch.arange(keys)[None, :] > qpos[:, None], -math.inf)
+    lse = torch.logsumexp(scores, dim=-1)
+    probs = torch.softmax(scores, dim=-1)
+    probs = torch.where(torch.isfinite(lse)[..., None], probs, 0.0)
+    out = probs.reshape(batch, kv_heads, groups * queries, keys) @ v.transpose(1, 2).float()
+    return out.reshape(batch, heads, queries, v.shape[-1]).transpose(1, 2), lse
+
+
+def project_query(q, weight, kv_heads):
+    batch, heads, length, dim = q.shape
+    grouped = q.reshape(batch, kv_heads, heads // kv_heads * length, dim)
+    return (grouped @ weight.reshape(kv_heads, dim, weight.shape[-1])).reshape(batch, heads, length, -1)
+
+
+def project_value(out, weight, kv_heads):
+    batch, heads, length, rank = out.shape
+    dim = weight.shape[0] // kv_heads
+    grouped = out.reshape(batch, kv_heads, heads // kv_heads * length, rank)
+    return (grouped @ weight.reshape(kv_heads, dim, rank).transpose(-1, -2)).reshape(batch, heads, length, dim)
+
+
+def latent_layer(q_rot, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, kv_heads):
+    """q_rot [B,H,1,D]; raw_k/raw_v [B,Nr,Hkv,D]; lat_k/lat_v [B,Nl,1,R]; fp32."""
+    raw_out, raw_lse = eager_forward(q_rot.transpose(1, 2), raw_k, raw_v, scale)
+    latent_q = project_query(q_rot, up_k, kv_heads)
+    lat_out, lat_lse = eager_forward(latent_q.transpose(1, 2), lat_k, lat_v, scale)
+    lat_out = project_value(lat_out.transpose(1, 2), up_v, kv_heads)
+    total = torch.logaddexp(raw_lse, lat_lse)
+    return (torch.exp(raw_lse - total)[..., None] * raw_out.transpose(1, 2)
+            + torch.exp(lat_lse - total)[..., None] * lat_out)

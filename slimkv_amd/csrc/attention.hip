@@ -545,6 +545,20 @@ prologue_kernel(PrologueParams pp) {
 namespace {
 
 thread_local std::string g_error;
+thread_local hipEvent_t g_before = nullptr;
+thread_local hipEvent_t g_after = nullptr;
+
+// Launch the split kernel bracketed by the caller's profiling events, if set.
+hipError_t dispatch_split(int ka, int kb, const struct SplitParams& prm, int grid, hipStream_t st);
+hipError_t timed_split(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st) {
+    if (g_before) {
+        hipError_t e = hipEventRecord(g_before, st);
+        if (e != hipSuccess) return e;
+    }
+    hipError_t e = dispatch_split(ka, kb, prm, grid, st);
+    if (e == hipSuccess && g_after) e = hipEventRecord(g_after, st);
+    return e;
+}
 
 int round_even_tile(int width) {
     // MFMA k-steps of 16 needed for `width`, rounded to the instantiated set.
@@ -685,6 +699,13 @@ extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
 extern "C" int slimkv_abi_version(void) { return 1; }
 
+extern "C" int slimkv_set_profile_events(void* before, void* after) {
+    if ((before == nullptr) != (after == nullptr)) return fail(SLIMKV_EINVAL, "set both events or neither");
+    g_before = static_cast<hipEvent_t>(before);
+    g_after = static_cast<hipEvent_t>(after);
+    return SLIMKV_OK;
+}
+
 extern "C" size_t slimkv_attention_workspace(const slimkv_attention_args* a) {
     AttnPlan plan{};
     if (plan_attention(a, &plan) != SLIMKV_OK) return 0;
@@ -724,7 +745,7 @@ extern "C" int slimkv_attention_forward(const slimkv_attention_args* a, void* wo
     sg.wown = (int)a->width_v;
     sg.nwg = plan.sp.nwg;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    rc = check_hip(dispatch_split(plan.sp.ks, 0, prm, sg.nwg, st), "split kernel launch");
+    rc = check_hip(timed_split(plan.sp.ks, 0, prm, sg.nwg, st), "split kernel launch");
     if (rc != SLIMKV_OK) return rc;
     CombineParams cp{};
     cp.a_ml = sg.part_ml; cp.a_acc = sg.part_acc; cp.a_splits = sg.splits; cp.a_w = sg.wown;
@@ -899,7 +920,7 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
         kb = p.lat.ks;
     }
     const int grid = r.nwg + (has_lat ? prm.seg[1].nwg : 0);
-    rc = check_hip(dispatch_split(8, kb, prm, grid, st), "split kernel launch");
+    rc = check_hip(timed_split(8, kb, prm, grid, st), "split kernel launch");
     if (rc != SLIMKV_OK) return rc;
 
     CombineParams cp{};

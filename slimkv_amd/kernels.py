@@ -74,16 +74,8 @@ def attention_forward(q, k, v, scale, causal=False, splits=0, seqlens=None, out=
     return out, lse
 
 
-def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias=None, up_v_bias=None,
-                  block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
-                  raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None,
-                  workspace=None):
-    """Fused latent beacon decode for one layer.
-
-    q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given),
-    raw_k/raw_v [B,Nr,Hkv,D] with RoPE'd K, lat_k [B,Nl,Rk], lat_v [B,Nl,Rv],
-    up_k [Hkv*D,Rk], up_v [Hkv*D,Rv].  Returns (out [B,Lq,Hq,D] bf16, lse [B,Hq,Lq]).
-    """
+def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias, block_diagonal,
+                 lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse):
     _need_device(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v)
     _need_bf16(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, up_k_bias, up_v_bias)
     B, Lq, Hq, D = q.shape
@@ -121,21 +113,50 @@ def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias
         _ptr(up_k), _ptr(up_k_bias), _ptr(up_v), _ptr(up_v_bias),
         B, Lq, Hq, Hkv, D, Rk, Rv, float(scale),
         _ptr(out), *out.stride()[:3], _ptr(lse), int(raw_splits), int(lat_splits))
+    keep = (q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, cos, sin, q_positions)
+    return a, out, lse, keep
+
+
+def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias=None, up_v_bias=None,
+                  block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
+                  raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None,
+                  workspace=None):
+    """Fused latent beacon decode for one layer.
+
+    q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given),
+    raw_k/raw_v [B,Nr,Hkv,D] with RoPE'd K, lat_k [B,Nl,Rk], lat_v [B,Nl,Rv],
+    up_k [Hkv*D,Rk], up_v [Hkv*D,Rv].  Returns (out [B,Lq,Hq,D] bf16, lse [B,Hq,Lq]).
+    A caller-provided `workspace` (uint8, at least latent_decode_workspace_bytes)
+    makes the call allocation-free, e.g. under HIP graph capture.
+    """
+    a, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
+                                     block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
+                                     lat_lengths, raw_splits, lat_splits, out, lse)
     nbytes = lib().slimkv_latent_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
     if workspace is None or workspace.numel() < nbytes:
         workspace = _workspace(nbytes, q.device)
     check(lib().slimkv_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    del keep
     return out, lse
 
 
-def latent_decode_workspace_bytes(**shape):
-    """Workspace size for a latent decode of the given sizes (no tensors needed)."""
-    a = _lib.LatentDecodeArgs()
-    for key, value in shape.items():
-        setattr(a, key, value)
-    return lib().slimkv_latent_decode_workspace(ctypes.byref(a))
+def latent_decode_workspace_bytes(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale=1.0, **kw):
+    """Workspace bytes latent_decode needs for these tensors (same keywords)."""
+    names = ('up_k_bias', 'up_v_bias', 'block_diagonal', 'lat_causal', 'q_positions', 'cos', 'sin',
+             'raw_lengths', 'lat_lengths', 'raw_splits', 'lat_splits', 'out', 'lse')
+    defaults = dict(up_k_bias=None, up_v_bias=None, block_diagonal=False, lat_causal=False, q_positions=None,
+                    cos=None, sin=None, raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0,
+                    out=None, lse=None)
+    defaults.update({k: v for k, v in kw.items() if k in names})
+    a, _, _, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale,
+                                 *(defaults[n] for n in names))
+    nbytes = lib().slimkv_latent_decode_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    del keep
+    return nbytes
 
 
 def rope_decode(q, k, cos, sin, query_positions, raw_indices, sink, history):
