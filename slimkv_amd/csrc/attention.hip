@@ -46,7 +46,7 @@ struct Seg {
     int g;                                           // query heads per KV head
     int wk, wv;                                      // K / V row widths
     int causal;
-    int tiles, splits, rows_per_split;
+    int tiles, cols, splits, rows_per_split;            // cols: packed query rows per tile (<= 16)
     int blk_heads, blk_k, blk_v;                     // block-diagonal layout (0 = full rows)
     int q_compact;                                   // q operand holds only the own block slice
     float* part_ml;                                  // [B][Hq*Lq][splits][2]
@@ -68,12 +68,68 @@ constexpr int kThreads = kWaves * 64;
 template <int KS>
 struct SplitLds {
     static constexpr int RS = 16 * KS + 8;                       // padded V row (bf16)
-    static constexpr int vbytes = kWaves * 2 * 16 * RS * 2;      // double-buffered V tiles
-    static constexpr int mbytes = kWaves * 16 * 16 * KS * 4;     // per-wave accumulators
-    static constexpr int bytes = (vbytes > mbytes ? vbytes : mbytes) + kWaves * 16 * 2 * 4;
+    static constexpr int bytes = kWaves * 2 * 16 * RS * 2;      // per-wave double-buffered V tiles
 };
 
+// Order LDS accesses of one wavefront: a wave's LDS instructions execute in
+// issue order, so only compiler reordering has to be prevented.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One 16-key tile held in registers: the K tile already in MFMA A-operand
+// order, the V tile as coalesced 16-byte pieces on their way to LDS.
 template <int KS>
+struct TileRegs {
+    u32x4 k[KS / 2];
+    u32x4 v[KS / 2];
+};
+
+// Loads are branch-free: an invalid piece reads a clamped in-bounds address and
+// is zeroed by a select, so the compiler can count outstanding loads across
+// the software pipeline instead of draining them (vmcnt(0)) at every join.
+__device__ __forceinline__ u32x4 zero_unless(bool ok, u32x4 v) {
+    return u32x4{ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
+}
+
+template <int KS>
+__device__ __forceinline__ void load_tile(TileRegs<KS>& t, const uint16_t* kbase, const uint16_t* vbase,
+                                          int64_t k_sn, int64_t v_sn, int r0, int r_end, int last_row,
+                                          int span_k, int span_v, int col, int grp, int lane, bool act) {
+    constexpr int VT = KS;
+    // K: lane (row = col, group grp) takes elements [32c + 8*grp, +8) of the
+    // tile's k range for c < KS/2 -- a row's four groups read 64 contiguous bytes.
+    {
+        const int row = r0 + col;
+        const bool rv = act && row < r_end;
+        const uint16_t* src = kbase + (int64_t)min(row, last_row) * k_sn;
+#pragma unroll
+        for (int c = 0; c < KS / 2; ++c) {
+            const int kk = 32 * c + 8 * grp;
+            const bool ok = rv && kk + 8 <= span_k;
+            t.k[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src + (ok ? kk : 0)));
+        }
+    }
+    // V: 16 rows x 2*VT pieces of 16 bytes; piece p = 64c + lane is row
+    // p / (2VT), column piece p % (2VT) -- consecutive lanes, consecutive bytes.
+#pragma unroll
+    for (int c = 0; c < VT / 2; ++c) {
+        const int p = 64 * c + lane;
+        const int row = r0 + p / (2 * VT);
+        const int pc = p % (2 * VT);
+        const bool ok = act && row < r_end && 8 * pc + 8 <= span_v;
+        const uint16_t* src = vbase + (int64_t)min(row, last_row) * v_sn + (ok ? 8 * pc : 0);
+        t.v[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src));
+    }
+}
+
+// A workgroup owns (batch b, group of 4 tile slots, key split s); a slot is a
+// (KV head, column tile) pair and each wave takes one slot.  The four waves
+// therefore stream the same keys' rows at the same time (whole DRAM pages),
+// never exchange data, and write their own partials.
+template <int KS, bool PIPE>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int Hq,
                                               float scale_log2, char* lds) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
@@ -83,59 +139,42 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
     const int col = lane & 15;
     const int grp = lane >> 4;
 
+    const int slots = sg.hk * sg.tiles;
+    const int groups = (slots + kWaves - 1) / kWaves;
     const int s = w % sg.splits;
     int rem = w / sg.splits;
-    const int t = rem % sg.tiles;
-    rem /= sg.tiles;
-    const int h = rem % sg.hk;
-    const int b = rem / sg.hk;
+    const int sgp = rem % groups;
+    const int b = rem / groups;
+    const int slot = sgp * kWaves + wave;
+    if (slot >= slots) return;               // waves never synchronise, so an idle one may leave
+    const int h = slot / sg.tiles;
+    const int t = slot % sg.tiles;
 
     const int P = Lq * sg.g;
-    const int p0 = t * 16;
+    const int p0 = t * sg.cols;
     const int pl = p0 + col;
-    const bool colv = pl < P;
+    const bool colv = col < sg.cols && pl < P;
     const int jj = colv ? pl / Lq : 0;
     const int lq = colv ? pl % Lq : 0;
     const int j = h * sg.g + jj;
 
-    int k_off = 0, v_off = 0;
+    int k_off = 0, v_off = 0, first_blk = 0;
     int span_k = sg.wk, span_v = sg.wv;
-    int own_k_lo = 0, own_k_w = sg.wk, own_v_lo = 0, own_v_w = sg.wv;
+    int own_k_lo = 0, own_k_w = sg.wk, own_v_lo = 0;
     if (sg.blk_heads) {
-        const int pend = (P < p0 + 16 ? P : p0 + 16) - 1;
-        const int first_blk = (p0 / Lq) / sg.blk_heads;
+        const int pend = (P < p0 + sg.cols ? P : p0 + sg.cols) - 1;
+        first_blk = (p0 / Lq) / sg.blk_heads;
         const int last_blk = (pend / Lq) / sg.blk_heads;
         k_off = first_blk * sg.blk_k;
         v_off = first_blk * sg.blk_v;
         span_k = (last_blk - first_blk + 1) * sg.blk_k;
         span_v = (last_blk - first_blk + 1) * sg.blk_v;
-        const int blk = jj / sg.blk_heads;
-        own_k_lo = blk * sg.blk_k - k_off;
+        own_k_lo = (jj / sg.blk_heads) * sg.blk_k - k_off;
         own_k_w = sg.blk_k;
-        own_v_lo = blk * sg.blk_v - v_off;
-        own_v_w = sg.blk_v;
+        own_v_lo = (jj / sg.blk_heads) * sg.blk_v - v_off;
     }
     if (k_off + span_k > sg.wk) span_k = sg.wk - k_off;
     if (v_off + span_v > sg.wv) span_v = sg.wv - v_off;
-
-    // Query operand (B of the score MFMA): lane group `grp` owns the contiguous
-    // tile-relative k range [grp*4*KS, (grp+1)*4*KS); step s uses 4 of them.
-    v4s qb[KS];
-    {
-        const uint16_t* qrow = sg.q + (int64_t)b * sg.q_sb + (int64_t)lq * sg.q_sl + (int64_t)j * sg.q_sh;
-#pragma unroll
-        for (int c = 0; c < KS / 2; ++c) {
-            const int kk = grp * 4 * KS + 8 * c;
-            u32x4 val = {0u, 0u, 0u, 0u};
-            const bool in = colv && kk >= own_k_lo && kk + 8 <= own_k_lo + own_k_w && kk + 8 <= span_k;
-            if (in) {
-                const int idx = sg.q_compact ? (kk - own_k_lo) : (k_off + kk);
-                val = *reinterpret_cast<const u32x4*>(qrow + idx);
-            }
-            qb[2 * c] = as_v4s(val.x, val.y);
-            qb[2 * c + 1] = as_v4s(val.z, val.w);
-        }
-    }
 
     int Nb = sg.n;
     if (sg.seqlens) {
@@ -146,8 +185,35 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
     const int r_begin = s * sg.rows_per_split;
     const int r_end = min(r_begin + sg.rows_per_split, Nb);
     const int ntile = r_end > r_begin ? (r_end - r_begin + 15) / 16 : 0;
-    const int niter = (ntile + kWaves - 1) / kWaves;
     const int vis = min(lim, r_end);
+    const int last_row = sg.n - 1;
+
+    const uint16_t* kbase = sg.k + (int64_t)b * sg.k_sb + (int64_t)h * sg.k_sh + k_off;
+    const uint16_t* vbase = sg.v + (int64_t)b * sg.v_sb + (int64_t)h * sg.v_sh + v_off;
+
+    auto fetch = [&](TileRegs<KS>& tr, int it) {
+        const bool act = it < ntile;
+        const int r0 = act ? r_begin + it * 16 : r_begin;
+        load_tile<KS>(tr, kbase, vbase, sg.k_sn, sg.v_sn, r0, act ? r_end : r_begin, last_row, span_k, span_v,
+                      col, grp, lane, act);
+    };
+    // First tile in flight before the query operand is fetched.
+    TileRegs<KS> cur;
+    fetch(cur, 0);
+
+    // Query operand (B of the score MFMA), same k permutation as the K tile:
+    // step 2c+e holds elements 32c + 8*grp + 4e + [0,4).
+    u32x4 qv[KS / 2];
+    {
+        const uint16_t* qrow = sg.q + (int64_t)b * sg.q_sb + (int64_t)lq * sg.q_sl + (int64_t)j * sg.q_sh;
+#pragma unroll
+        for (int c = 0; c < KS / 2; ++c) {
+            const int kk = 32 * c + 8 * grp;
+            const bool in = colv && kk >= own_k_lo && kk + 8 <= own_k_lo + own_k_w && kk + 8 <= span_k;
+            const int idx = in ? (sg.q_compact ? (kk - own_k_lo) : (k_off + kk)) : 0;
+            qv[c] = zero_unless(in, *reinterpret_cast<const u32x4*>(qrow + idx));
+        }
+    }
 
     float m = kNegInf, lsum = 0.f;
     v4f acc[VT];
@@ -155,191 +221,136 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
     for (int i = 0; i < VT; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
 
     uint16_t* vbuf = reinterpret_cast<uint16_t*>(lds) + wave * 2 * 16 * RS;
-    const uint16_t* kbase = sg.k + (int64_t)b * sg.k_sb + (int64_t)h * sg.k_sh + k_off;
-    const uint16_t* vbase = sg.v + (int64_t)b * sg.v_sb + (int64_t)h * sg.v_sh + v_off;
-    const int vrow = lane >> 2;
-    const int vpart = lane & 3;
 
-    for (int it = 0; it < niter; ++it) {
-        const int rt = it * kWaves + wave;
-        const int r0 = r_begin + rt * 16;
-        const bool act = rt < ntile;
-
-        // K tile as the A operand: lane row = col, contiguous 4*KS elements.
-        v4s ka[KS];
-        {
-            const int row = r0 + col;
-            const bool rv = act && row < r_end;
-            const uint16_t* src = kbase + (int64_t)row * sg.k_sn;
+    // One 16-key tile: V to LDS, scores, online softmax, P^T V^T.
+    auto consume = [&](const TileRegs<KS>& tile, int it) {
+        const int r0 = r_begin + it * 16;
+        uint16_t* vb = vbuf + (it & 1) * 16 * RS;
 #pragma unroll
-            for (int c = 0; c < KS / 2; ++c) {
-                const int kk = grp * 4 * KS + 8 * c;
-                u32x4 val = {0u, 0u, 0u, 0u};
-                if (rv && kk + 8 <= span_k) val = *reinterpret_cast<const u32x4*>(src + kk);
-                ka[2 * c] = as_v4s(val.x, val.y);
-                ka[2 * c + 1] = as_v4s(val.z, val.w);
-            }
+        for (int c = 0; c < VT / 2; ++c) {
+            const int p = 64 * c + lane;
+            *reinterpret_cast<u32x4*>(vb + (p / (2 * VT)) * RS + 8 * (p % (2 * VT))) = tile.v[c];
         }
-        // V tile staged in LDS: lane copies 4*VT elements of row vrow.
-        {
-            const int row = r0 + vrow;
-            const bool rv = act && row < r_end;
-            const uint16_t* src = vbase + (int64_t)row * sg.v_sn;
-            uint16_t* dst = vbuf + (it & 1) * 16 * RS + vrow * RS + vpart * 4 * VT;
+        // Two independent accumulation chains halve the MFMA dependency latency.
+        v4f sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < VT / 2; ++c) {
-                const int vv = vpart * 4 * VT + 8 * c;
-                u32x4 val = {0u, 0u, 0u, 0u};
-                if (rv && vv + 8 <= span_v) val = *reinterpret_cast<const u32x4*>(src + vv);
-                *reinterpret_cast<u32x4*>(dst + 8 * c) = val;
-            }
+        for (int c = 0; c < KS / 2; ++c) {
+            sc0 = mfma16(as_v4s(tile.k[c].x, tile.k[c].y), as_v4s(qv[c].x, qv[c].y), sc0);
+            sc1 = mfma16(as_v4s(tile.k[c].z, tile.k[c].w), as_v4s(qv[c].z, qv[c].w), sc1);
         }
-
-        uint32_t pw0 = 0, pw1 = 0;
-        if (act) {
-            v4f sc = {0.f, 0.f, 0.f, 0.f};
+        const v4f sc = sc0 + sc1;
+        float sv[4];
+        float tmax = kNegInf;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) sc = mfma16(ka[ks], qb[ks], sc);
-            float sv[4];
-            float tmax = kNegInf;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int n = r0 + 4 * grp + i;
-                const float x = n < vis ? sc[i] * scale_log2 : kNegInf;
-                sv[i] = x;
-                tmax = fmaxf(tmax, x);
-            }
-            tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-            tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-            const float mnew = fmaxf(m, tmax);
-            const float mref = mnew == kNegInf ? 0.f : mnew;
-            const float alpha = fast_exp2(m - mref);
-            float p[4];
-            float psum = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                p[i] = fast_exp2(sv[i] - mref);
-                psum += p[i];
-            }
-            lsum = lsum * alpha + psum;
-            m = mnew;
-#pragma unroll
-            for (int i = 0; i < VT; ++i) acc[i] *= alpha;
-            pw0 = f32_to_bf16(p[0]) | (f32_to_bf16(p[1]) << 16);
-            pw1 = f32_to_bf16(p[2]) | (f32_to_bf16(p[3]) << 16);
+        for (int i = 0; i < 4; ++i) {
+            const int n = r0 + 4 * grp + i;
+            const float x = n < vis ? sc[i] * scale_log2 : kNegInf;
+            sv[i] = x;
+            tmax = fmaxf(tmax, x);
         }
-        __syncthreads();
-        if (act) {
-            const v4s pb = as_v4s(pw0, pw1);
-            const uint16_t* vb = vbuf + (it & 1) * 16 * RS;
+        tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
+        tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+        const float mnew = fmaxf(m, tmax);
+        const float mref = mnew == kNegInf ? 0.f : mnew;
+        const float alpha = fast_exp2(m - mref);
+        float p[4];
+        float psum = 0.f;
 #pragma unroll
-            for (int u = 0; u < VT / 2; ++u) {
-                uint32_t w4[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    w4[i] = *reinterpret_cast<const uint32_t*>(vb + (4 * grp + i) * RS + 32 * u + 2 * col);
-                const v4s lo = as_v4s((w4[0] & 0xffffu) | (w4[1] << 16), (w4[2] & 0xffffu) | (w4[3] << 16));
-                const v4s hi = as_v4s((w4[0] >> 16) | (w4[1] & 0xffff0000u), (w4[2] >> 16) | (w4[3] & 0xffff0000u));
-                acc[2 * u] = mfma16(lo, pb, acc[2 * u]);
-                acc[2 * u + 1] = mfma16(hi, pb, acc[2 * u + 1]);
-            }
+        for (int i = 0; i < 4; ++i) {
+            p[i] = fast_exp2(sv[i] - mref);
+            psum += p[i];
         }
-    }
-
-    // Per-wave column sums: every lane group holds a quarter of the keys.
-    lsum += shfl_xor_f(lsum, 16);
-    lsum += shfl_xor_f(lsum, 32);
-
-    // Merge the four wavefront states through LDS (reusing the V buffers).
-    __syncthreads();
-    float* macc = reinterpret_cast<float*>(lds);                      // [wave][col][16*VT]
-    float* mml = reinterpret_cast<float*>(lds + SplitLds<KS>::bytes - kWaves * 16 * 2 * 4);
-    {
-        float* dst = macc + (wave * 16 + col) * 16 * VT;
+        lsum = lsum * alpha + psum;
+        m = mnew;
+#pragma unroll
+        for (int i = 0; i < VT; ++i) acc[i] *= alpha;
+        const v4s pb = as_v4s(f32_to_bf16(p[0]) | (f32_to_bf16(p[1]) << 16),
+                              f32_to_bf16(p[2]) | (f32_to_bf16(p[3]) << 16));
+        wave_lds_fence();
 #pragma unroll
         for (int u = 0; u < VT / 2; ++u) {
-            // lane holds v = 32u + 8*grp + 2i + e in acc[2u+e][i]
-            float o[8];
+            uint32_t w4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                o[2 * i] = acc[2 * u][i];
-                o[2 * i + 1] = acc[2 * u + 1][i];
-            }
-            float4* d4 = reinterpret_cast<float4*>(dst + 32 * u + 8 * grp);
-            d4[0] = make_float4(o[0], o[1], o[2], o[3]);
-            d4[1] = make_float4(o[4], o[5], o[6], o[7]);
+            for (int i = 0; i < 4; ++i)
+                w4[i] = *reinterpret_cast<const uint32_t*>(vb + (4 * grp + i) * RS + 32 * u + 2 * col);
+            const v4s lo = as_v4s((w4[0] & 0xffffu) | (w4[1] << 16), (w4[2] & 0xffffu) | (w4[3] << 16));
+            const v4s hi = as_v4s((w4[0] >> 16) | (w4[1] & 0xffff0000u), (w4[2] >> 16) | (w4[3] & 0xffff0000u));
+            acc[2 * u] = mfma16(lo, pb, acc[2 * u]);
+            acc[2 * u + 1] = mfma16(hi, pb, acc[2 * u + 1]);
         }
-        if (grp == 0) {
-            mml[(wave * 16 + col) * 2] = m;
-            mml[(wave * 16 + col) * 2 + 1] = lsum;
+        wave_lds_fence();
+    };
+
+    if constexpr (PIPE) {
+        // Ping-pong between two register sets so a tile's loads stay in flight
+        // while the previous tile is consumed (no register copy on the back
+        // edge).  Loads past the last tile are issued anyway (clamped, zeroed)
+        // to keep the outstanding-load count uniform.
+        TileRegs<KS> other;
+        for (int it = 0; it < ntile; it += 2) {
+            fetch(other, it + 1);
+            consume(cur, it);
+            if (it + 1 >= ntile) break;
+            fetch(cur, it + 2);
+            consume(other, it + 1);
         }
-    }
-    __syncthreads();
-    {
-        const int c = threadIdx.x & 15;
-        const int chunk = threadIdx.x >> 4;        // 16 chunks of VT values
-        const int pc = p0 + c;
-        if (pc < P) {
-            const int cj = h * sg.g + pc / Lq;
-            const int cl = pc % Lq;
-            const int pr = cj * Lq + cl;
-            float mw[kWaves];
-            float M = kNegInf;
-#pragma unroll
-            for (int ww = 0; ww < kWaves; ++ww) {
-                mw[ww] = mml[(ww * 16 + c) * 2];
-                M = fmaxf(M, mw[ww]);
-            }
-            const float Mref = M == kNegInf ? 0.f : M;
-            float wt[kWaves];
-            float L = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < kWaves; ++ww) {
-                wt[ww] = fast_exp2(mw[ww] - Mref);
-                L += mml[(ww * 16 + c) * 2 + 1] * wt[ww];
-            }
-            const int64_t slot = ((int64_t)b * Hq * Lq + pr) * sg.splits + s;
-            if (chunk == 0) {
-                sg.part_ml[slot * 2] = M;
-                sg.part_ml[slot * 2 + 1] = L;
-            }
-            int c_own_lo = 0;
-            if (sg.blk_heads) {
-                const int first_blk = (p0 / Lq) / sg.blk_heads;
-                c_own_lo = (pc / Lq / sg.blk_heads) * sg.blk_v - first_blk * sg.blk_v;
-            }
-            float* dst = sg.part_acc + slot * sg.wown;
-#pragma unroll
-            for (int e = 0; e < VT; ++e) {
-                const int vv = chunk * VT + e;
-                const int o = vv - c_own_lo;
-                if (o >= 0 && o < sg.wown && vv < span_v) {
-                    float sum = 0.f;
-#pragma unroll
-                    for (int ww = 0; ww < kWaves; ++ww)
-                        sum += macc[(ww * 16 + c) * 16 * VT + vv] * wt[ww];
-                    dst[o] = sum;
-                }
-            }
+    } else {
+        for (int it = 0; it < ntile; ++it) {
+            if (it) fetch(cur, it);
+            consume(cur, it);
         }
     }
-    (void)own_v_lo;
-    (void)own_v_w;
+
+    // Column sums: every lane group holds a quarter of the keys.
+    lsum += shfl_xor_f(lsum, 16);
+    lsum += shfl_xor_f(lsum, 32);
+    if (!colv) return;
+    const int pr = j * Lq + lq;
+    const int64_t slot_out = ((int64_t)b * Hq * Lq + pr) * sg.splits + s;
+    if (grp == 0) {
+        sg.part_ml[slot_out * 2] = m;
+        sg.part_ml[slot_out * 2 + 1] = lsum;
+    }
+    // Lane holds v = 32u + 8*grp + 2i + e in acc[2u+e][i]: eight consecutive
+    // values per u, all inside or all outside the column's own V slice.
+    float* dst = sg.part_acc + slot_out * sg.wown;
+#pragma unroll
+    for (int u = 0; u < VT / 2; ++u) {
+        const int v0 = 32 * u + 8 * grp;
+        const int o = v0 - own_v_lo;
+        if (o >= 0 && o + 8 <= sg.wown && v0 + 8 <= span_v) {
+            float4* d4 = reinterpret_cast<float4*>(dst + o);
+            d4[0] = make_float4(acc[2 * u][0], acc[2 * u + 1][0], acc[2 * u][1], acc[2 * u + 1][1]);
+            d4[1] = make_float4(acc[2 * u][2], acc[2 * u + 1][2], acc[2 * u][3], acc[2 * u + 1][3]);
+        }
+    }
+    (void)first_blk;
 }
 
+// Segment 0 (KA, pipelined) is the bulk segment.  The optional segment 1 (KB,
+// single register set) is short work -- the raw rows of the fused decode in
+// 32-key splits -- and is placed first in the grid so it drains while the bulk
+// workgroups stream.
+template <int KA>
+struct SplitWaves {
+    static constexpr int value = KA <= 4 ? 4 : (KA <= 6 ? 3 : 1);
+};
+
 template <int KA, int KB>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SplitWaves<KA>::value)))
 split_kernel(SplitParams prm) {
     constexpr int LA = SplitLds<KA>::bytes;
     constexpr int LB = KB > 0 ? SplitLds<(KB > 0 ? KB : 2)>::bytes : 0;
     __shared__ __attribute__((aligned(16))) char lds[LA > LB ? LA : LB];
     int w = blockIdx.x;
-    if (w < prm.seg[0].nwg) {
-        split_segment<KA>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
-    } else if constexpr (KB > 0) {
-        w -= prm.seg[0].nwg;
-        split_segment<KB>(prm.seg[1], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+    if constexpr (KB > 0) {
+        if (w < prm.seg[1].nwg) {
+            split_segment<KB, false>(prm.seg[1], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+            return;
+        }
+        w -= prm.seg[1].nwg;
     }
+    split_segment<KA, true>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -359,13 +370,35 @@ struct CombineParams {
 
 constexpr int kMaxSplits = 256;
 constexpr int kMaxLatW = 1024;
+constexpr int kCombineThreads = 128;
 
-__global__ void __launch_bounds__(256)
+__device__ __forceinline__ float block_max128(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor_f(v, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = fmaxf(red[0], red[1]);
+    __syncthreads();
+    return v;
+}
+
+__device__ __forceinline__ float block_sum128(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_f(v, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0] + red[1];
+    __syncthreads();
+    return v;
+}
+
+// One workgroup per (b, query head, query): LSE-merge the split partials of
+// both segments, lift the latent accumulator through U_V, fold the biases.
+__global__ void __launch_bounds__(kCombineThreads)
 combine_kernel(CombineParams cp) {
-    __shared__ float wa[kMaxSplits];
-    __shared__ float wb[kMaxSplits];
+    __shared__ float wts[2 * kMaxSplits];
     __shared__ float accb[kMaxLatW];
-    __shared__ float red[4];
+    __shared__ float red[2];
     const int HL = cp.Hq * cp.Lq;
     const int pr = blockIdx.x % HL;
     const int b = blockIdx.x / HL;
@@ -376,49 +409,62 @@ combine_kernel(CombineParams cp) {
     const float* aml = cp.a_ml + row * cp.a_splits * 2;
     const float* bml = cp.b_splits ? cp.b_ml + row * cp.b_splits * 2 : nullptr;
     const float shift = (cp.b_splits && cp.b_shift) ? cp.b_shift[row] * kLog2e : 0.f;
+    const int total = cp.a_splits + cp.b_splits;
 
-    if (threadIdx.x == 0) {
-        float M = kNegInf;
-        for (int s = 0; s < cp.a_splits; ++s) M = fmaxf(M, aml[2 * s]);
-        for (int s = 0; s < cp.b_splits; ++s) {
-            const float mb = bml[2 * s];
-            if (mb != kNegInf) M = fmaxf(M, mb + shift);
-        }
-        const float Mref = M == kNegInf ? 0.f : M;
-        float LA = 0.f, LB = 0.f;
-        for (int s = 0; s < cp.a_splits; ++s) {
-            const float wgt = fast_exp2(aml[2 * s] - Mref);
-            wa[s] = wgt;
-            LA += aml[2 * s + 1] * wgt;
-        }
-        for (int s = 0; s < cp.b_splits; ++s) {
-            const float mb = bml[2 * s];
-            const float wgt = mb == kNegInf ? 0.f : fast_exp2(mb + shift - Mref);
-            wb[s] = wgt;
-            LB += bml[2 * s + 1] * wgt;
-        }
-        red[0] = M;
-        red[1] = LA;
-        red[2] = LB;
+    // Split maxima and masses, one split per thread.
+    float mloc = kNegInf;
+    for (int s = threadIdx.x; s < total; s += kCombineThreads) {
+        float mv = s < cp.a_splits ? aml[2 * s] : bml[2 * (s - cp.a_splits)];
+        if (s >= cp.a_splits && mv != kNegInf) mv += shift;
+        wts[s] = mv;
+        mloc = fmaxf(mloc, mv);
     }
-    __syncthreads();
-    const float M = red[0], LA = red[1], LB = red[2];
+    const float M = block_max128(mloc, red);
+    const float Mref = M == kNegInf ? 0.f : M;
+    float la = 0.f, lb = 0.f;
+    for (int s = threadIdx.x; s < total; s += kCombineThreads) {
+        const float wgt = wts[s] == kNegInf ? 0.f : fast_exp2(wts[s] - Mref);
+        wts[s] = wgt;
+        if (s < cp.a_splits) la += aml[2 * s + 1] * wgt;
+        else lb += bml[2 * (s - cp.a_splits) + 1] * wgt;
+    }
+    const float LA = block_sum128(la, red);
+    const float LB = block_sum128(lb, red);
     const float L = LA + LB;
+
     if (cp.b_splits) {
+        // Weighted latent accumulator: threads split (k, split group).
         const float* bacc = cp.b_acc + row * cp.b_splits * cp.b_w;
-        for (int k = threadIdx.x; k < cp.b_w; k += blockDim.x) {
+        const float* wb = wts + cp.a_splits;
+        if (cp.b_w <= kCombineThreads / 2) {
+            const int groups = kCombineThreads / cp.b_w;
+            const int k = threadIdx.x % cp.b_w, gsel = threadIdx.x / cp.b_w;
             float sum = 0.f;
-            for (int s = 0; s < cp.b_splits; ++s) sum += bacc[(int64_t)s * cp.b_w + k] * wb[s];
-            accb[k] = sum;
+            if (gsel < groups)
+                for (int s = gsel; s < cp.b_splits; s += groups) sum += bacc[(int64_t)s * cp.b_w + k] * wb[s];
+            __shared__ float part[kCombineThreads];
+            part[threadIdx.x] = sum;
+            __syncthreads();
+            if (threadIdx.x < cp.b_w) {
+                float t = 0.f;
+                for (int g2 = 0; g2 < groups; ++g2) t += part[g2 * cp.b_w + threadIdx.x];
+                accb[threadIdx.x] = t;
+            }
+        } else {
+            for (int k = threadIdx.x; k < cp.b_w; k += kCombineThreads) {
+                float sum = 0.f;
+                for (int s = 0; s < cp.b_splits; ++s) sum += bacc[(int64_t)s * cp.b_w + k] * wb[s];
+                accb[k] = sum;
+            }
         }
         __syncthreads();
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
     const float* aacc = cp.a_acc + row * cp.a_splits * cp.a_w;
     uint16_t* orow = cp.out + (int64_t)b * cp.o_sb + (int64_t)lq * cp.o_sl + (int64_t)j * cp.o_sh;
-    for (int dd = threadIdx.x; dd < cp.D; dd += blockDim.x) {
+    for (int dd = threadIdx.x; dd < cp.D; dd += kCombineThreads) {
         float sum = 0.f;
-        for (int s = 0; s < cp.a_splits; ++s) sum += aacc[(int64_t)s * cp.a_w + dd] * wa[s];
+        for (int s = 0; s < cp.a_splits; ++s) sum += aacc[(int64_t)s * cp.a_w + dd] * wts[s];
         if (cp.b_splits) {
             const int64_t wrow = (int64_t)h * cp.D + dd;
             const uint16_t* wr = cp.up_v + wrow * cp.up_v_ld + (cp.blockdiag ? h * cp.b_w : 0);
@@ -442,6 +488,127 @@ combine_kernel(CombineParams cp) {
     }
 }
 
+// Fast path for the fused decode's shapes (D <= 128 output features, few raw
+// splits, narrow latent slices): every global load is issued before the first
+// reduction, so the whole combine costs one memory round trip.
+constexpr int kFastRawSplits = 32;
+constexpr int kFastLatW = 64;
+constexpr int kFastLatPer = 32;     // latent partial values per thread
+
+__global__ void __launch_bounds__(kCombineThreads)
+combine_fast_kernel(CombineParams cp) {
+    __shared__ float wts[2 * kMaxSplits];
+    __shared__ float part[kCombineThreads];
+    __shared__ float accb[kFastLatW];
+    __shared__ float red[2];
+    const int t = threadIdx.x;
+    const int HL = cp.Hq * cp.Lq;
+    const int pr = blockIdx.x % HL;
+    const int b = blockIdx.x / HL;
+    const int j = pr / cp.Lq;
+    const int lq = pr % cp.Lq;
+    const int h = j / (cp.Hq / cp.Hkv);
+    const int64_t row = (int64_t)b * HL + pr;
+    const int total = cp.a_splits + cp.b_splits;
+    const float* aml = cp.a_ml + row * cp.a_splits * 2;
+    const float* bml = cp.b_splits ? cp.b_ml + row * cp.b_splits * 2 : nullptr;
+
+    // -- issue every load --
+    float mv = kNegInf, lv = 0.f;
+    if (t < total) {
+        const float* src = t < cp.a_splits ? aml + 2 * t : bml + 2 * (t - cp.a_splits);
+        mv = src[0];
+        lv = src[1];
+    }
+    const float shift = (cp.b_splits && cp.b_shift) ? cp.b_shift[row] * kLog2e : 0.f;
+    const int dd = t;
+    const bool has_dd = dd < cp.D;
+    float ra[kFastRawSplits];
+    const float* aacc = cp.a_acc + row * cp.a_splits * cp.a_w;
+#pragma unroll
+    for (int s = 0; s < kFastRawSplits; ++s) ra[s] = (has_dd && s < cp.a_splits) ? aacc[(int64_t)s * cp.a_w + dd] : 0.f;
+    // latent: thread handles column k = t % b_w of splits s = t / b_w + i * (128 / b_w)
+    float lb[kFastLatPer];
+    const int kcol = cp.b_w ? t % cp.b_w : 0;
+    const int sstep = cp.b_w ? kCombineThreads / cp.b_w : 1;
+    const int s0 = cp.b_w ? t / cp.b_w : 0;
+    const float* bacc = cp.b_splits ? cp.b_acc + row * cp.b_splits * cp.b_w : nullptr;
+#pragma unroll
+    for (int i = 0; i < kFastLatPer; ++i) {
+        const int s = s0 + i * sstep;
+        lb[i] = (bacc && s < cp.b_splits && s0 < sstep) ? bacc[(int64_t)s * cp.b_w + kcol] : 0.f;
+    }
+    u32x4 wv[kFastLatW / 8];
+    const uint16_t* wr = nullptr;
+    if (cp.b_splits && has_dd) {
+        const int64_t wrow = (int64_t)h * cp.D + dd;
+        wr = cp.up_v + wrow * cp.up_v_ld + (cp.blockdiag ? h * cp.b_w : 0);
+    }
+#pragma unroll
+    for (int c = 0; c < kFastLatW / 8; ++c)
+        wv[c] = (wr && 8 * c < cp.b_w) ? *reinterpret_cast<const u32x4*>(wr + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    const float bias_v = (cp.b_splits && cp.up_v_bias && has_dd) ? bf16_to_f32(cp.up_v_bias[(int64_t)h * cp.D + dd]) : 0.f;
+
+    // -- split weights --
+    if (t >= cp.a_splits && t < total && mv != kNegInf) mv += shift;
+    const float M = block_max128(mv, red);
+    const float Mref = M == kNegInf ? 0.f : M;
+    const float wgt = (t < total && mv != kNegInf) ? fast_exp2(mv - Mref) : 0.f;
+    if (t < total) wts[t] = wgt;
+    const float LA = block_sum128(t < cp.a_splits ? lv * wgt : 0.f, red);
+    const float LB = block_sum128(t >= cp.a_splits && t < total ? lv * wgt : 0.f, red);
+    const float L = LA + LB;    // block_sum128 synchronised, so wts[] is visible
+
+    // -- latent accumulator --
+    if (cp.b_splits) {
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < kFastLatPer; ++i) {
+            const int s = s0 + i * sstep;
+            if (s < cp.b_splits && s0 < sstep) sum += lb[i] * wts[cp.a_splits + s];
+        }
+        part[t] = sum;
+        __syncthreads();
+        if (t < cp.b_w) {
+            float acc = 0.f;
+            for (int g2 = 0; g2 < sstep; ++g2) acc += part[g2 * cp.b_w + t];
+            accb[t] = acc;
+        }
+        __syncthreads();
+    }
+    // -- output --
+    if (has_dd) {
+        float sum = 0.f;
+#pragma unroll
+        for (int s = 0; s < kFastRawSplits; ++s)
+            if (s < cp.a_splits) sum += ra[s] * wts[s];
+        if (cp.b_splits) {
+            float lift = 0.f;
+#pragma unroll
+            for (int c = 0; c < kFastLatW / 8; ++c) {
+                if (8 * c >= cp.b_w) break;
+                const uint32_t w4[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lift += bf16_to_f32(w4[e] & 0xffffu) * accb[8 * c + 2 * e];
+                    lift += bf16_to_f32(w4[e] >> 16) * accb[8 * c + 2 * e + 1];
+                }
+            }
+            sum += lift + bias_v * LB;
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        cp.out[(int64_t)b * cp.o_sb + (int64_t)lq * cp.o_sl + (int64_t)j * cp.o_sh + dd] = (uint16_t)f32_to_bf16(sum * inv);
+    }
+    if (cp.lse && t == 0)
+        cp.lse[((int64_t)b * cp.Hq + j) * cp.Lq + lq] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
+}
+
+bool combine_fast_ok(const CombineParams& cp) {
+    return cp.D <= kCombineThreads && cp.a_splits <= kFastRawSplits && cp.a_splits + cp.b_splits <= kCombineThreads &&
+           cp.b_w <= kFastLatW && (cp.b_splits == 0 ||
+           (kCombineThreads % cp.b_w == 0 && cp.b_splits <= kFastLatPer * (kCombineThreads / cp.b_w)));
+}
+
 // ---------------------------------------------------------------------------
 // prologue: query RoPE + absorption into U_K + K-bias shift
 // ---------------------------------------------------------------------------
@@ -455,84 +622,121 @@ struct PrologueParams {
     int blockdiag; int wq;                 // q_lat width (own block or Rk)
     uint16_t* q_lat;                       // [B][Lq][Hq][wq]
     float* shift;                          // [B][Hq*Lq] or null
-    int B, Lq, Hq, Hkv, D, Rk, parts;
+    int B, Lq, Hq, Hkv, D, Rk, parts;      // parts: power of two <= 16 dividing D
     float scale;
 };
 
 constexpr int kMaxRows = 16;
+constexpr int kMaxD = 256;
 
+// One workgroup per (b, KV head).  Rows r = jj*Lq + l of the head's query group
+// are rotated into LDS; thread (k8, part) then forms 8 consecutive q_lat
+// columns over a D/parts slice with 16-byte weight loads, and the parts are
+// reduced with lane shuffles (they are adjacent lanes).
 __global__ void __launch_bounds__(256)
 prologue_kernel(PrologueParams pp) {
-    extern __shared__ float sh[];          // [rows][D] rotated q, then [parts][rows][wq chunk]
+    __shared__ float qs[kMaxRows * kMaxD];
     const int h = blockIdx.x % pp.Hkv;
     const int b = blockIdx.x / pp.Hkv;
     const int g = pp.Hq / pp.Hkv;
-    const int rows = g * pp.Lq;            // r = jj*Lq + l
-    float* qs = sh;
-    // RoPE (or copy) each query row of this KV head.
-    for (int e = threadIdx.x; e < rows * pp.D; e += blockDim.x) {
-        const int r = e / pp.D, dd = e % pp.D;
+    const int rows = g * pp.Lq;
+    const int D = pp.D;
+    const int pieces = D / 8;
+    for (int e = threadIdx.x; e < rows * pieces; e += blockDim.x) {
+        const int r = e / pieces, dd = (e % pieces) * 8;
         const int jj = r / pp.Lq, l = r % pp.Lq;
         const int jh = h * g + jj;
         const uint16_t* qrow = pp.q + (int64_t)b * pp.q_sb + (int64_t)l * pp.q_sl + (int64_t)jh * pp.q_sh;
-        float x = bf16_to_f32(qrow[dd]);
-        if (pp.cos) {
-            const int half = pp.D / 2;
-            const float partner = bf16_to_f32(qrow[(dd + half) % pp.D]);
-            const float rot = dd < half ? -partner : partner;
-            const int64_t ps = clamp_i64(pp.pos[(int64_t)b * pp.pos_sb + l], 0, pp.rope_rows - 1);
-            const float c = round_bf16(pp.cos[ps * pp.D + dd]);
-            const float sn = round_bf16(pp.sin[ps * pp.D + dd]);
-            x = round_bf16(round_bf16(x * c) + round_bf16(rot * sn));
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(qrow + dd);
+        uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = bf16_to_f32(xs[i] & 0xffffu);
+            x[2 * i + 1] = bf16_to_f32(xs[i] >> 16);
         }
-        qs[e] = x;
-        pp.q_rot[(((int64_t)b * pp.Lq + l) * pp.Hq + jh) * pp.D + dd] = (uint16_t)f32_to_bf16(x);
+        if (pp.cos) {
+            const int half = D / 2;
+            const int pd = dd < half ? dd + half : dd - half;
+            const u32x4 pv = *reinterpret_cast<const u32x4*>(qrow + pd);
+            const uint32_t ps[4] = {pv.x, pv.y, pv.z, pv.w};
+            const int64_t pos = clamp_i64(pp.pos[(int64_t)b * pp.pos_sb + l], 0, pp.rope_rows - 1);
+            const float4* c4 = reinterpret_cast<const float4*>(pp.cos + pos * D + dd);
+            const float4* s4 = reinterpret_cast<const float4*>(pp.sin + pos * D + dd);
+            const float4 ca = c4[0], cb = c4[1], sa = s4[0], sb = s4[1];
+            const float cs[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+            const float ss[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float pt = bf16_to_f32(i & 1 ? (ps[i / 2] >> 16) : (ps[i / 2] & 0xffffu));
+                if (dd < half) pt = -pt;
+                x[i] = round_bf16(round_bf16(x[i] * round_bf16(cs[i])) + round_bf16(pt * round_bf16(ss[i])));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xs[i] = f32_to_bf16(x[2 * i]) | (f32_to_bf16(x[2 * i + 1]) << 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qs[r * D + dd + i] = x[i];
+        *reinterpret_cast<u32x4*>(pp.q_rot + (((int64_t)b * pp.Lq + l) * pp.Hq + jh) * D + dd) =
+            u32x4{xs[0], xs[1], xs[2], xs[3]};
     }
     __syncthreads();
     if (pp.shift && threadIdx.x < rows) {
         const int r = threadIdx.x;
         const int jj = r / pp.Lq, l = r % pp.Lq;
         float sum = 0.f;
-        for (int dd = 0; dd < pp.D; ++dd)
-            sum += qs[r * pp.D + dd] * bf16_to_f32(pp.up_k_bias[(int64_t)h * pp.D + dd]);
+        for (int dd = 0; dd < D; ++dd)
+            sum += qs[r * D + dd] * bf16_to_f32(pp.up_k_bias[(int64_t)h * D + dd]);
         pp.shift[(int64_t)b * pp.Hq * pp.Lq + (h * g + jj) * pp.Lq + l] = sum * pp.scale;
     }
-    // Absorption: q_lat[r][k] = sum_dd qs[r][dd] * W[h*D+dd][kg].
-    float* part = sh + rows * pp.D;        // [parts][rows][256]
+    if (pp.wq == 0) return;
+    // Absorption: thread (row r, 8-column group k8, part) sums D/parts terms for
+    // 8 consecutive q_lat columns; partial sums meet in LDS.
+    __shared__ float red[256 * 8];
     const int parts = pp.parts;
-    const int per = pp.D / parts;
-    for (int k0 = 0; k0 < pp.wq; k0 += 256 / parts) {
-        const int kc = 256 / parts;
-        const int tk = threadIdx.x % kc, tp = threadIdx.x / kc;
-        const int k = k0 + tk;
-        float accr[kMaxRows];
+    const int per = D / parts;
+    const int k8n = pp.wq / 8;
+    for (int base = 0; base < rows * k8n * parts; base += 256) {
+        const int task = base + threadIdx.x;
+        const bool active = task < rows * k8n * parts;
+        const int part = task % parts;
+        const int rk = task / parts;            // r * k8n + k8
+        const int r = rk / k8n, k8 = rk % k8n;
+        float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (active) {
+            const int kg = (pp.blockdiag ? h * pp.wq : 0) + 8 * k8;
+            const uint16_t* wbase = pp.up_k + ((int64_t)h * D + part * per) * pp.Rk + kg;
+            const float* qr = qs + r * D + part * per;
+            for (int d0 = 0; d0 < per; d0 += 8) {
+                u32x4 wv[8];
 #pragma unroll
-        for (int r = 0; r < kMaxRows; ++r) accr[r] = 0.f;
-        if (k < pp.wq && tp < parts) {
-            const int kg = pp.blockdiag ? h * pp.wq + k : k;
-            const uint16_t* wcol = pp.up_k + ((int64_t)h * pp.D) * pp.Rk + kg;
-            for (int dd = tp * per; dd < (tp + 1) * per; ++dd) {
-                const float wv = bf16_to_f32(wcol[(int64_t)dd * pp.Rk]);
+                for (int i = 0; i < 8; ++i) wv[i] = *reinterpret_cast<const u32x4*>(wbase + (int64_t)(d0 + i) * pp.Rk);
 #pragma unroll
-                for (int r = 0; r < kMaxRows; ++r)
-                    if (r < rows) accr[r] += qs[r * pp.D + dd] * wv;
+                for (int i = 0; i < 8; ++i) {
+                    const float qv = qr[d0 + i];
+                    const uint32_t w4[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc8[2 * e] += qv * bf16_to_f32(w4[e] & 0xffffu);
+                        acc8[2 * e + 1] += qv * bf16_to_f32(w4[e] >> 16);
+                    }
+                }
             }
         }
-        __syncthreads();
-        if (k < pp.wq && tp < parts) {
 #pragma unroll
-            for (int r = 0; r < kMaxRows; ++r)
-                if (r < rows) part[(tp * rows + r) * kc + tk] = accr[r];
-        }
+        for (int e = 0; e < 8; ++e) red[threadIdx.x * 8 + e] = acc8[e];
         __syncthreads();
-        for (int e = threadIdx.x; e < rows * kc; e += blockDim.x) {
-            const int r = e / kc, kk = e % kc;
-            const int kq = k0 + kk;
-            if (kq >= pp.wq) continue;
-            float sum = 0.f;
-            for (int p = 0; p < parts; ++p) sum += part[(p * rows + r) * kc + kk];
+        if (active && part == 0) {
+            float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int q = 0; q < parts; ++q)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sum[e] += red[(threadIdx.x + q) * 8 + e];
             const int jj = r / pp.Lq, l = r % pp.Lq;
-            pp.q_lat[(((int64_t)b * pp.Lq + l) * pp.Hq + h * g + jj) * pp.wq + kq] = (uint16_t)f32_to_bf16(sum);
+            uint32_t o4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = f32_to_bf16(sum[2 * e]) | (f32_to_bf16(sum[2 * e + 1]) << 16);
+            *reinterpret_cast<u32x4*>(pp.q_lat + (((int64_t)b * pp.Lq + l) * pp.Hq + h * g + jj) * pp.wq + 8 * k8) =
+                u32x4{o4[0], o4[1], o4[2], o4[3]};
         }
         __syncthreads();
     }
@@ -563,7 +767,7 @@ hipError_t timed_split(int ka, int kb, const SplitParams& prm, int grid, hipStre
 int round_even_tile(int width) {
     // MFMA k-steps of 16 needed for `width`, rounded to the instantiated set.
     const int ks = (width + 15) / 16;
-    const int set[] = {4, 8, 12, 16, 24};
+    const int set[] = {2, 4, 6, 8, 12, 16, 24};
     for (int v : set)
         if (ks <= v) return v;
     return -1;
@@ -575,25 +779,27 @@ bool ptr_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15)
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct SegPlan {
-    int tiles, splits, rows_per_split, nwg, wown, ks;
+    int tiles, cols, splits, rows_per_split, nwg, wown, ks;
 };
 
 // Split the key range so the launch holds a few workgroups per CU.
-SegPlan plan_segment(int B, int hk, int P, int n, int span_k, int wown, int req_splits, int target_wg) {
+SegPlan plan_segment(int B, int hk, int P, int cols, int n, int span_k, int wown, int req_splits,
+                     int target_wg) {
     SegPlan sp{};
-    sp.tiles = (P + 15) / 16;
+    sp.cols = std::min(cols, 16);
+    sp.tiles = (P + sp.cols - 1) / sp.cols;
     sp.ks = round_even_tile(span_k);
     sp.wown = wown;
-    const int groups = B * hk * sp.tiles;
+    const int groups = B * ((hk * sp.tiles + kWaves - 1) / kWaves);
     int splits = req_splits;
     if (splits <= 0) {
-        const int max_by_rows = std::max(1, (n + 63) / 64);
+        const int max_by_rows = std::max(1, (n + 15) / 16);
         splits = std::max(1, std::min(max_by_rows, (target_wg + groups - 1) / groups));
         splits = std::min(splits, kMaxSplits);
     }
     splits = std::min(splits, kMaxSplits);
     int rps = (n + splits - 1) / splits;
-    rps = std::max(64, (rps + 63) / 64 * 64);
+    rps = std::max(16, (rps + 15) / 16 * 16);
     splits = std::max(1, (n + rps - 1) / rps);
     sp.splits = splits;
     sp.rows_per_split = rps;
@@ -608,25 +814,53 @@ hipError_t launch_split(const SplitParams& prm, int grid, hipStream_t st) {
 }
 
 hipError_t dispatch_split(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st) {
-#define SLIMKV_CASE_B(A)                                            \
-    switch (kb) {                                                   \
-        case 0: return launch_split<A, 0>(prm, grid, st);           \
-        case 4: return launch_split<A, 4>(prm, grid, st);           \
-        case 8: return launch_split<A, 8>(prm, grid, st);           \
-        case 12: return launch_split<A, 12>(prm, grid, st);         \
-        case 16: return launch_split<A, 16>(prm, grid, st);         \
-        case 24: return launch_split<A, 24>(prm, grid, st);         \
-        default: return hipErrorInvalidValue;                       \
+    if (kb == 0) {
+        switch (ka) {
+            case 2: return launch_split<2, 0>(prm, grid, st);
+            case 4: return launch_split<4, 0>(prm, grid, st);
+            case 6: return launch_split<6, 0>(prm, grid, st);
+            case 8: return launch_split<8, 0>(prm, grid, st);
+            case 12: return launch_split<12, 0>(prm, grid, st);
+            case 16: return launch_split<16, 0>(prm, grid, st);
+            case 24: return launch_split<24, 0>(prm, grid, st);
+            default: return hipErrorInvalidValue;
+        }
     }
+    if (kb != 8) return hipErrorInvalidValue;   // the raw segment is head_dim 128
     switch (ka) {
-        case 4: if (kb != 0) return hipErrorInvalidValue; return launch_split<4, 0>(prm, grid, st);
-        case 8: SLIMKV_CASE_B(8)
-        case 12: if (kb != 0) return hipErrorInvalidValue; return launch_split<12, 0>(prm, grid, st);
-        case 16: if (kb != 0) return hipErrorInvalidValue; return launch_split<16, 0>(prm, grid, st);
-        case 24: if (kb != 0) return hipErrorInvalidValue; return launch_split<24, 0>(prm, grid, st);
+        case 2: return launch_split<2, 8>(prm, grid, st);
+        case 4: return launch_split<4, 8>(prm, grid, st);
+        case 6: return launch_split<6, 8>(prm, grid, st);
+        case 8: return launch_split<8, 8>(prm, grid, st);
+        case 12: return launch_split<12, 8>(prm, grid, st);
+        case 16: return launch_split<16, 8>(prm, grid, st);
+        case 24: return launch_split<24, 8>(prm, grid, st);
         default: return hipErrorInvalidValue;
     }
-#undef SLIMKV_CASE_B
+}
+
+// Resident workgroups per CU of a split-kernel instance (cached per device).
+int split_occupancy(int ka, int kb) {
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> keys;
+    static std::vector<int> vals;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const int key = (dev << 16) | (ka << 8) | kb;
+    std::lock_guard<std::mutex> lock(mu);
+    for (size_t i = 0; i < keys.size(); ++i)
+        if (keys[i].first == key) return vals[i];
+    const void* fn = nullptr;
+#define SLIMKV_FN(A, B) if (ka == A && kb == B) fn = reinterpret_cast<const void*>(&split_kernel<A, B>);
+    SLIMKV_FN(2, 0) SLIMKV_FN(2, 8) SLIMKV_FN(4, 0) SLIMKV_FN(6, 0) SLIMKV_FN(8, 0) SLIMKV_FN(12, 0) SLIMKV_FN(16, 0) SLIMKV_FN(24, 0)
+    SLIMKV_FN(4, 8) SLIMKV_FN(6, 8) SLIMKV_FN(8, 8) SLIMKV_FN(12, 8) SLIMKV_FN(16, 8) SLIMKV_FN(24, 8)
+#undef SLIMKV_FN
+    int blocks = 0;
+    if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, 0) != hipSuccess || blocks < 1)
+        blocks = 1;
+    keys.push_back({key, 0});
+    vals.push_back(blocks);
+    return blocks;
 }
 
 struct AttnPlan {
@@ -651,9 +885,10 @@ int plan_attention(const slimkv_attention_args* a, AttnPlan* plan) {
     const int g = (int)(Hq / Hk);
     const int P = (int)Lq * g;
     const int span = (int)std::max(a->width_k, a->width_v);
-    const int target = 4 * device_cu_count();
-    plan->sp = plan_segment((int)B, (int)Hk, P, (int)N, span, (int)a->width_v, a->splits, target);
-    if (plan->sp.ks < 0) return fail(SLIMKV_EUNSUP, "width not supported");
+    const int ks = round_even_tile(span);
+    if (ks < 0) return fail(SLIMKV_EUNSUP, "width not supported");
+    const int target = device_cu_count() * split_occupancy(ks, 0);
+    plan->sp = plan_segment((int)B, (int)Hk, P, 16, (int)N, span, (int)a->width_v, a->splits, target);
     if (a->splits > kMaxSplits) return fail(SLIMKV_EINVAL, "too many splits");
     const size_t rows = (size_t)B * Hq * Lq * plan->sp.splits;
     plan->ml_off = 0;
@@ -738,6 +973,7 @@ extern "C" int slimkv_attention_forward(const slimkv_attention_args* a, void* wo
     sg.wv = (int)a->width_v;
     sg.causal = a->causal ? 1 : 0;
     sg.tiles = plan.sp.tiles;
+    sg.cols = plan.sp.cols;
     sg.splits = plan.sp.splits;
     sg.rows_per_split = plan.sp.rows_per_split;
     sg.part_ml = reinterpret_cast<float*>(ws + plan.ml_off);
@@ -753,7 +989,10 @@ extern "C" int slimkv_attention_forward(const slimkv_attention_args* a, void* wo
     cp.B = prm.B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hk; cp.D = (int)a->width_v;
     cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
     cp.lse = a->lse;
-    hipLaunchKernelGGL(combine_kernel, dim3(prm.B * Hq * Lq), dim3(128), 0, st, cp);
+    if (combine_fast_ok(cp))
+        hipLaunchKernelGGL(combine_fast_kernel, dim3(prm.B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
+    else
+        hipLaunchKernelGGL(combine_kernel, dim3(prm.B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
     return check_hip(hipGetLastError(), "combine kernel launch");
 }
 
@@ -802,31 +1041,41 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p) {
     const int rk = (int)(bd ? Rk / Hkv : Rk);
     const int rv = (int)(bd ? Rv / Hkv : Rv);
     const int cu = device_cu_count();
-    // Raw: one column tile per KV head over the full head width.
-    p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, (int)a->raw_keys, (int)D, (int)D, a->raw_splits, cu);
-    if (p->raw.tiles != 1 || p->raw.ks != 8) return fail(SLIMKV_EUNSUP, "raw tile shape");
-    // Latent: every query head against shared rows; block-diagonal tiles only
-    // span the latent slices of their own heads.
+    // Latent: every query head against shared rows.  With block-diagonal bases a
+    // tile spans only its own heads' latent slices; narrow tiles (8 packed rows)
+    // keep the slice span -- and the register footprint -- small.
     const int P = (int)(Lq * Hq);
-    int span = (int)std::max(Rk, Rv);
-    if (bd) {
+    auto span_of = [&](int cols) {
+        if (!bd) return (int)std::max(Rk, Rv);
         int worst = 0;
-        for (int t = 0; t * 16 < P; ++t) {
-            const int p0 = t * 16, pend = std::min(P, p0 + 16) - 1;
+        for (int t = 0; t * cols < P; ++t) {
+            const int p0 = t * cols, pend = std::min(P, p0 + cols) - 1;
             const int blocks = (pend / (int)Lq) / g - (p0 / (int)Lq) / g + 1;
             worst = std::max(worst, blocks * std::max(rk, rv));
         }
-        span = worst;
-    }
+        return worst;
+    };
+    // Eight packed rows per tile: 32 heads give four tiles, one per wave of a
+    // workgroup, all streaming the same latent rows.
+    const int cols = 8;
+    const int span = span_of(cols);
+    const int lat_ks = round_even_tile(span);
+    if (lat_ks < 0) return fail(SLIMKV_EUNSUP, "latent width not supported");
     const int64_t nl = std::max<int64_t>(a->lat_keys, 1);
-    p->lat = plan_segment((int)B, 1, P, (int)nl, span, rv, a->lat_splits, 4 * cu);
-    if (p->lat.ks < 0) return fail(SLIMKV_EUNSUP, "latent width not supported");
+    const int has_lat = a->lat_keys > 0;
+    const int slots = cu * split_occupancy(has_lat ? lat_ks : 8, has_lat ? 8 : 0);
+    p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, slots);
+    // Raw: one column tile per KV head over the full head width, one split per
+    // 16 keys so every raw wave issues all of its loads at once (the raw set is
+    // sinks + tail + current token).
+    const int raw_req = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
+    p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req, 0);
+    if (p->raw.tiles != 1 || p->raw.ks != 8) return fail(SLIMKV_EUNSUP, "raw tile shape");
     p->wq = rk;
     int parts = 1;
-    while (parts < 8 && p->wq * parts * 2 <= 256) parts *= 2;
+    while (parts < 16 && g * (int)Lq * (p->wq / 8) * parts * 2 <= 256) parts *= 2;
     p->parts = parts;
-    const int rows = g * (int)Lq;
-    p->prologue_lds = (size_t)rows * D * 4 + (size_t)parts * rows * (256 / parts) * 4;
+    p->prologue_lds = 0;
     size_t off = 0;
     p->qrot_off = off; off = align256(off + (size_t)B * Lq * Hq * D * 2);
     p->qlat_off = off; off = align256(off + (size_t)B * Lq * Hq * p->wq * 2);
@@ -880,7 +1129,7 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
     pp.shift = (has_lat && a->up_k_bias) ? shift : nullptr;
     pp.B = B; pp.Lq = Lq; pp.Hq = Hq; pp.Hkv = Hkv; pp.D = D; pp.Rk = Rk; pp.parts = p.parts;
     pp.scale = (float)a->scale;
-    hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), p.prologue_lds, st, pp);
+    hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
     rc = check_hip(hipGetLastError(), "prologue kernel launch");
     if (rc != SLIMKV_OK) return rc;
 
@@ -888,28 +1137,31 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
     prm.B = B; prm.Lq = Lq; prm.Hq = Hq;
     prm.scale_log2 = (float)(a->scale * 1.4426950408889634);
     prm.nseg = has_lat ? 2 : 1;
-    Seg& r = prm.seg[0];
+    // Latent rows (the bulk) are segment 0 so they take the first residency
+    // slots; the short raw segment follows.
+    Seg& r = prm.seg[has_lat ? 1 : 0];
     r.q = q_rot; r.q_sb = (int64_t)Lq * Hq * D; r.q_sl = (int64_t)Hq * D; r.q_sh = D;
     r.k = static_cast<const uint16_t*>(a->raw_k); r.k_sb = a->rk_sb; r.k_sn = a->rk_sn; r.k_sh = a->rk_sh;
     r.v = static_cast<const uint16_t*>(a->raw_v); r.v_sb = a->rv_sb; r.v_sn = a->rv_sn; r.v_sh = a->rv_sh;
     r.seqlens = a->raw_lengths;
     r.n = (int)a->raw_keys;
     r.hk = Hkv; r.g = g; r.wk = D; r.wv = D; r.causal = 0;
-    r.tiles = p.raw.tiles; r.splits = p.raw.splits; r.rows_per_split = p.raw.rows_per_split;
+    r.tiles = p.raw.tiles; r.cols = p.raw.cols; r.splits = p.raw.splits; r.rows_per_split = p.raw.rows_per_split;
     r.part_ml = reinterpret_cast<float*>(ws + p.rml_off);
     r.part_acc = reinterpret_cast<float*>(ws + p.racc_off);
     r.wown = D;
     r.nwg = p.raw.nwg;
-    int kb = 0;
+    int ka = 8, kb = 0;
     if (has_lat) {
-        Seg& l = prm.seg[1];
+        Seg& l = prm.seg[0];
         l.q = q_lat; l.q_sb = (int64_t)Lq * Hq * p.wq; l.q_sl = (int64_t)Hq * p.wq; l.q_sh = p.wq;
         l.k = static_cast<const uint16_t*>(a->lat_k); l.k_sb = a->lk_sb; l.k_sn = a->lk_sn; l.k_sh = 0;
         l.v = static_cast<const uint16_t*>(a->lat_v); l.v_sb = a->lv_sb; l.v_sn = a->lv_sn; l.v_sh = 0;
         l.seqlens = a->lat_lengths;
         l.n = (int)a->lat_keys;
         l.hk = 1; l.g = Hq; l.wk = Rk; l.wv = Rv; l.causal = a->lat_causal ? 1 : 0;
-        l.tiles = p.lat.tiles; l.splits = p.lat.splits; l.rows_per_split = p.lat.rows_per_split;
+        l.tiles = p.lat.tiles; l.cols = p.lat.cols; l.splits = p.lat.splits;
+        l.rows_per_split = p.lat.rows_per_split;
         if (bd) {
             l.blk_heads = g; l.blk_k = Rk / Hkv; l.blk_v = Rv / Hkv; l.q_compact = 1;
         }
@@ -917,17 +1169,18 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
         l.part_acc = reinterpret_cast<float*>(ws + p.lacc_off);
         l.wown = bd ? Rv / Hkv : Rv;
         l.nwg = p.lat.nwg;
-        kb = p.lat.ks;
+        ka = p.lat.ks;
+        kb = 8;
     }
-    const int grid = r.nwg + (has_lat ? prm.seg[1].nwg : 0);
-    rc = check_hip(timed_split(8, kb, prm, grid, st), "split kernel launch");
+    const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
+    rc = check_hip(timed_split(ka, kb, prm, grid, st), "split kernel launch");
     if (rc != SLIMKV_OK) return rc;
 
     CombineParams cp{};
     cp.a_ml = r.part_ml; cp.a_acc = r.part_acc; cp.a_splits = r.splits; cp.a_w = D;
     if (has_lat) {
-        cp.b_ml = prm.seg[1].part_ml; cp.b_acc = prm.seg[1].part_acc;
-        cp.b_splits = prm.seg[1].splits; cp.b_w = prm.seg[1].wown;
+        cp.b_ml = prm.seg[0].part_ml; cp.b_acc = prm.seg[0].part_acc;
+        cp.b_splits = prm.seg[0].splits; cp.b_w = prm.seg[0].wown;
         cp.up_v = static_cast<const uint16_t*>(a->up_v); cp.up_v_ld = Rv;
         cp.up_v_bias = static_cast<const uint16_t*>(a->up_v_bias);
         cp.blockdiag = bd ? 1 : 0;
@@ -936,6 +1189,9 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
     cp.B = B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hkv; cp.D = D;
     cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
     cp.lse = a->lse;
-    hipLaunchKernelGGL(combine_kernel, dim3(B * Hq * Lq), dim3(128), 0, st, cp);
+    if (combine_fast_ok(cp))
+        hipLaunchKernelGGL(combine_fast_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
+    else
+        hipLaunchKernelGGL(combine_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
     return check_hip(hipGetLastError(), "combine kernel launch");
 }
