@@ -124,6 +124,52 @@ int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
                          size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Beacon reconstruction: the up-projection of latent rows to full-dim K or V.
+ * Replaces the up-projection inside ReconstructionCache.materialize
+ *   (slimkv/llama3/memory.py:29-36) and the per-step history rebuild of the
+ *   reconstruction route (tools/benchmark/context_decode_runtime.py:318-332).
+ * out[b, dst(n), h, :] = rope?(bf16(latent[b, n, :] @ W[h*D:(h+1)*D, :]^T + bias[h*D:...]))
+ * latent [B, n, R]; weight [Hkv*D, R] (nn.Linear); bias [Hkv*D] or NULL;
+ * out: 4-D with strides (batch, row, head), last dim contiguous.
+ * dst_rows [n] int64 scatters rows (the window/raw interleave of materialize),
+ * NULL = identity.  positions [B, n] int64 applies bf16-exact RoPE (beacon K
+ * with RoPE, modeling_llama.py:1144-1145), NULL = none.  block_diagonal = 1
+ * contracts each head with its own R/Hkv latent slice only.  head_dim 128.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_reconstruct_args {
+    const void* latent; int64_t l_sb, l_sn;
+    const void* weight; const void* bias;
+    void* out; int64_t o_sb, o_sn, o_sh;
+    const int64_t* dst_rows;
+    const float* cos; const float* sin; int64_t rope_rows;
+    const int64_t* positions; int64_t pos_sb;
+    int64_t batch, rows, rank, kv_heads, head_dim;
+    int32_t block_diagonal;
+} slimkv_reconstruct_args;
+
+int slimkv_reconstruct(const slimkv_reconstruct_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Reconstruction decode for one attention layer: rebuild every beacon's K
+ * (RoPE'd at `beacon_positions` when given) and V from the latents, then one
+ * split-K online softmax over [reconstructed beacons ; raw rows].
+ * Replaces the reconstruction route of LlamaAttention.forward
+ *   (slimkv/llama3/modeling_llama.py:1405-1483) and
+ *   OptimizedDecodeRuntime.reconstruction_attention
+ *   (tools/benchmark/context_decode_runtime.py:298-344).
+ * Argument meaning as slimkv_latent_decode; lat_causal makes the beacon
+ * segment bottom-right causal (the raw query of an insertion step does not
+ * see the new beacon).  The workspace holds the rebuilt K/V.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_recon_decode_args {
+    slimkv_latent_decode_args base;
+    const int64_t* beacon_positions; int64_t bpos_sb;   /* [B, Nl] or NULL */
+} slimkv_recon_decode_args;
+
+size_t slimkv_recon_decode_workspace(const slimkv_recon_decode_args* a);
+int slimkv_recon_decode(const slimkv_recon_decode_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Decode RoPE of the query and the raw K cache, bf16-exact.
  * Replaces decode_ops.fused_rope (slimkv/llama3/decode_ops.py:14-31) and its
  * kernel (slimkv/llama3/decode_kernels.py:7-51).

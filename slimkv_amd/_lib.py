@@ -60,6 +60,22 @@ LatentDecodeArgs = _struct('slimkv_latent_decode_args', [
     ('raw_splits', c_i32), ('lat_splits', c_i32),
 ])
 
+ReconstructArgs = _struct('slimkv_reconstruct_args', [
+    ('latent', c_ptr), *_i64s('l_sb', 'l_sn'),
+    ('weight', c_ptr), ('bias', c_ptr),
+    ('out', c_ptr), *_i64s('o_sb', 'o_sn', 'o_sh'),
+    ('dst_rows', c_ptr),
+    ('cos', c_ptr), ('sin', c_ptr), ('rope_rows', c_i64),
+    ('positions', c_ptr), ('pos_sb', c_i64),
+    *_i64s('batch', 'rows', 'rank', 'kv_heads', 'head_dim'),
+    ('block_diagonal', c_i32),
+])
+
+ReconDecodeArgs = _struct('slimkv_recon_decode_args', [
+    ('base', LatentDecodeArgs),
+    ('beacon_positions', c_ptr), ('bpos_sb', c_i64),
+])
+
 RopeDecodeArgs = _struct('slimkv_rope_decode_args', [
     ('q', c_ptr), *_i64s('q_sb', 'q_sh', 'q_ss'),
     ('k', c_ptr), *_i64s('k_sb', 'k_sh', 'k_ss'),
@@ -99,6 +115,9 @@ SIGNATURES = {
     'slimkv_attention_forward': (ctypes.c_int, [ctypes.POINTER(AttentionArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(LatentDecodeArgs)]),
     'slimkv_latent_decode': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_reconstruct': (ctypes.c_int, [ctypes.POINTER(ReconstructArgs), c_ptr]),
+    'slimkv_recon_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(ReconDecodeArgs)]),
+    'slimkv_recon_decode': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_rope_decode': (ctypes.c_int, [ctypes.POINTER(RopeDecodeArgs), c_ptr]),
     'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
     'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),

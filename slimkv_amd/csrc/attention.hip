@@ -465,7 +465,9 @@ combine_kernel(CombineParams cp) {
     for (int dd = threadIdx.x; dd < cp.D; dd += kCombineThreads) {
         float sum = 0.f;
         for (int s = 0; s < cp.a_splits; ++s) sum += aacc[(int64_t)s * cp.a_w + dd] * wts[s];
-        if (cp.b_splits) {
+        if (cp.b_splits && !cp.up_v) {
+            sum += accb[dd];          // full-dim second segment: no lift
+        } else if (cp.b_splits) {
             const int64_t wrow = (int64_t)h * cp.D + dd;
             const uint16_t* wr = cp.up_v + wrow * cp.up_v_ld + (cp.blockdiag ? h * cp.b_w : 0);
             float lift = 0.f;
@@ -604,6 +606,7 @@ combine_fast_kernel(CombineParams cp) {
 }
 
 bool combine_fast_ok(const CombineParams& cp) {
+    if (cp.b_splits && !cp.up_v) return false;
     return cp.D <= kCombineThreads && cp.a_splits <= kFastRawSplits && cp.a_splits + cp.b_splits <= kCombineThreads &&
            cp.b_w <= kFastLatW && (cp.b_splits == 0 ||
            (kCombineThreads % cp.b_w == 0 && cp.b_splits <= kFastLatPer * (kCombineThreads / cp.b_w)));
@@ -1193,5 +1196,148 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
         hipLaunchKernelGGL(combine_fast_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
     else
         hipLaunchKernelGGL(combine_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
+    return check_hip(hipGetLastError(), "combine kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// reconstruction decode
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct ReconPlan {
+    SegPlan raw, rec;
+    size_t qrot_off, k_off, v_off, rml_off, racc_off, bml_off, bacc_off, total;
+};
+
+int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
+    const slimkv_latent_decode_args* a = &r->base;
+    if (!a->q || !a->raw_k || !a->raw_v || !a->out || !a->up_k || !a->up_v) return fail(SLIMKV_EINVAL, "null tensor pointer");
+    const int64_t B = a->batch, Lq = a->queries, Hq = a->heads, Hkv = a->kv_heads, D = a->head_dim;
+    if (B <= 0 || Lq <= 0 || Lq > 2 || Hq <= 0 || Hkv <= 0 || Hq % Hkv) return fail(SLIMKV_EINVAL, "invalid sizes");
+    if (D != 128) return fail(SLIMKV_EUNSUP, "reconstruction decode is built for head_dim 128");
+    if (a->raw_keys <= 0 || a->lat_keys < 0) return fail(SLIMKV_EINVAL, "invalid key counts");
+    if (a->lat_keys > 0 && (!a->lat_k || !a->lat_v)) return fail(SLIMKV_EINVAL, "null latent pointer");
+    const int g = (int)(Hq / Hkv);
+    if (g * Lq > kMaxRows) return fail(SLIMKV_EUNSUP, "more than 16 query rows per KV head");
+    const int cu = device_cu_count();
+    const int nl = (int)std::max<int64_t>(a->lat_keys, 1);
+    p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, (int)D, a->lat_splits,
+                          cu * split_occupancy(8, 8));
+    const int raw_req = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
+    p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req, 0);
+    size_t off = 0;
+    p->qrot_off = off; off = align256(off + (size_t)B * Lq * Hq * D * 2);
+    p->k_off = off; off = align256(off + (size_t)B * nl * Hkv * D * 2);
+    p->v_off = off; off = align256(off + (size_t)B * nl * Hkv * D * 2);
+    const size_t rr = (size_t)B * Hq * Lq * p->raw.splits;
+    p->rml_off = off; off = align256(off + rr * 8);
+    p->racc_off = off; off = align256(off + rr * D * 4);
+    const size_t br = (size_t)B * Hq * Lq * p->rec.splits;
+    p->bml_off = off; off = align256(off + br * 8);
+    p->bacc_off = off; off = align256(off + br * D * 4);
+    p->total = off;
+    return SLIMKV_OK;
+}
+
+}  // namespace
+
+extern "C" size_t slimkv_recon_decode_workspace(const slimkv_recon_decode_args* r) {
+    ReconPlan p{};
+    if (!r || plan_recon(r, &p) != SLIMKV_OK) return 0;
+    return p.total;
+}
+
+extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    if (!r) return fail(SLIMKV_EINVAL, "null arguments");
+    ReconPlan p{};
+    int rc = plan_recon(r, &p);
+    if (rc != SLIMKV_OK) return rc;
+    if (!workspace || workspace_bytes < p.total) return fail(SLIMKV_EWORKSPACE, "workspace too small");
+    const slimkv_latent_decode_args* a = &r->base;
+    char* ws = static_cast<char*>(workspace);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int B = (int)a->batch, Lq = (int)a->queries, Hq = (int)a->heads, Hkv = (int)a->kv_heads, D = (int)a->head_dim;
+    const int g = Hq / Hkv;
+    const bool has_lat = a->lat_keys > 0;
+    uint16_t* q_rot = reinterpret_cast<uint16_t*>(ws + p.qrot_off);
+    uint16_t* kbuf = reinterpret_cast<uint16_t*>(ws + p.k_off);
+    uint16_t* vbuf = reinterpret_cast<uint16_t*>(ws + p.v_off);
+
+    // 1. query RoPE (no absorption)
+    PrologueParams pp{};
+    pp.q = static_cast<const uint16_t*>(a->q); pp.q_sb = a->q_sb; pp.q_sl = a->q_sl; pp.q_sh = a->q_sh;
+    pp.pos = a->q_positions; pp.pos_sb = a->pos_sb;
+    pp.cos = a->cos; pp.sin = a->sin; pp.rope_rows = a->rope_rows;
+    pp.q_rot = q_rot;
+    pp.wq = 0;
+    pp.B = B; pp.Lq = Lq; pp.Hq = Hq; pp.Hkv = Hkv; pp.D = D; pp.Rk = (int)a->rank_k; pp.parts = 1;
+    pp.scale = (float)a->scale;
+    hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
+    rc = check_hip(hipGetLastError(), "prologue kernel launch");
+    if (rc != SLIMKV_OK) return rc;
+
+    // 2. rebuild beacon K (optionally RoPE'd) and V: [B, Nl, Hkv, D]
+    if (has_lat) {
+        for (int kind = 0; kind < 2; ++kind) {
+            slimkv_reconstruct_args ra{};
+            ra.latent = kind ? a->lat_v : a->lat_k;
+            ra.l_sb = kind ? a->lv_sb : a->lk_sb;
+            ra.l_sn = kind ? a->lv_sn : a->lk_sn;
+            ra.weight = kind ? a->up_v : a->up_k;
+            ra.bias = kind ? a->up_v_bias : a->up_k_bias;
+            ra.out = kind ? (void*)vbuf : (void*)kbuf;
+            ra.o_sb = (int64_t)a->lat_keys * Hkv * D; ra.o_sn = (int64_t)Hkv * D; ra.o_sh = D;
+            if (!kind && r->beacon_positions) {
+                ra.cos = a->cos; ra.sin = a->sin; ra.rope_rows = a->rope_rows;
+                ra.positions = r->beacon_positions; ra.pos_sb = r->bpos_sb;
+            }
+            ra.batch = B; ra.rows = a->lat_keys; ra.rank = kind ? a->rank_v : a->rank_k;
+            ra.kv_heads = Hkv; ra.head_dim = D; ra.block_diagonal = a->block_diagonal;
+            rc = reconstruct(&ra, st);
+            if (rc != SLIMKV_OK) return rc;
+        }
+    }
+
+    // 3. split-K attention over [rebuilt beacons ; raw rows]
+    SplitParams prm{};
+    prm.B = B; prm.Lq = Lq; prm.Hq = Hq;
+    prm.scale_log2 = (float)(a->scale * 1.4426950408889634);
+    prm.nseg = has_lat ? 2 : 1;
+    Seg& rs = prm.seg[has_lat ? 1 : 0];
+    rs.q = q_rot; rs.q_sb = (int64_t)Lq * Hq * D; rs.q_sl = (int64_t)Hq * D; rs.q_sh = D;
+    rs.k = static_cast<const uint16_t*>(a->raw_k); rs.k_sb = a->rk_sb; rs.k_sn = a->rk_sn; rs.k_sh = a->rk_sh;
+    rs.v = static_cast<const uint16_t*>(a->raw_v); rs.v_sb = a->rv_sb; rs.v_sn = a->rv_sn; rs.v_sh = a->rv_sh;
+    rs.seqlens = a->raw_lengths; rs.n = (int)a->raw_keys;
+    rs.hk = Hkv; rs.g = g; rs.wk = D; rs.wv = D; rs.causal = 0;
+    rs.tiles = p.raw.tiles; rs.cols = p.raw.cols; rs.splits = p.raw.splits; rs.rows_per_split = p.raw.rows_per_split;
+    rs.part_ml = reinterpret_cast<float*>(ws + p.rml_off); rs.part_acc = reinterpret_cast<float*>(ws + p.racc_off);
+    rs.wown = D; rs.nwg = p.raw.nwg;
+    if (has_lat) {
+        Seg& bs = prm.seg[0];
+        bs = rs;
+        bs.k = kbuf; bs.k_sb = (int64_t)a->lat_keys * Hkv * D; bs.k_sn = (int64_t)Hkv * D; bs.k_sh = D;
+        bs.v = vbuf; bs.v_sb = bs.k_sb; bs.v_sn = bs.k_sn; bs.v_sh = D;
+        bs.seqlens = a->lat_lengths; bs.n = (int)a->lat_keys; bs.causal = a->lat_causal ? 1 : 0;
+        bs.tiles = p.rec.tiles; bs.cols = p.rec.cols; bs.splits = p.rec.splits; bs.rows_per_split = p.rec.rows_per_split;
+        bs.part_ml = reinterpret_cast<float*>(ws + p.bml_off); bs.part_acc = reinterpret_cast<float*>(ws + p.bacc_off);
+        bs.nwg = p.rec.nwg;
+    }
+    const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
+    rc = check_hip(timed_split(8, has_lat ? 8 : 0, prm, grid, st), "split kernel launch");
+    if (rc != SLIMKV_OK) return rc;
+
+    // 4. merge the two segments
+    CombineParams cp{};
+    cp.a_ml = rs.part_ml; cp.a_acc = rs.part_acc; cp.a_splits = rs.splits; cp.a_w = D;
+    if (has_lat) {
+        cp.b_ml = prm.seg[0].part_ml; cp.b_acc = prm.seg[0].part_acc; cp.b_splits = prm.seg[0].splits; cp.b_w = D;
+        cp.up_v = nullptr;
+    }
+    cp.B = B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hkv; cp.D = D;
+    cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
+    cp.lse = a->lse;
+    hipLaunchKernelGGL(combine_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
     return check_hip(hipGetLastError(), "combine kernel launch");
 }

@@ -65,5 +65,6 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_hip(hipError_t err, const char* what);
 int device_cu_count();
+int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st);
 
 }  // namespace slimkv

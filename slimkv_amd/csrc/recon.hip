@@ -1,0 +1,158 @@
+// Beacon reconstruction (up-projection) on MFMA, with the bias, an optional
+// bf16-exact RoPE epilogue and an optional row scatter.
+//
+// out[b, dst(n), h, :] = rope?(bf16(latent[b, n, :] @ W[h*D:(h+1)*D, :]^T + bias))
+//
+// One wavefront computes a 16-row x 128-feature block of one KV head as
+// C^T[o, n] = W[o, :] . latent[n, :] on v_mfma_f32_16x16x16_bf16: the A operand
+// (W rows) and the B operand (latent rows) are both contiguous along the
+// contraction, so neither needs a transpose, and lane (n, g) ends with features
+// o = 16t + 4g + i of row n for t = 0..7 -- d and d + 64 sit in the same lane,
+// so rotate-half RoPE is applied in registers before the 8-byte stores.
+
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace slimkv {
+
+struct ReconParams {
+    const uint16_t* latent; int64_t l_sb, l_sn;
+    const uint16_t* w; const uint16_t* bias; int64_t w_ld;   // W [Hkv*D, R] row-major
+    uint16_t* out; int64_t o_sb, o_sn, o_sh;
+    const int64_t* dst_rows;                                  // [n] or null (identity)
+    const float* cos; const float* sin; int64_t rope_rows;
+    const int64_t* positions; int64_t pos_sb;                 // [B, n] or null
+    int B, n, R, Hkv, blockdiag, k_lo_step;                   // k_lo_step: per-head latent slice width
+};
+
+constexpr int kReconWaves = 4;
+
+template <int KSTEPS>
+__global__ void __launch_bounds__(kReconWaves * 64)
+recon_kernel(ReconParams p) {
+    constexpr int D = 128;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int tiles = (p.n + 16 * kReconWaves - 1) / (16 * kReconWaves);
+    const int h = blockIdx.x % p.Hkv;
+    const int rt = (blockIdx.x / p.Hkv) % tiles;
+    const int b = blockIdx.x / (p.Hkv * tiles);
+    const int row = (rt * kReconWaves + wave) * 16 + col;
+    const bool rv = row < p.n;
+    const int k_lo = p.blockdiag ? h * p.k_lo_step : 0;
+
+    const uint16_t* lrow = p.latent + (int64_t)b * p.l_sb + (int64_t)(rv ? row : 0) * p.l_sn + k_lo;
+    v4f acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int k = 16 * ks + 4 * grp;
+        u32x2 bl = *reinterpret_cast<const u32x2*>(lrow + k);
+        if (!rv) bl = u32x2{0u, 0u};
+        const v4s bop = as_v4s(bl.x, bl.y);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint16_t* wr = p.w + ((int64_t)h * D + 16 * t + col) * p.w_ld + k_lo + k;
+            const u32x2 al = *reinterpret_cast<const u32x2*>(wr);
+            acc[t] = mfma16(as_v4s(al.x, al.y), bop, acc[t]);
+        }
+    }
+    if (!rv) return;
+    // lane holds x[d] for d = 16t + 4*grp + i
+    float x[8][4];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = 16 * t + 4 * grp + i;
+            float v = acc[t][i];
+            if (p.bias) v += bf16_to_f32(p.bias[(int64_t)h * D + d]);
+            x[t][i] = round_bf16(v);
+        }
+    if (p.positions) {
+        const int64_t pos = clamp_i64(p.positions[(int64_t)b * p.pos_sb + row], 0, p.rope_rows - 1);
+        const float* cr = p.cos + pos * D;
+        const float* sr = p.sin + pos * D;
+        float y[8][4];
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 16 * t + 4 * grp + i;
+                const float partner = t < 4 ? -x[t + 4][i] : x[t - 4][i];
+                y[t][i] = round_bf16(round_bf16(x[t][i] * round_bf16(cr[d])) + round_bf16(partner * round_bf16(sr[d])));
+            }
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[t][i] = y[t][i];
+    }
+    const int64_t dst = p.dst_rows ? p.dst_rows[row] : row;
+    uint16_t* orow = p.out + (int64_t)b * p.o_sb + dst * p.o_sn + (int64_t)h * p.o_sh;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t lo = f32_to_bf16(x[t][0]) | (f32_to_bf16(x[t][1]) << 16);
+        const uint32_t hi = f32_to_bf16(x[t][2]) | (f32_to_bf16(x[t][3]) << 16);
+        *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * grp) = u32x2{lo, hi};
+    }
+}
+
+namespace {
+bool al4(int64_t x) { return (x & 3) == 0; }
+bool pal8(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7) == 0; }
+
+template <int K>
+hipError_t launch_recon(const ReconParams& p, int grid, hipStream_t st) {
+    hipLaunchKernelGGL((recon_kernel<K>), dim3(grid), dim3(kReconWaves * 64), 0, st, p);
+    return hipGetLastError();
+}
+}  // namespace
+
+int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
+    if (!a || !a->latent || !a->weight || !a->out) return fail(SLIMKV_EINVAL, "null pointer");
+    if (a->batch <= 0 || a->rows < 0 || a->rank <= 0 || a->kv_heads <= 0 || a->head_dim != 128)
+        return fail(SLIMKV_EINVAL, "invalid reconstruction sizes (head_dim must be 128)");
+    if (a->rows == 0) return SLIMKV_OK;
+    const bool bd = a->block_diagonal != 0;
+    const int64_t kw = bd ? a->rank / a->kv_heads : a->rank;
+    if ((bd && a->rank % a->kv_heads) || kw % 16 || kw > 512)
+        return fail(SLIMKV_EUNSUP, "the contracted latent width must be a multiple of 16 up to 512");
+    const int64_t strides[] = {a->l_sb, a->l_sn, a->o_sb, a->o_sn, a->o_sh, a->rank};
+    for (int64_t s : strides)
+        if (!al4(s)) return fail(SLIMKV_EINVAL, "strides must be multiples of 4 elements");
+    if (!pal8(a->latent) || !pal8(a->weight) || !pal8(a->out)) return fail(SLIMKV_EINVAL, "tensors must be 8-byte aligned");
+    if (a->positions && (!a->cos || !a->sin || a->rope_rows <= 0)) return fail(SLIMKV_EINVAL, "RoPE needs tables");
+    ReconParams p{};
+    p.latent = static_cast<const uint16_t*>(a->latent); p.l_sb = a->l_sb; p.l_sn = a->l_sn;
+    p.w = static_cast<const uint16_t*>(a->weight); p.bias = static_cast<const uint16_t*>(a->bias); p.w_ld = a->rank;
+    p.out = static_cast<uint16_t*>(a->out); p.o_sb = a->o_sb; p.o_sn = a->o_sn; p.o_sh = a->o_sh;
+    p.dst_rows = a->dst_rows;
+    p.cos = a->cos; p.sin = a->sin; p.rope_rows = a->rope_rows;
+    p.positions = a->positions; p.pos_sb = a->pos_sb;
+    p.B = (int)a->batch; p.n = (int)a->rows; p.R = (int)a->rank; p.Hkv = (int)a->kv_heads;
+    p.blockdiag = bd ? 1 : 0; p.k_lo_step = (int)kw;
+    const int tiles = (p.n + 16 * kReconWaves - 1) / (16 * kReconWaves);
+    const int grid = p.B * tiles * p.Hkv;
+    hipError_t e;
+    switch (kw / 16) {
+        case 1: e = launch_recon<1>(p, grid, st); break;
+        case 2: e = launch_recon<2>(p, grid, st); break;
+        case 3: e = launch_recon<3>(p, grid, st); break;
+        case 4: e = launch_recon<4>(p, grid, st); break;
+        case 8: e = launch_recon<8>(p, grid, st); break;
+        case 12: e = launch_recon<12>(p, grid, st); break;
+        case 16: e = launch_recon<16>(p, grid, st); break;
+        case 24: e = launch_recon<24>(p, grid, st); break;
+        case 32: e = launch_recon<32>(p, grid, st); break;
+        default: return fail(SLIMKV_EUNSUP, "latent width not instantiated");
+    }
+    return check_hip(e, "reconstruction kernel launch");
+}
+
+}  // namespace slimkv
+
+extern "C" int slimkv_reconstruct(const slimkv_reconstruct_args* a, void* stream) {
+    return slimkv::reconstruct(a, static_cast<hipStream_t>(stream));
+}

@@ -159,6 +159,57 @@ def latent_decode_workspace_bytes(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, sca
     return nbytes
 
 
+def reconstruct(latent, weight, bias=None, *, kv_heads, out=None, dst_rows=None, positions=None, cos=None,
+                sin=None, block_diagonal=False):
+    """Up-project latent rows [B, n, R] with an nn.Linear weight [Hkv*D, R] into
+    out [B, rows, Hkv, D] (any 4-D view with a contiguous last dim), optionally
+    scattered to dst_rows and RoPE'd at positions [B, n]."""
+    _need_device(latent, weight, bias, out)
+    _need_bf16(latent, weight, bias, out)
+    latent = _last_contiguous(latent)
+    weight = weight.contiguous()
+    B, n, R = latent.shape
+    D = weight.shape[0] // kv_heads
+    if out is None:
+        out = torch.empty(B, n, kv_heads, D, dtype=BF16, device=latent.device)
+    if dst_rows is not None:
+        dst_rows = dst_rows.to(device=latent.device, dtype=torch.int64).contiguous()
+    if positions is not None:
+        positions = positions.to(torch.int64)
+        positions = positions if positions.stride(-1) == 1 else positions.contiguous()
+    a = _lib.ReconstructArgs(
+        _ptr(latent), latent.stride(0), latent.stride(1), _ptr(weight), _ptr(bias),
+        _ptr(out), out.stride(0), out.stride(1), out.stride(2), _ptr(dst_rows),
+        _ptr(cos), _ptr(sin), 0 if cos is None else cos.shape[0],
+        _ptr(positions), 0 if positions is None else positions.stride(0),
+        B, n, R, kv_heads, D, int(bool(block_diagonal)))
+    check(lib().slimkv_reconstruct(ctypes.byref(a), _lib.stream_handle(latent.device)))
+    return out
+
+
+def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_positions=None, up_k_bias=None,
+                 up_v_bias=None, block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
+                 raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None, workspace=None):
+    """Reconstruction decode: rebuild beacon K (RoPE'd at beacon_positions
+    [B, Nl] when given) and V, then attend over [beacons ; raw rows]."""
+    base, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
+                                        block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
+                                        lat_lengths, raw_splits, lat_splits, out, lse)
+    if beacon_positions is not None:
+        beacon_positions = beacon_positions.to(torch.int64)
+        beacon_positions = beacon_positions if beacon_positions.stride(-1) == 1 else beacon_positions.contiguous()
+    a = _lib.ReconDecodeArgs(base, _ptr(beacon_positions),
+                             0 if beacon_positions is None else beacon_positions.stride(0))
+    nbytes = lib().slimkv_recon_decode_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = _workspace(nbytes, q.device)
+    check(lib().slimkv_recon_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    del keep
+    return out, lse
+
+
 def rope_decode(q, k, cos, sin, query_positions, raw_indices, sink, history):
     """q [B,Hq,Lq,D], k [B,Hk,Nk,D] (BHSD); returns new contiguous (oq, ok)."""
     _need_device(q, k, cos, sin, query_positions)

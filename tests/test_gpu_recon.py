@@ -1,0 +1,167 @@
+"""Reconstruction path: the MFMA up-projection (ReconstructionCache.materialize,
+slimkv/llama3/memory.py:26-48) and the reconstruction decode (LlamaAttention
+.forward after materialize, slimkv/llama3/modeling_llama.py:1405-1483).
+
+Up-projection: bf16 output of an fp32-accumulated GEMM, compared with the
+oracle's float64 GEMM rounded once to bf16 -- every element within one bf16
+ulp (the summation order differs), almost all identical.  Decode: within the
+bf16 bar (max abs 2e-2, mean 2e-3) of both the oracle's float64 attention and
+its restatement of the reference eager path with bf16 score/probability
+roundings.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import rope as orope
+from oracle.bf16 import round_bf16
+from slimkv_amd.workloads import block_diagonal, latent_case, orthonormal_columns, rope_tables
+from tests.helpers import assert_close, assert_lse_close, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _neighbour_of_exact(actual, exact, rounded, abs_terms):
+    """Every bf16 output is one of the two bf16 neighbours of the float64 GEMM
+    result up to the fp32 accumulation error (any fp32-accumulating GEMM -- this
+    kernel or hipBLASLt -- can land on either side of a near-tie, and near a
+    cancellation the error is absolute), and almost all equal its correct
+    rounding.  abs_terms: the GEMM of absolute values (sum |w||x|)."""
+    a, x = np.asarray(actual, np.float64), np.asarray(exact, np.float64)
+    mag = np.maximum(np.abs(x), 1e-30)
+    ulp = 2.0 ** (np.floor(np.log2(mag)) - 7)
+    accumulation = np.asarray(abs_terms, np.float64) * 2.0 ** -20
+    err = np.abs(a - x)
+    bad = err >= ulp * 1.0001 + accumulation
+    assert not bad.any(), list(zip(a[bad][:4], x[bad][:4]))
+    assert (a == np.asarray(rounded, np.float64)).mean() > 0.98
+
+
+@pytest.mark.parametrize('bd,rank,bias', [(True, 32, False), (True, 48, True), (False, 256, True), (True, 16, False)])
+def test_reconstruct_matches_oracle_gemm(device, bd, rank, bias):
+    from slimkv_amd import kernels
+    gen = torch.Generator(device=device).manual_seed(rank)
+    B, n, Hkv, D = 2, 203, 8, 128
+    R = Hkv * rank if bd else rank
+    lat = torch.randn(B, n, R, generator=gen, device=device).to(torch.bfloat16)
+    if bd:
+        w = block_diagonal([orthonormal_columns(D, rank, torch.Generator().manual_seed(i)) for i in range(Hkv)])
+        w = w.to(device, torch.bfloat16)
+    else:
+        w = (torch.randn(Hkv * D, R, generator=gen, device=device) / R ** 0.5).to(torch.bfloat16)
+    b = torch.randn(Hkv * D, generator=gen, device=device).to(torch.bfloat16) if bias else None
+    out = kernels.reconstruct(lat, w, b, kv_heads=Hkv, block_diagonal=bd)
+    torch.cuda.synchronize()
+    bias_np = None if b is None else to_np(b)
+    exact = oa.reconstruct(to_np(lat)[:, None], to_np(w), bias_np, Hkv, D, bf16_boundaries=False)
+    rounded = oa.reconstruct(to_np(lat)[:, None], to_np(w), bias_np, Hkv, D)
+    abs_terms = oa.reconstruct(np.abs(to_np(lat))[:, None], np.abs(to_np(w)), None, Hkv, D, bf16_boundaries=False)
+    _neighbour_of_exact(to_np(out).transpose(0, 2, 1, 3), exact, rounded, abs_terms)
+
+
+def test_reconstruct_scatter_and_rope_epilogue(device):
+    from slimkv_amd import kernels
+    gen = torch.Generator(device=device).manual_seed(7)
+    B, n, Hkv, D, r = 2, 37, 8, 128, 32
+    lat = torch.randn(B, n, Hkv * r, generator=gen, device=device).to(torch.bfloat16)
+    w = block_diagonal([orthonormal_columns(D, r, torch.Generator().manual_seed(10 + i)) for i in range(Hkv)])
+    w = w.to(device, torch.bfloat16)
+    cos, sin = rope_tables(5000, D, 500000.0, device)
+    pos = torch.randint(0, 5000, (B, n), generator=gen, device=device)
+    dst = torch.randperm(n + 5, generator=torch.Generator().manual_seed(3))[:n].to(device)
+    out = torch.zeros(B, n + 5, Hkv, D, dtype=torch.bfloat16, device=device)
+    kernels.reconstruct(lat, w, kv_heads=Hkv, out=out, dst_rows=dst, positions=pos, cos=cos, sin=sin,
+                        block_diagonal=True)
+    plain = kernels.reconstruct(lat, w, kv_heads=Hkv, block_diagonal=True)
+    torch.cuda.synchronize()
+    # RoPE epilogue is bit-exact given the bf16 reconstruction the kernel itself produced
+    x = to_np(plain).astype(np.float32)                              # [B, n, Hkv, D]
+    c, s = to_np(cos).astype(np.float32), to_np(sin).astype(np.float32)
+    p = pos.cpu().numpy()
+    rot = np.stack([orope.rotate_bf16(x[bb], c[p[bb]][:, None], s[p[bb]][:, None]) for bb in range(B)])
+    got = to_np(out)[:, dst.cpu().numpy()]
+    np.testing.assert_array_equal(got, rot)
+    untouched = np.setdiff1d(np.arange(n + 5), dst.cpu().numpy())
+    assert (to_np(out)[:, untouched] == 0).all()
+
+
+def _recon_oracles(case, q_rot, k_rot, beacon_pos, lat_causal, bk=None, bv=None):
+    """Float64 attention over [rebuilt beacons ; raw rows] and the reference
+    eager formulation with bf16 scores/probabilities."""
+    Hkv, D = case.kv_heads, 128
+    rk = oa.reconstruct(to_np(case.lat_k)[:, None], to_np(case.up_k), None if bk is None else to_np(bk), Hkv, D)
+    rv = oa.reconstruct(to_np(case.lat_v)[:, None], to_np(case.up_v), None if bv is None else to_np(bv), Hkv, D)
+    if beacon_pos is not None:
+        c, s = to_np(case.cos).astype(np.float32), to_np(case.sin).astype(np.float32)
+        bp = beacon_pos.cpu().numpy()
+        rk = np.stack([orope.rotate_bf16(rk[b].astype(np.float32), c[bp[b]][None], s[bp[b]][None])
+                       for b in range(rk.shape[0])]).astype(np.float64)
+    raw_k, raw_v = to_np(k_rot), to_np(case.raw_v.transpose(1, 2))
+    q = to_np(q_rot)                                                  # [B, H, L, D]
+    B, H, L, _ = q.shape
+    nl = rk.shape[2]
+    exact = np.empty((B, H, L, D))
+    eager = np.empty((B, H, L, D))
+    lse = np.empty((B, H, L))
+    for i in range(L):
+        vis = nl - L + i + 1 if lat_causal else nl
+        k = np.concatenate([rk[:, :, :vis], raw_k], axis=2)
+        v = np.concatenate([rv[:, :, :vis], raw_v], axis=2)
+        o, l = oa.eager_forward(q[:, :, i:i + 1].transpose(0, 2, 1, 3), k.transpose(0, 2, 1, 3),
+                                v.transpose(0, 2, 1, 3), case.scale)
+        exact[:, :, i], lse[:, :, i] = o[:, 0], l[:, :, 0]
+        e, _ = oa.eager_recon_layer(q[:, :, i:i + 1], k, v, case.scale)
+        eager[:, :, i] = e[:, :, 0]
+    return exact, eager, lse
+
+
+def _rotate(case):
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import decode_rope_layout
+    raw_idx, history = decode_rope_layout(case)
+    return kernels.rope_decode(case.q.transpose(1, 2), case.raw_k.transpose(1, 2), case.cos, case.sin,
+                               case.q_positions, raw_idx, case.sinks, history)
+
+
+@pytest.mark.parametrize('beacon_rope', [True, False])
+def test_recon_decode_qwen14b_layer_shape(device, beacon_rope):
+    """Qwen2.5-14B attention layer shape: 40 query / 8 KV heads (GQA 5), r 32,
+    4 sinks + 128 tail, K-RoPE on the rebuilt beacons at their slot positions."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=4, heads=40, context=4096 + 132, tail=128, seed=31, device=device)
+    q_rot, k_rot = _rotate(case)
+    nl = case.lat_k.shape[1]
+    bpos = (torch.arange(nl, device=device) * 4 + 4)[None].expand(4, -1).contiguous() if beacon_rope else None
+    out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                    case.up_v, case.scale, beacon_positions=bpos, block_diagonal=True,
+                                    q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    torch.cuda.synchronize()
+    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, False)
+    got = to_np(out.transpose(1, 2))
+    assert_close(got, exact, what='vs float64')
+    assert_close(got, eager, what='vs bf16 eager')
+    assert_lse_close(to_np(lse), lse_e)
+
+
+def test_recon_decode_insertion_step_with_biases_general_weights(device):
+    from slimkv_amd import kernels
+    case = latent_case(batch=2, context=900, tail=40, seed=5, device=device)
+    gen = torch.Generator(device=device).manual_seed(6)
+    case.up_k = (torch.randn(1024, 256, generator=gen, device=device) / 16).to(torch.bfloat16)
+    case.up_v = (torch.randn(1024, 256, generator=gen, device=device) / 16).to(torch.bfloat16)
+    bk = (0.3 * torch.randn(1024, generator=gen, device=device)).to(torch.bfloat16)
+    bv = (0.3 * torch.randn(1024, generator=gen, device=device)).to(torch.bfloat16)
+    case.q = torch.randn(2, 2, 32, 128, generator=gen, device=device).to(torch.bfloat16)
+    case.q_positions = torch.tensor([[900, 901]] * 2, device=device)
+    case.cos, case.sin = rope_tables(902, 128, 500000.0, device)
+    q_rot, k_rot = _rotate(case)
+    out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                    case.up_v, case.scale, up_k_bias=bk, up_v_bias=bv, lat_causal=True,
+                                    q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    torch.cuda.synchronize()
+    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, None, True, bk, bv)
+    got = to_np(out.transpose(1, 2))
+    assert_close(got, exact)
+    assert_close(got, eager)
+    assert_lse_close(to_np(lse), lse_e)
