@@ -232,6 +232,60 @@ typedef struct slimkv_merge_args {
 
 int slimkv_merge(const slimkv_merge_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Beacon-page I/O: exact bf16 copies between engine-owned pages and dense
+ * latent rows, for `batch` requests at once.
+ * Replaces BeaconPages._indices/read/append (slimkv/vllm_plugin/paged_cache.py:60-87)
+ * with the layout of BeaconPageLayout (paged_cache.py:11-44).
+ * pages: bf16 [num_pages, page_stride] (each page's features contiguous).
+ * Logical beacon i of request b lives in physical page
+ *   p = table[b*t_sb + i / slots]
+ * at columns sink_elements + (i % slots)*(key_rank + value_rank) + [0, key_rank)
+ * (K latent), followed by [key_rank, key_rank + value_rank) (V latent).
+ * Beacons start .. start+count-1 map to dense row i - start:
+ *   K at dense_k[b*dk_sb + (i-start)*dk_sn + c], V likewise.
+ * lengths: optional device int32 [batch]; request b moves only beacons
+ * i < lengths[b] (the rest of its dense rows and pages are untouched).
+ * A table entry outside [0, num_pages) moves nothing for its rows.
+ * to_pages = 1 appends (dense -> pages), 0 reads (pages -> dense).
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_beacon_pages_args {
+    void* pages; int64_t num_pages, page_stride;
+    const int64_t* table; int64_t t_sb;
+    void* dense_k; int64_t dk_sb, dk_sn;
+    void* dense_v; int64_t dv_sb, dv_sn;
+    const int32_t* lengths;
+    int64_t batch, start, count;
+    int64_t slots, key_rank, value_rank, sink_elements;
+    int32_t to_pages;
+} slimkv_beacon_pages_args;
+
+int slimkv_beacon_pages(const slimkv_beacon_pages_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Raw-page I/O: exact bf16 copies between raw KV blocks and dense K/V.
+ * Replaces RawPages.read/write (slimkv/vllm_plugin/paged_cache.py:102-127).
+ * pages: bf16 [blocks, block_size, 2, kv_heads, head_dim] with strides
+ * (p_sblk, p_stok, p_skind, p_sh, 1).  Token position t of request b lives in
+ * block table[b*t_sb + t / block_size], row t % block_size; positions
+ * start .. start+count-1 map to dense row t - start:
+ *   K at dense_k[b*dk_sb + h*dk_sh + (t-start)*dk_sn + d], V likewise.
+ * lengths: optional device int32 [batch] token counts (positions >= lengths[b]
+ * are skipped).  A table entry outside [0, num_blocks) moves nothing.
+ * to_pages = 1 writes, 0 reads.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_raw_pages_args {
+    void* pages; int64_t num_blocks, p_sblk, p_stok, p_skind, p_sh;
+    const int64_t* table; int64_t t_sb;
+    void* dense_k; int64_t dk_sb, dk_sh, dk_sn;
+    void* dense_v; int64_t dv_sb, dv_sh, dv_sn;
+    const int32_t* lengths;
+    int64_t batch, start, count, block_size, kv_heads, head_dim;
+    int32_t to_pages;
+} slimkv_raw_pages_args;
+
+int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -106,6 +106,26 @@ MergeArgs = _struct('slimkv_merge_args', [
     *_i64s('batch', 'heads', 'length', 'dim'),
 ])
 
+BeaconPagesArgs = _struct('slimkv_beacon_pages_args', [
+    ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
+    ('table', c_ptr), ('t_sb', c_i64),
+    ('dense_k', c_ptr), *_i64s('dk_sb', 'dk_sn'),
+    ('dense_v', c_ptr), *_i64s('dv_sb', 'dv_sn'),
+    ('lengths', c_ptr),
+    *_i64s('batch', 'start', 'count', 'slots', 'key_rank', 'value_rank', 'sink_elements'),
+    ('to_pages', c_i32),
+])
+
+RawPagesArgs = _struct('slimkv_raw_pages_args', [
+    ('pages', c_ptr), *_i64s('num_blocks', 'p_sblk', 'p_stok', 'p_skind', 'p_sh'),
+    ('table', c_ptr), ('t_sb', c_i64),
+    ('dense_k', c_ptr), *_i64s('dk_sb', 'dk_sh', 'dk_sn'),
+    ('dense_v', c_ptr), *_i64s('dv_sb', 'dv_sh', 'dv_sn'),
+    ('lengths', c_ptr),
+    *_i64s('batch', 'start', 'count', 'block_size', 'kv_heads', 'head_dim'),
+    ('to_pages', c_i32),
+])
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     'slimkv_last_error': (ctypes.c_char_p, []),
@@ -121,6 +141,8 @@ SIGNATURES = {
     'slimkv_rope_decode': (ctypes.c_int, [ctypes.POINTER(RopeDecodeArgs), c_ptr]),
     'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
     'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),
+    'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
+    'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
 ABI_VERSION = 1

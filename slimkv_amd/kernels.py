@@ -267,3 +267,76 @@ def merge(raw, raw_lse, latent, latent_lse):
 
 def default_scale(head_dim):
     return 1.0 / math.sqrt(head_dim)
+
+
+def _table(table, device):
+    """Block table as device int64 [B, T] (a 1-D table is one request)."""
+    table = table.to(device=device, dtype=torch.long)
+    if table.dim() == 1:
+        table = table[None]
+    if table.dim() != 2 or table.stride(1) != 1:
+        table = table.reshape(table.shape[0], -1).contiguous()
+    return table
+
+
+def _lengths(lengths, batch, device):
+    if lengths is None:
+        return None
+    lengths = lengths.to(device=device, dtype=torch.int32).contiguous()
+    if lengths.shape != (batch,):
+        raise ValueError('lengths must be [batch]')
+    return lengths
+
+
+def beacon_pages(pages, table, dense_k, dense_v, *, slots, key_rank, value_rank, sink_elements, start, count,
+                 to_pages, lengths=None):
+    """Copy beacon latents between pages [num_pages, >=page_elements] and dense
+    rows dense_k [B, count, key_rank], dense_v [B, count, value_rank]
+    (slimkv/vllm_plugin/paged_cache.py:60-87).  table: [B, T] or [T] int64."""
+    _need_device(pages, dense_k, dense_v)
+    _need_bf16(pages, dense_k, dense_v)
+    if pages.dim() != 2 or pages.stride(1) != 1:
+        raise ValueError('pages must be [num_pages, features] with contiguous features')
+    table = _table(table, pages.device)
+    B = table.shape[0]
+    for t, w in ((dense_k, key_rank), (dense_v, value_rank)):
+        if t.dim() != 3 or t.shape != (B, count, w) or t.stride(2) != 1:
+            raise ValueError(f'dense latents must be [{B}, {count}, {w}] with contiguous rows')
+    if table.shape[1] * slots < start + count:
+        raise ValueError('block table does not cover the requested beacons')
+    lengths = _lengths(lengths, B, pages.device)
+    a = _lib.BeaconPagesArgs(
+        pages=_ptr(pages), num_pages=pages.shape[0], page_stride=pages.stride(0),
+        table=_ptr(table), t_sb=table.stride(0),
+        dense_k=_ptr(dense_k), dk_sb=dense_k.stride(0), dk_sn=dense_k.stride(1),
+        dense_v=_ptr(dense_v), dv_sb=dense_v.stride(0), dv_sn=dense_v.stride(1),
+        lengths=_ptr(lengths), batch=B, start=start, count=count, slots=slots, key_rank=key_rank,
+        value_rank=value_rank, sink_elements=sink_elements, to_pages=int(bool(to_pages)))
+    check(lib().slimkv_beacon_pages(ctypes.byref(a), _lib.stream_handle(pages.device)))
+
+
+def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths=None):
+    """Copy raw K/V between pages [blocks, block_size, 2, Hkv, D] and dense
+    dense_k/dense_v [B, Hkv, count, D] (slimkv/vllm_plugin/paged_cache.py:102-127)."""
+    _need_device(pages, dense_k, dense_v)
+    _need_bf16(pages, dense_k, dense_v)
+    if pages.dim() != 5 or pages.shape[2] != 2 or pages.stride(4) != 1:
+        raise ValueError('pages must be [blocks, block_size, 2, heads, dim] with contiguous dim')
+    table = _table(table, pages.device)
+    B = table.shape[0]
+    _, block_size, _, H, D = pages.shape
+    for t in (dense_k, dense_v):
+        if t.dim() != 4 or t.shape != (B, H, count, D) or t.stride(3) != 1:
+            raise ValueError(f'dense K/V must be [{B}, {H}, {count}, {D}] with contiguous rows')
+    if table.shape[1] * block_size < start + count:
+        raise ValueError('block table does not cover the requested tokens')
+    lengths = _lengths(lengths, B, pages.device)
+    a = _lib.RawPagesArgs(
+        pages=_ptr(pages), num_blocks=pages.shape[0], p_sblk=pages.stride(0), p_stok=pages.stride(1),
+        p_skind=pages.stride(2), p_sh=pages.stride(3),
+        table=_ptr(table), t_sb=table.stride(0),
+        dense_k=_ptr(dense_k), dk_sb=dense_k.stride(0), dk_sh=dense_k.stride(1), dk_sn=dense_k.stride(2),
+        dense_v=_ptr(dense_v), dv_sb=dense_v.stride(0), dv_sh=dense_v.stride(1), dv_sn=dense_v.stride(2),
+        lengths=_ptr(lengths), batch=B, start=start, count=count, block_size=block_size, kv_heads=H,
+        head_dim=D, to_pages=int(bool(to_pages)))
+    check(lib().slimkv_raw_pages(ctypes.byref(a), _lib.stream_handle(pages.device)))

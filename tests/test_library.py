@@ -30,16 +30,47 @@ def test_library_exports_every_declared_symbol():
         assert name in _lib.SIGNATURES, f'{name} has no ctypes signature'
 
 
+def STRUCTS(_lib):
+    return (_lib.AttentionArgs, _lib.LatentDecodeArgs, _lib.ReconstructArgs, _lib.ReconDecodeArgs,
+            _lib.RopeDecodeArgs, _lib.PrefillRopeArgs, _lib.MergeArgs, _lib.BeaconPagesArgs, _lib.RawPagesArgs)
+
+
 def test_struct_layouts_match_header_field_order():
     """ctypes mirrors list the header's fields in order with matching widths."""
     from slimkv_amd import _lib
     header = (ROOT / 'include' / 'slimkv_hip.h').read_text()
-    for struct in (_lib.AttentionArgs, _lib.LatentDecodeArgs, _lib.RopeDecodeArgs,
-                   _lib.PrefillRopeArgs, _lib.MergeArgs):
+    for struct in STRUCTS(_lib):
         body = re.search(r'typedef struct %s \{(.*?)\}' % struct.__name__, header, re.S).group(1)
         body = re.sub(r'/\*.*?\*/', '', body)
         fields = re.findall(r'\*?\s*([a-z_][a-z0-9_]*)\s*(?=[,;])', body)
         assert fields == [f[0] for f in struct._fields_], struct.__name__
+
+
+def test_struct_offsets_match_the_c_compiler(tmp_path):
+    """sizeof and every offsetof of each argument struct, as gcc lays out the
+    header, equal the ctypes mirror's."""
+    import shutil
+    import subprocess
+    from slimkv_amd import _lib
+    if shutil.which('gcc') is None:
+        pytest.skip('gcc not available')
+    lines = []
+    for struct in STRUCTS(_lib):
+        name = struct.__name__
+        lines.append(f'printf("%s size %zu\\n", "{name}", sizeof({name}));')
+        for field, _ in struct._fields_:
+            lines.append(f'printf("%s %s %zu\\n", "{name}", "{field}", offsetof({name}, {field}));')
+    src = tmp_path / 'layout.c'
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "slimkv_hip.h"\nint main(void){\n' +
+                   '\n'.join(lines) + '\nreturn 0;}\n')
+    exe = tmp_path / 'layout'
+    subprocess.run(['gcc', '-I', str(ROOT / 'include'), str(src), '-o', str(exe)], check=True)
+    got = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split('\n')
+    want = []
+    for struct in STRUCTS(_lib):
+        want.append(f'{struct.__name__} size {ctypes.sizeof(struct)}')
+        want += [f'{struct.__name__} {f} {getattr(struct, f).offset}' for f, _ in struct._fields_]
+    assert got[:-1] == want
 
 
 def test_errors_are_reported_without_a_gpu():
