@@ -233,6 +233,31 @@ typedef struct slimkv_merge_args {
 int slimkv_merge(const slimkv_merge_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Prefill attention: causal (bottom-right aligned) GQA attention over a full
+ * window, head_dim 128, bf16 in/out, fp32 accumulation and softmax.
+ * Replaces the flash_attn_func call of LlamaFlashAttention2._flash_attention_forward
+ * (slimkv/llama3/modeling_llama.py:1752-1809) made by the prefill forward
+ * (modeling_llama.py:1632-1750) over [sink | up(history) | window | current].
+ * q [B, Lq, Hq, 128]  k, v [B, Nk, Hk, 128]  out [B, Lq, Hq, 128] (BSHD);
+ * lse [B, Hq, Lq] fp32 contiguous (may be NULL).  With `causal` query i sees
+ * keys [0, n_b - Lq + i] where n_b = seqlens_k ? seqlens_k[b] : keys; a row
+ * that sees no key gets output 0 and LSE -inf.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_prefill_attention_args {
+    const void* q; int64_t q_sb, q_sl, q_sh;
+    const void* k; int64_t k_sb, k_sn, k_sh;
+    const void* v; int64_t v_sb, v_sn, v_sh;
+    void* out; int64_t o_sb, o_sl, o_sh;
+    float* lse;
+    const int32_t* seqlens_k;
+    int64_t batch, queries, heads, kv_heads, keys, head_dim;
+    double scale;
+    int32_t causal;
+} slimkv_prefill_attention_args;
+
+int slimkv_prefill_attention(const slimkv_prefill_attention_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
  * Beacon-page I/O: exact bf16 copies between engine-owned pages and dense
  * latent rows, for `batch` requests at once.
  * Replaces BeaconPages._indices/read/append (slimkv/vllm_plugin/paged_cache.py:60-87)

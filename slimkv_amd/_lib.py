@@ -106,6 +106,18 @@ MergeArgs = _struct('slimkv_merge_args', [
     *_i64s('batch', 'heads', 'length', 'dim'),
 ])
 
+PrefillAttentionArgs = _struct('slimkv_prefill_attention_args', [
+    ('q', c_ptr), *_i64s('q_sb', 'q_sl', 'q_sh'),
+    ('k', c_ptr), *_i64s('k_sb', 'k_sn', 'k_sh'),
+    ('v', c_ptr), *_i64s('v_sb', 'v_sn', 'v_sh'),
+    ('out', c_ptr), *_i64s('o_sb', 'o_sl', 'o_sh'),
+    ('lse', c_ptr),
+    ('seqlens_k', c_ptr),
+    *_i64s('batch', 'queries', 'heads', 'kv_heads', 'keys', 'head_dim'),
+    ('scale', c_f64),
+    ('causal', c_i32),
+])
+
 BeaconPagesArgs = _struct('slimkv_beacon_pages_args', [
     ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
     ('table', c_ptr), ('t_sb', c_i64),
@@ -141,6 +153,7 @@ SIGNATURES = {
     'slimkv_rope_decode': (ctypes.c_int, [ctypes.POINTER(RopeDecodeArgs), c_ptr]),
     'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
     'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),
+    'slimkv_prefill_attention': (ctypes.c_int, [ctypes.POINTER(PrefillAttentionArgs), c_ptr]),
     'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }

@@ -1,0 +1,301 @@
+// Prefill attention for gfx950: causal (bottom-right aligned) GQA flash
+// attention over a whole window, head_dim 128, bf16 operands on the
+// 16x16x32 bf16 MFMA with fp32 accumulation and an fp32 online softmax.
+//
+// Semantics: flash_attn_func(q, k, v, causal=True) as called by
+// LlamaFlashAttention2._flash_attention_forward (slimkv/llama3/modeling_llama.py:1752-1809).
+//
+// Work split.  A workgroup is 4 waves and owns 128 query rows of one head;
+// each wave owns 32 rows (two 16-column MFMA tiles).  Keys stream through LDS
+// in tiles of 64: K row-major ([key][d]) and V transposed ([d][key]), both
+// prefetched into registers one tile ahead so global latency hides under the
+// current tile's MFMAs.
+//
+// Layouts (lane l, col = l % 16, grp = l / 16; the 16x16x32 MFMA takes
+// A[col][8*grp + j], B[8*grp + j][col] and returns D[4*grp + i][col]):
+//   S^T = K . Q^T   A = K rows from LDS (8 contiguous d), B = Q rows held in
+//                   registers for the whole loop; lane owns query column col.
+//   O^T = V^T . P^T P^T comes straight from S^T's accumulator layout with the
+//                   contraction order of the 32 keys of a step permuted to
+//                   (4*grp + j | 16 + 4*grp + j); V^T is read from LDS in the
+//                   same order (two 8-byte reads).  The query stays in the
+//                   lane, so softmax statistics never cross lanes except for
+//                   the two-step max/sum over grp.
+//
+// Scheduling.  Workgroups sharing a KV head (the g query heads of one group
+// for one query block) are placed on the same XCD so the group's K/V tiles
+// are fetched into that XCD's L2 once; groups are issued longest-first (the
+// last query block sees the most keys under the causal mask).
+
+#include "common.hpp"
+
+namespace slimkv {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v4f mfma32(u32x4 a, u32x4 b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+constexpr int kD = 128;                  // head dim
+constexpr int kQRows = 128;              // query rows per workgroup
+constexpr int kKeys = 64;                // keys per tile
+constexpr int kKStride = kD + 8;         // K tile row (bf16), 272 B
+constexpr int kVStride = kKeys + 4;      // V^T tile row (bf16), 136 B
+constexpr int kXcds = 8;
+
+struct PrefillParams {
+    const uint16_t* q; int64_t q_sb, q_sl, q_sh;
+    const uint16_t* k; int64_t k_sb, k_sn, k_sh;
+    const uint16_t* v; int64_t v_sb, v_sn, v_sh;
+    uint16_t* out; int64_t o_sb, o_sl, o_sh;
+    float* lse;
+    const int32_t* seqlens;
+    int B, Lq, Hq, Hk, Nk, causal;
+    int qblocks;
+    float scale_log2;
+};
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+__device__ __forceinline__ uint32_t half_of(const u32x4& v, int e) {
+    const uint32_t w = v[e >> 1];
+    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+struct TileRegs {
+    u32x4 k[4];     // 4 x 16 B of K: pieces threadIdx.x + 256 r -> (row p/16, d-piece p%16)
+    u32x4 v[4];     // 4 keys (4*kq + r) x 8 d (d-piece cp) of V
+};
+
+__device__ __forceinline__ void load_tile(TileRegs& t, const uint16_t* kb, const uint16_t* vb, int64_t k_sn,
+                                          int64_t v_sn, int k0, int n) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int p = tid + 256 * r;
+        const int key = min(k0 + (p >> 4), n - 1);
+        t.k[r] = *reinterpret_cast<const u32x4*>(kb + (int64_t)key * k_sn + 8 * (p & 15));
+    }
+    const int kq = tid & 15, cp = tid >> 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int key = min(k0 + 4 * kq + r, n - 1);
+        t.v[r] = *reinterpret_cast<const u32x4*>(vb + (int64_t)key * v_sn + 8 * cp);
+    }
+}
+
+__device__ __forceinline__ void store_tile(const TileRegs& t, uint16_t* ks, uint16_t* vts) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int p = tid + 256 * r;
+        *reinterpret_cast<u32x4*>(ks + (p >> 4) * kKStride + 8 * (p & 15)) = t.k[r];
+    }
+    const int kq = tid & 15, cp = tid >> 4;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        u32x2 w;
+        w.x = half_of(t.v[0], e) | (half_of(t.v[1], e) << 16);
+        w.y = half_of(t.v[2], e) | (half_of(t.v[3], e) << 16);
+        *reinterpret_cast<u32x2*>(vts + (8 * cp + e) * kVStride + 4 * kq) = w;
+    }
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+prefill_kernel(PrefillParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kKeys * kKStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vts[kD * kVStride];
+
+    const int g = p.Hq / p.Hk;
+    const int xcd = blockIdx.x % kXcds;
+    const int slot = blockIdx.x / kXcds;
+    const int group = (slot / g) * kXcds + xcd;
+    const int ngroups = p.qblocks * p.B * p.Hk;
+    if (group >= ngroups) return;
+    const int qb = p.qblocks - 1 - group / (p.B * p.Hk);
+    const int rem = group % (p.B * p.Hk);
+    const int b = rem / p.Hk, kvh = rem % p.Hk;
+    const int h = kvh * g + slot % g;
+    const int n = p.seqlens ? max(0, min(p.seqlens[b], p.Nk)) : p.Nk;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int q0 = qb * kQRows + wave * 32;
+    const int shift = n - p.Lq;
+    int k_end = n;
+    if (p.causal) k_end = min(n, min(qb * kQRows + kQRows, p.Lq) + shift);
+    const int ntiles = k_end > 0 ? (k_end + kKeys - 1) / kKeys : 0;
+
+    // Q operand: rows q0 + 16 nt + col, d = 32 ks + 8 grp .. +7
+    u32x4 qr[2][4];
+    {
+        const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int row = q0 + 16 * nt + col;
+            const bool ok = row < p.Lq;
+            const uint16_t* src = qbase + (int64_t)min(row, p.Lq - 1) * p.q_sl + 8 * grp;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const u32x4 x = *reinterpret_cast<const u32x4*>(src + 32 * kk);
+                qr[nt][kk] = u32x4{ok ? x.x : 0u, ok ? x.y : 0u, ok ? x.z : 0u, ok ? x.w : 0u};
+            }
+        }
+    }
+
+    v4f o[8][2];
+#pragma unroll
+    for (int md = 0; md < 8; ++md)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) o[md][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+    float m[2] = {kNegInf, kNegInf};
+    float l[2] = {0.f, 0.f};
+
+    const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)kvh * p.k_sh;
+    const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
+    TileRegs tr;
+    if (ntiles > 0) load_tile(tr, kb, vb, p.k_sn, p.v_sn, 0, n);
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int k0 = t * kKeys;
+        __syncthreads();
+        store_tile(tr, ks, vts);
+        __syncthreads();
+        if (t + 1 < ntiles) load_tile(tr, kb, vb, p.k_sn, p.v_sn, k0 + kKeys, n);
+
+        // S^T = K . Q^T for 64 keys x 32 queries
+        v4f s[4][2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) s[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (16 * mt + col) * kKStride + 32 * kk + 8 * grp);
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) s[mt][nt] = mfma32(a, qr[nt][kk], s[mt][nt]);
+            }
+        }
+
+        // masked, scaled scores and the online softmax (per query column)
+        u32x4 pb[2][2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int qi = q0 + 16 * nt + col;
+            const int last = p.causal ? min(qi + shift, n - 1) : n - 1;
+            float mx = kNegInf;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int kj = k0 + 16 * mt + 4 * grp + i;
+                    const float x = kj <= last ? s[mt][nt][i] * p.scale_log2 : kNegInf;
+                    s[mt][nt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, shfl_xor_f(mx, 16));
+            mx = fmaxf(mx, shfl_xor_f(mx, 32));
+            const float m_new = fmaxf(m[nt], mx);
+            const float base = m_new == kNegInf ? 0.f : m_new;
+            const float alpha = fast_exp2(m[nt] - base);
+            m[nt] = m_new;
+            float sum = 0.f;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = fast_exp2(s[mt][nt][i] - base);
+                    s[mt][nt][i] = e;
+                    sum += e;
+                }
+            l[nt] = l[nt] * alpha + sum;
+#pragma unroll
+            for (int md = 0; md < 8; ++md) o[md][nt] *= alpha;
+#pragma unroll
+            for (int ss = 0; ss < 2; ++ss)
+                pb[ss][nt] = u32x4{pack2(s[2 * ss][nt][0], s[2 * ss][nt][1]), pack2(s[2 * ss][nt][2], s[2 * ss][nt][3]),
+                                   pack2(s[2 * ss + 1][nt][0], s[2 * ss + 1][nt][1]),
+                                   pack2(s[2 * ss + 1][nt][2], s[2 * ss + 1][nt][3])};
+        }
+
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+#pragma unroll
+            for (int md = 0; md < 8; ++md) {
+                const uint16_t* row = vts + (16 * md + col) * kVStride + 32 * ss + 4 * grp;
+                const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
+                const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
+                const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) o[md][nt] = mfma32(a, pb[ss][nt], o[md][nt]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        float tot = l[nt];
+        tot += shfl_xor_f(tot, 16);
+        tot += shfl_xor_f(tot, 32);
+        const float inv = tot > 0.f ? 1.f / tot : 0.f;
+        const int qi = q0 + 16 * nt + col;
+        if (qi >= p.Lq) continue;
+        uint16_t* dst = p.out + (int64_t)b * p.o_sb + (int64_t)qi * p.o_sl + (int64_t)h * p.o_sh + 4 * grp;
+#pragma unroll
+        for (int md = 0; md < 8; ++md) {
+            u32x2 w;
+            w.x = pack2(o[md][nt][0] * inv, o[md][nt][1] * inv);
+            w.y = pack2(o[md][nt][2] * inv, o[md][nt][3] * inv);
+            *reinterpret_cast<u32x2*>(dst + 16 * md) = w;
+        }
+        if (p.lse && grp == 0)
+            p.lse[((int64_t)b * p.Hq + h) * p.Lq + qi] = tot > 0.f ? (m[nt] + __log2f(tot)) * kLn2 : kNegInf;
+    }
+}
+
+bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+
+}  // namespace slimkv
+
+using namespace slimkv;
+
+extern "C" int slimkv_prefill_attention(const slimkv_prefill_attention_args* a, void* stream) {
+    if (!a || !a->q || !a->k || !a->v || !a->out) return fail(SLIMKV_EINVAL, "null pointer");
+    if (a->head_dim != kD) return fail(SLIMKV_EUNSUP, "prefill attention supports head_dim 128");
+    if (a->batch < 0 || a->queries < 0 || a->keys < 0 || a->heads <= 0 || a->kv_heads <= 0 ||
+        a->heads % a->kv_heads || a->batch > 65535 || a->queries > (1 << 24) || a->keys > (1 << 30))
+        return fail(SLIMKV_EINVAL, "invalid prefill attention sizes");
+    for (int64_t s : {a->q_sb, a->q_sl, a->q_sh, a->k_sb, a->k_sn, a->k_sh, a->v_sb, a->v_sn, a->v_sh, a->o_sb,
+                      a->o_sl, a->o_sh})
+        if (s % 8) return fail(SLIMKV_EINVAL, "strides must be multiples of 8 elements");
+    if (!al16(a->q) || !al16(a->k) || !al16(a->v) || !al16(a->out))
+        return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
+    if (a->batch == 0 || a->queries == 0) return SLIMKV_OK;
+    PrefillParams p{};
+    p.q = static_cast<const uint16_t*>(a->q); p.q_sb = a->q_sb; p.q_sl = a->q_sl; p.q_sh = a->q_sh;
+    p.k = static_cast<const uint16_t*>(a->k); p.k_sb = a->k_sb; p.k_sn = a->k_sn; p.k_sh = a->k_sh;
+    p.v = static_cast<const uint16_t*>(a->v); p.v_sb = a->v_sb; p.v_sn = a->v_sn; p.v_sh = a->v_sh;
+    p.out = static_cast<uint16_t*>(a->out); p.o_sb = a->o_sb; p.o_sl = a->o_sl; p.o_sh = a->o_sh;
+    p.lse = a->lse;
+    p.seqlens = a->seqlens_k;
+    p.B = (int)a->batch; p.Lq = (int)a->queries; p.Hq = (int)a->heads; p.Hk = (int)a->kv_heads;
+    p.Nk = (int)a->keys; p.causal = a->causal ? 1 : 0;
+    p.qblocks = (p.Lq + kQRows - 1) / kQRows;
+    p.scale_log2 = (float)(a->scale * 1.4426950408889634);
+    const int64_t groups = (int64_t)p.qblocks * p.B * p.Hk;
+    const int64_t grid = (groups + kXcds - 1) / kXcds * kXcds * (p.Hq / p.Hk);
+    if (grid > 0x7fffffff) return fail(SLIMKV_EINVAL, "prefill grid too large");
+    hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)grid), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+    return check_hip(hipGetLastError(), "prefill attention launch");
+}

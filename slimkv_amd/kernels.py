@@ -74,6 +74,36 @@ def attention_forward(q, k, v, scale, causal=False, splits=0, seqlens=None, out=
     return out, lse
 
 
+def prefill_attention(q, k, v, scale, causal=True, seqlens_k=None, out=None, lse=None):
+    """Causal (bottom-right) GQA prefill attention, head_dim 128 (MFMA flash
+    attention).  q [B,Lq,Hq,128], k/v [B,N,Hk,128] BSHD bf16.
+
+    Returns (out [B,Lq,Hq,128] bf16, lse [B,Hq,Lq] fp32).
+    """
+    _need_device(q, k, v, seqlens_k)
+    _need_bf16(q, k, v)
+    q, k, v = (_last_contiguous(x) for x in (q, k, v))
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError('BSHD tensors required')
+    B, Lq, Hq, D = q.shape
+    _, N, Hk, _ = k.shape
+    if k.shape[0] != B or k.shape[-1] != D or v.shape != k.shape:
+        raise ValueError('invalid K/V shapes')
+    if out is None:
+        out = torch.empty(B, Lq, Hq, D, dtype=BF16, device=q.device)
+    if lse is None:
+        lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device)
+    if seqlens_k is not None:
+        if seqlens_k.dtype != torch.int32 or not seqlens_k.is_contiguous() or seqlens_k.numel() != B:
+            raise ValueError('One int32 key length per sequence required')
+    a = _lib.PrefillAttentionArgs(
+        _ptr(q), *q.stride()[:3], _ptr(k), *k.stride()[:3], _ptr(v), *v.stride()[:3],
+        _ptr(out), *out.stride()[:3], _ptr(lse), _ptr(seqlens_k),
+        B, Lq, Hq, Hk, N, D, float(scale), int(bool(causal)))
+    check(lib().slimkv_prefill_attention(ctypes.byref(a), _lib.stream_handle(q.device)))
+    return out, lse
+
+
 def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias, block_diagonal,
                  lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse):
     _need_device(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v)
