@@ -258,6 +258,31 @@ typedef struct slimkv_prefill_attention_args {
 int slimkv_prefill_attention(const slimkv_prefill_attention_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Beacon down-projection of the selected rows of a window.
+ * Replaces beacon_{k,v}_down_proj inside _project_beacon_key/_value and the
+ * beacon-row selection of _incremental_cache
+ * (slimkv/llama3/modeling_llama.py:383-390,444-451,1347-1367):
+ *   out[b, i, :] = bf16(x[b, rows[i], :] @ weight^T)
+ * x [B, length, in_features] bf16 (row strides x_sb, x_sl); rows: device int64
+ * [row_count] indices into length (NULL: rows 0..row_count-1; an index
+ * outside [0, length) yields a zero row); weight [out_features, in_features]
+ * contiguous (nn.Linear layout); out [B, row_count, out_features] bf16.
+ * blocks > 1 declares a block-diagonal weight with `blocks` diagonal blocks
+ * (per-KV-head bases): each output block contracts its own input block only.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_down_project_args {
+    const void* x; int64_t x_sb, x_sl;
+    const int64_t* rows; int64_t row_count, length;
+    const void* weight;
+    void* out; int64_t o_sb, o_sn;
+    int64_t batch, in_features, out_features, blocks;
+} slimkv_down_project_args;
+
+size_t slimkv_down_project_workspace(const slimkv_down_project_args* a);
+int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* ------------------------------------------------------------------------
  * Beacon-page I/O: exact bf16 copies between engine-owned pages and dense
  * latent rows, for `batch` requests at once.
  * Replaces BeaconPages._indices/read/append (slimkv/vllm_plugin/paged_cache.py:60-87)

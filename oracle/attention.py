@@ -156,6 +156,20 @@ def reconstruct(latent, up, bias, kv_heads, head_dim, bf16_boundaries=True):
     return np.asarray(rnd(full), np.float64).reshape(B, n, kv_heads, head_dim).transpose(0, 2, 1, 3)
 
 
+def down_project(x, weight, rows=None, bf16_boundaries=True):
+    """Beacon latents of the selected rows (modeling_llama.py:383-390 down
+    projection, then the role selection of _incremental_cache :1355-1359):
+    x [B,L,K] -> x[:, rows] @ weight^T -> [B,n,N]; a row index outside [0, L)
+    gives a zero row (the HIP kernel's documented out-of-range behaviour)."""
+    rnd = round_bf16 if bf16_boundaries else (lambda a: np.asarray(a, np.float64))
+    x = np.asarray(x, np.float64)
+    B, L, K = x.shape
+    rows = np.arange(L) if rows is None else np.asarray(rows, np.int64)
+    valid = (rows >= 0) & (rows < L)
+    picked = np.where(valid[None, :, None], x[:, np.clip(rows, 0, L - 1)], 0.0)
+    return np.asarray(rnd(picked @ np.asarray(weight, np.float64).T), np.float64)
+
+
 def materialize(sink, history, raw, window, window_roles, up, bias, kv_heads, head_dim,
                 current=None, bf16_boundaries=True):
     """[sink ; up(history) ; interleave(up(window), raw by roles) ; current] along keys

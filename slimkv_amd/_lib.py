@@ -118,6 +118,14 @@ PrefillAttentionArgs = _struct('slimkv_prefill_attention_args', [
     ('causal', c_i32),
 ])
 
+DownProjectArgs = _struct('slimkv_down_project_args', [
+    ('x', c_ptr), *_i64s('x_sb', 'x_sl'),
+    ('rows', c_ptr), *_i64s('row_count', 'length'),
+    ('weight', c_ptr),
+    ('out', c_ptr), *_i64s('o_sb', 'o_sn'),
+    *_i64s('batch', 'in_features', 'out_features', 'blocks'),
+])
+
 BeaconPagesArgs = _struct('slimkv_beacon_pages_args', [
     ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
     ('table', c_ptr), ('t_sb', c_i64),
@@ -154,6 +162,8 @@ SIGNATURES = {
     'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
     'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),
     'slimkv_prefill_attention': (ctypes.c_int, [ctypes.POINTER(PrefillAttentionArgs), c_ptr]),
+    'slimkv_down_project_workspace': (ctypes.c_size_t, [ctypes.POINTER(DownProjectArgs)]),
+    'slimkv_down_project': (ctypes.c_int, [ctypes.POINTER(DownProjectArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }

@@ -13,7 +13,7 @@ from pathlib import Path
 PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / 'csrc'
 LIBRARY = PACKAGE / 'libslimkv_hip.so'
-SOURCES = ['attention.hip', 'rope.hip', 'recon.hip', 'paged.hip', 'prefill.hip']
+SOURCES = ['attention.hip', 'rope.hip', 'recon.hip', 'paged.hip', 'prefill.hip', 'down.hip']
 
 FLAGS = [
     '--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared',
@@ -31,7 +31,7 @@ def hipcc():
 
 
 def sources():
-    return [CSRC / name for name in SOURCES if (CSRC / name).exists()]
+    return [CSRC / name for name in SOURCES]
 
 
 def build(verbose=False, extra=()):

@@ -1,0 +1,192 @@
+// Beacon down-projection on the 16x16x32 bf16 MFMA: the latents of the
+// selected (beacon) rows of a window,
+//
+//   out[b, i, :] = bf16(x[b, rows[i], :] @ W^T),   W [N, K] (nn.Linear weight)
+//
+// as in _project_beacon_key/_project_beacon_value followed by the role
+// selection of _incremental_cache (slimkv/llama3/modeling_llama.py:383-390,
+// 444-451, 1347-1367); only the selected rows are projected.  A block-diagonal
+// W (per-KV-head bases, `blocks` diagonal blocks) contracts each output block
+// over its own K block only.
+//
+// One wavefront computes C^T[n, m] = W[n, :] . x[m, :] for 16 outputs x 64
+// rows: A = W rows and B = x rows are both contiguous along the contraction,
+// and a lane ends with 4 consecutive outputs of one row (8-byte stores).  Long
+// contractions are split over workgroups into fp32 partials summed in a fixed
+// order by a second kernel, so results do not depend on scheduling.
+
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace slimkv {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v4f mfma32(u32x4 a, u32x4 b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+struct DownParams {
+    const uint16_t* x; int64_t x_sb, x_sl;
+    const int64_t* rows; int64_t length;
+    const uint16_t* w;
+    uint16_t* out; int64_t o_sb, o_sn;
+    float* part;                 // [splits, M, N] when splits > 1
+    int B, n, N, K, blocks, splits, kchunk;
+};
+
+constexpr int kMFrags = 4;       // 64 rows per wave
+
+__global__ void __launch_bounds__(256) down_kernel(DownParams p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int ngroups = (p.N + 63) / 64;
+    const int M = p.B * p.n;
+    const int mtiles = (M + 16 * kMFrags - 1) / (16 * kMFrags);
+    const int s = blockIdx.x % p.splits;
+    const int rest = blockIdx.x / p.splits;
+    const int ng = rest % ngroups;
+    const int mt = rest / ngroups;
+    if (mt >= mtiles) return;
+    const int n0 = ng * 64 + wave * 16;
+    if (n0 >= p.N) return;
+
+    const int kb = p.K / p.blocks;
+    const int head = n0 / (p.N / p.blocks);
+    int k_lo = p.blocks > 1 ? head * kb : 0;
+    int k_hi = p.blocks > 1 ? k_lo + kb : p.K;
+    k_lo += s * p.kchunk;
+    k_hi = min(k_hi, k_lo + p.kchunk);
+
+    const uint16_t* wrow = p.w + (int64_t)(n0 + col) * p.K + 8 * grp;
+    const uint16_t* xrow[kMFrags];
+    bool mok[kMFrags], rok[kMFrags];
+#pragma unroll
+    for (int f = 0; f < kMFrags; ++f) {
+        const int m = mt * 16 * kMFrags + 16 * f + col;
+        mok[f] = m < M;
+        const int mm = mok[f] ? m : 0;
+        const int b = mm / p.n, i = mm % p.n;
+        const int64_t r = p.rows ? p.rows[i] : i;
+        rok[f] = r >= 0 && r < p.length;            // a row outside x projects to zeros
+        xrow[f] = p.x + (int64_t)b * p.x_sb + (rok[f] ? r : 0) * p.x_sl + 8 * grp;
+    }
+    v4f acc[kMFrags];
+#pragma unroll
+    for (int f = 0; f < kMFrags; ++f) acc[f] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int k = k_lo; k < k_hi; k += 32) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(wrow + k);
+#pragma unroll
+        for (int f = 0; f < kMFrags; ++f) acc[f] = mfma32(a, *reinterpret_cast<const u32x4*>(xrow[f] + k), acc[f]);
+    }
+    const int M_ = M;
+#pragma unroll
+    for (int f = 0; f < kMFrags; ++f) {
+        if (!mok[f]) continue;
+        if (!rok[f]) acc[f] = v4f{0.f, 0.f, 0.f, 0.f};
+        const int m = mt * 16 * kMFrags + 16 * f + col;
+        const int nn = n0 + 4 * grp;
+        if (p.splits == 1) {
+            const int b = m / p.n, i = m % p.n;
+            u32x2 w;
+            w.x = f32_to_bf16(acc[f][0]) | (f32_to_bf16(acc[f][1]) << 16);
+            w.y = f32_to_bf16(acc[f][2]) | (f32_to_bf16(acc[f][3]) << 16);
+            *reinterpret_cast<u32x2*>(p.out + (int64_t)b * p.o_sb + (int64_t)i * p.o_sn + nn) = w;
+        } else {
+            *reinterpret_cast<v4f*>(p.part + ((int64_t)s * M_ + m) * p.N + nn) = acc[f];
+        }
+    }
+}
+
+// Sum the split partials in split order and round once to bf16.
+__global__ void __launch_bounds__(256) down_reduce_kernel(DownParams p) {
+    const int64_t M = (int64_t)p.B * p.n;
+    const int64_t quads = M * (p.N / 4);
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= quads) return;
+    const int64_t m = id / (p.N / 4);
+    const int nn = (int)(id % (p.N / 4)) * 4;
+    v4f sum = *reinterpret_cast<const v4f*>(p.part + m * p.N + nn);
+    for (int s = 1; s < p.splits; ++s) sum += *reinterpret_cast<const v4f*>(p.part + ((int64_t)s * M + m) * p.N + nn);
+    const int b = (int)(m / p.n), i = (int)(m % p.n);
+    u32x2 w;
+    w.x = f32_to_bf16(sum[0]) | (f32_to_bf16(sum[1]) << 16);
+    w.y = f32_to_bf16(sum[2]) | (f32_to_bf16(sum[3]) << 16);
+    *reinterpret_cast<u32x2*>(p.out + (int64_t)b * p.o_sb + (int64_t)i * p.o_sn + nn) = w;
+}
+
+bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+struct DownPlan {
+    int splits, kchunk;
+    size_t bytes;
+};
+
+int plan_down(const slimkv_down_project_args* a, DownPlan* plan) {
+    if (!a || !a->x || !a->weight || !a->out) return fail(SLIMKV_EINVAL, "null pointer");
+    if (a->batch < 0 || a->row_count < 0 || a->length < 0 || (!a->rows && a->row_count > a->length) ||
+        a->in_features <= 0 || a->out_features <= 0 || a->blocks <= 0 || a->batch > (1 << 20) ||
+        a->row_count > (1 << 24) || a->batch * a->row_count > (1 << 30))
+        return fail(SLIMKV_EINVAL, "invalid down-projection sizes");
+    if (a->out_features % (16 * a->blocks) || a->in_features % (32 * a->blocks))
+        return fail(SLIMKV_EUNSUP, "down-projection needs out_features/blocks % 16 == 0 and in_features/blocks % 32 == 0");
+    if (a->x_sb % 8 || a->x_sl % 8 || a->o_sb % 4 || a->o_sn % 4 || !al16(a->x) || !al16(a->weight) ||
+        (reinterpret_cast<uintptr_t>(a->out) & 7))
+        return fail(SLIMKV_EINVAL, "x rows must be 16-byte aligned and out rows 8-byte aligned");
+    const int64_t M = a->batch * a->row_count;
+    const int64_t kb = a->in_features / a->blocks;
+    const int64_t base = (a->out_features + 63) / 64 * ((M + 63) / 64);
+    int splits = 1;
+    if (base > 0 && base < 512) splits = (int)std::min<int64_t>((512 + base - 1) / base, kb / 256);
+    splits = std::max(splits, 1);
+    int64_t kchunk = (kb + splits - 1) / splits;
+    kchunk = (kchunk + 31) / 32 * 32;
+    splits = (int)((kb + kchunk - 1) / kchunk);
+    plan->splits = splits;
+    plan->kchunk = (int)kchunk;
+    plan->bytes = splits > 1 ? (size_t)splits * M * a->out_features * sizeof(float) : 0;
+    return SLIMKV_OK;
+}
+
+}  // namespace
+
+}  // namespace slimkv
+
+using namespace slimkv;
+
+extern "C" size_t slimkv_down_project_workspace(const slimkv_down_project_args* a) {
+    DownPlan plan{};
+    if (plan_down(a, &plan) != SLIMKV_OK) return 0;
+    return std::max<size_t>(plan.bytes, 1);
+}
+
+extern "C" int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    DownPlan plan{};
+    int rc = plan_down(a, &plan);
+    if (rc != SLIMKV_OK) return rc;
+    if (plan.bytes && (!workspace || workspace_bytes < plan.bytes))
+        return fail(SLIMKV_EWORKSPACE, "workspace too small");
+    const int64_t M = a->batch * a->row_count;
+    if (M == 0) return SLIMKV_OK;
+    DownParams p{};
+    p.x = static_cast<const uint16_t*>(a->x); p.x_sb = a->x_sb; p.x_sl = a->x_sl;
+    p.rows = a->rows; p.length = a->length;
+    p.w = static_cast<const uint16_t*>(a->weight);
+    p.out = static_cast<uint16_t*>(a->out); p.o_sb = a->o_sb; p.o_sn = a->o_sn;
+    p.part = static_cast<float*>(workspace);
+    p.B = (int)a->batch; p.n = (int)a->row_count; p.N = (int)a->out_features; p.K = (int)a->in_features;
+    p.blocks = (int)a->blocks; p.splits = plan.splits; p.kchunk = plan.kchunk;
+    const int64_t grid = (p.N + 63) / 64 * ((M + 63) / 64) * p.splits;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(down_kernel, dim3((unsigned)grid), dim3(256), 0, st, p);
+    rc = check_hip(hipGetLastError(), "down-projection launch");
+    if (rc != SLIMKV_OK || p.splits == 1) return rc;
+    const int64_t quads = M * (p.N / 4);
+    hipLaunchKernelGGL(down_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p);
+    return check_hip(hipGetLastError(), "down-projection reduce launch");
+}

@@ -104,6 +104,38 @@ def prefill_attention(q, k, v, scale, causal=True, seqlens_k=None, out=None, lse
     return out, lse
 
 
+def down_project(x, weight, rows=None, *, blocks=1, out=None):
+    """Latents of selected rows: out[b, i] = bf16(x[b, rows[i]] @ weight^T).
+
+    x [B, L, K] bf16, weight [N, K] (nn.Linear layout), rows int64 [n] or None
+    (all rows).  `blocks` > 1 declares a block-diagonal weight.  Returns
+    out [B, n, N] bf16.
+    """
+    _need_device(x, weight, rows)
+    _need_bf16(x, weight)
+    if x.dim() != 3 or weight.dim() != 2 or weight.shape[1] != x.shape[2]:
+        raise ValueError('x must be [B, L, K] and weight [N, K]')
+    x = _last_contiguous(x)
+    weight = weight.contiguous()
+    B, L, K = x.shape
+    N = weight.shape[0]
+    if rows is not None:
+        rows = rows.to(dtype=torch.long).contiguous()
+    n = L if rows is None else rows.numel()
+    if out is None:
+        out = torch.empty(B, n, N, dtype=BF16, device=x.device)
+    if out.shape != (B, n, N) or out.stride(2) != 1:
+        raise ValueError('out must be [B, n, N] with contiguous rows')
+    a = _lib.DownProjectArgs(_ptr(x), x.stride(0), x.stride(1), _ptr(rows), n, L, _ptr(weight),
+                             _ptr(out), out.stride(0), out.stride(1), B, K, N, int(blocks))
+    nbytes = lib().slimkv_down_project_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    ws = _workspace(nbytes, x.device)
+    check(lib().slimkv_down_project(ctypes.byref(a), _ptr(ws), nbytes, _lib.stream_handle(x.device)))
+    return out
+
+
 def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias, block_diagonal,
                  lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse):
     _need_device(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v)

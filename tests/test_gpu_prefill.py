@@ -64,3 +64,161 @@ def test_rejects_other_head_dims(device):
     x = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16, device=device)
     with pytest.raises(RuntimeError):
         kernels.prefill_attention(x, x, x, 0.125)
+
+
+def _neighbour_of_exact(actual, exact, abs_terms):
+    """bf16 outputs of an fp32-accumulated GEMM: each within one bf16 ulp of the
+    float64 result plus the fp32 accumulation bound, almost all correctly rounded."""
+    from oracle.bf16 import round_bf16
+    a, x = np.asarray(actual, np.float64), np.asarray(exact, np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(x), 1e-30))) - 7)
+    bad = np.abs(a - x) >= ulp * 1.0001 + np.asarray(abs_terms) * 2.0 ** -20
+    assert not bad.any(), list(zip(a[bad][:4], x[bad][:4]))
+    assert (a == round_bf16(x)).mean() > 0.98
+
+
+@pytest.mark.parametrize('K,N,blocks,rows', [
+    (4096, 256, 1, 'beacons'),      # hidden -> global rank (split contraction)
+    (1024, 256, 8, 'beacons'),      # per-head K_full[128] -> r 32, block-diagonal
+    (512, 128, 1, 'all'),
+    (1024, 384, 8, 'bad'),          # rank 48 per head; an out-of-range row gives zeros
+])
+def test_down_projection_matches_oracle(device, K, N, blocks, rows):
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import orthonormal_columns
+    gen = torch.Generator(device=device).manual_seed(K + N)
+    B, L = 3, 320
+    x = torch.randn(B, L, K, generator=gen, device=device).to(torch.bfloat16)
+    if blocks > 1:
+        w = torch.zeros(N, K)
+        nb, kb = N // blocks, K // blocks
+        for h in range(blocks):
+            w[h * nb:(h + 1) * nb, h * kb:(h + 1) * kb] = orthonormal_columns(kb, nb, torch.Generator().manual_seed(h)).t()
+        w = w.to(device, torch.bfloat16)
+    else:
+        w = (torch.randn(N, K, generator=gen, device=device) / K ** 0.5).to(torch.bfloat16)
+    if rows == 'all':
+        idx = None
+    else:
+        idx = torch.arange(4, L, 5, device=device)           # one beacon after every 4 raw tokens
+        if rows == 'bad':
+            idx[3] = L + 7
+    out = kernels.down_project(x, w, idx, blocks=blocks)
+    torch.cuda.synchronize()
+    ridx = None if idx is None else idx.cpu().numpy()
+    exact = oa.down_project(to_np(x), to_np(w), ridx, bf16_boundaries=False)
+    terms = oa.down_project(np.abs(to_np(x)), np.abs(to_np(w)), ridx, bf16_boundaries=False)
+    _neighbour_of_exact(to_np(out), exact, terms)
+    if rows == 'bad':
+        assert not to_np(out)[:, 3].any()
+
+
+class RotaryEmbedding:          # the type name the RoPE fusion recognises
+    def __init__(self, rows, device):
+        from slimkv_amd.workloads import rope_tables
+        self.cos_cached, self.sin_cached = rope_tables(rows, 128, 500000.0, device)
+        self.max_seq_len_cached = rows
+
+
+def _prefill_module(device, per_head_down, bias, seed):
+    """An attention layer as the prefill forward uses it: 8 query / 2 KV heads,
+    head_dim 128, hidden 256, beacon rank 32 per KV head (global 64)."""
+    from types import SimpleNamespace
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+    H, Hk, D, hidden, r = 8, 2, 128, 256, 32
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def linear(i, o, b=False, weight=None):
+        lin = torch.nn.Linear(i, o, bias=b, device=device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.copy_(weight if weight is not None else torch.randn(o, i, generator=gen, device=device) / i ** 0.5)
+            if b:
+                lin.bias.copy_(0.3 * torch.randn(o, generator=gen, device=device))
+        return lin
+
+    up = [block_diagonal([orthonormal_columns(D, r, torch.Generator().manual_seed(seed + 10 * j + i))
+                          for i in range(Hk)]).to(device, torch.bfloat16) for j in range(2)]
+    if per_head_down:        # down weight [Hk*r, hidden] with hidden split per KV head
+        down = [block_diagonal([orthonormal_columns(hidden // Hk, r, torch.Generator().manual_seed(seed + 50 + 10 * j + i))
+                                for i in range(Hk)]).t().contiguous().to(device, torch.bfloat16) for j in range(2)]
+    else:
+        down = [None, None]
+    config = SimpleNamespace(beacon_param=['q', 'k', 'v'], beacon_decode_backend='latent', beacon_sink_size=1,
+                             _attn_implementation='flash_attention_2')
+    att = SimpleNamespace(
+        config=config, num_heads=H, num_key_value_heads=Hk, head_dim=D, hidden_size=hidden,
+        q_proj=linear(hidden, H * D), k_proj=linear(hidden, Hk * D, bias), v_proj=linear(hidden, Hk * D, bias),
+        beacon_q_proj=linear(hidden, H * D),
+        beacon_k_down_proj=linear(hidden, Hk * r, weight=down[0]), beacon_v_down_proj=linear(hidden, Hk * r, weight=down[1]),
+        beacon_k_up_proj=linear(Hk * r, Hk * D, bias, up[0]), beacon_v_up_proj=linear(Hk * r, Hk * D, bias, up[1]),
+        rotary_emb=RotaryEmbedding(4096, device))
+    att._use_shared_kv_down_proj = lambda: False
+    att.o_proj_with_beacon = lambda output, size, indices: output
+    return att, gen
+
+
+@pytest.mark.parametrize('per_head_down,bias,n_hist', [(False, False, 24), (True, True, 40), (False, True, 0)])
+def test_prefill_window_matches_oracle(device, per_head_down, bias, n_hist):
+    """One prefill window: [sink | up(history latents) | 1024/4-style window of
+    32 raw + 8 beacons], latents of the new beacons, output after attention."""
+    from oracle import rope as orope
+    from slimkv_amd.memory import ReconstructionCache
+    from slimkv_amd.prefill import prefill_forward
+    from slimkv_amd.prefill_ops import PrefillMetadata
+    att, gen = _prefill_module(device, per_head_down, bias, seed=7 + n_hist)
+    B, L, Hk, D, R = 2, 40, 2, 128, 64
+    rnd = lambda *s: torch.randn(*s, generator=gen, device=device).to(torch.bfloat16)
+    sink_k, sink_v = rnd(B, Hk, 1, D), rnd(B, Hk, 1, D)
+    hist_k = rnd(B, 1, n_hist, R) if n_hist else None
+    hist_v = rnd(B, 1, n_hist, R) if n_hist else None
+    pk = ReconstructionCache(sink_k, hist_k, None, None, None, Hk, D, 'k')
+    pv = ReconstructionCache(sink_v, hist_v, None, None, None, Hk, D, 'v')
+    roles = torch.zeros(L, dtype=torch.long, device=device)
+    roles[4::5] = 1
+    N = 1 + n_hist + L
+    positions = torch.arange(N, device=device)[None].expand(B, -1)
+    att._prefill_metadata = PrefillMetadata((roles == 0).nonzero().flatten(), (roles != 0).nonzero().flatten(),
+                                            roles, positions, False)
+    hidden = (0.5 * torch.randn(B, L, 256, generator=gen, device=device)).to(torch.bfloat16)
+    with torch.no_grad():
+        out, none, update = prefill_forward(att, hidden, positions, (pk, pv, 8, roles))
+        torch.cuda.synchronize()
+        # oracle: the module's own projections, then the restated low-rank path
+        q = torch.where((roles == 0)[:, None], att.q_proj(hidden), att.beacon_q_proj(hidden))
+        kf, vf = att.k_proj(hidden), att.v_proj(hidden)
+    brows = (roles != 0).nonzero().flatten().cpu().numpy()
+    h = to_np(hidden)
+    lat = {}
+    cur = {}
+    for kind, full in (('k', kf), ('v', vf)):
+        down = getattr(att, f'beacon_{kind}_down_proj').weight
+        up = getattr(att, f'beacon_{kind}_up_proj')
+        lat[kind] = oa.down_project(h, to_np(down), brows)
+        rec = oa.reconstruct(lat[kind][:, None], to_np(up.weight), None if up.bias is None else to_np(up.bias), Hk, D)
+        c = to_np(full).reshape(B, L, Hk, D).transpose(0, 2, 1, 3).copy()
+        c[:, :, brows] = rec
+        cur[kind] = c
+    # latents: bit-level check against the oracle GEMM (one bf16 ulp at most)
+    for kind, got in (('k', update.key_latents), ('v', update.value_latents)):
+        down = getattr(att, f'beacon_{kind}_down_proj').weight
+        exact = oa.down_project(h, to_np(down), brows, bf16_boundaries=False)
+        terms = oa.down_project(np.abs(h), np.abs(to_np(down)), brows, bf16_boundaries=False)
+        assert got.shape == (B, 1, len(brows), R)
+        _neighbour_of_exact(to_np(got[:, 0]), exact, terms)
+    up_k, up_v = att.beacon_k_up_proj, att.beacon_v_up_proj
+    bk = None if up_k.bias is None else to_np(up_k.bias)
+    bv = None if up_v.bias is None else to_np(up_v.bias)
+    K = oa.materialize(to_np(sink_k), None if hist_k is None else to_np(hist_k), None, None, None,
+                       to_np(up_k.weight), bk, Hk, D, cur['k'])
+    V = oa.materialize(to_np(sink_v), None if hist_v is None else to_np(hist_v), None, None, None,
+                       to_np(up_v.weight), bv, Hk, D, cur['v'])
+    c = to_np(att.rotary_emb.cos_cached).astype(np.float32)
+    s = to_np(att.rotary_emb.sin_cached).astype(np.float32)
+    qn = to_np(q).reshape(B, L, 8, D).transpose(0, 2, 1, 3).astype(np.float32)
+    q_rot, k_rot = orope.prefill_rope(qn, K.astype(np.float32), c, s, positions.cpu().numpy(),
+                                      roles.cpu().numpy(), 1)
+    want, _ = oa.eager_forward(q_rot.transpose(0, 2, 1, 3), k_rot.transpose(0, 2, 1, 3), V.transpose(0, 2, 1, 3),
+                               D ** -0.5, causal=True)
+    assert none is None
+    assert_close(to_np(out), want.reshape(B, L, 8 * D))
+    assert update[2] == 8 and update.raw_indices.tolist() == (roles == 0).nonzero().flatten().tolist()

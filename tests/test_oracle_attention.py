@@ -156,3 +156,19 @@ def test_materialize_interleaves_window_beacons_by_role():
     np.testing.assert_allclose(full[:, :, 1:3], oa.reconstruct(hist, up, None, Hkv, D, False))
     np.testing.assert_array_equal(full[:, :, [3, 4, 6]], raw)
     np.testing.assert_allclose(full[:, :, 5:6], oa.reconstruct(win, up, None, Hkv, D, False))
+
+
+def test_down_project_matches_loops_and_selects_rows():
+    """The down-projection oracle against explicit sums over the selected rows
+    (rounding switched off), and its bf16 rounding against the bf16 module."""
+    from oracle.bf16 import round_bf16
+    x, w = rand(2, 7, 5), rand(3, 5)
+    rows = [4, 0, 6, -1, 7]
+    got = oa.down_project(x, w, rows, bf16_boundaries=False)
+    for b in range(2):
+        for i, r in enumerate(rows):
+            for n in range(3):
+                want = sum(x[b, r, k] * w[n, k] for k in range(5)) if 0 <= r < 7 else 0.0
+                assert abs(got[b, i, n] - want) < 1e-12
+    np.testing.assert_array_equal(oa.down_project(x, w, rows), round_bf16(got))
+    np.testing.assert_array_equal(oa.down_project(x, w), oa.down_project(x, w, list(range(7))))
