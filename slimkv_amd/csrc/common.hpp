@@ -48,6 +48,16 @@ __device__ __forceinline__ v4f mfma16(v4s a, v4s b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// D = A(16x32) * B(32x16) + C on the gfx950 16x16x32 bf16 MFMA.  Lane l holds
+// A[l%16][8*(l/16)+j], B[8*(l/16)+j][l%16] (j = 0..7, eight bf16 in a u32x4)
+// and D[4*(l/16)+i][l%16].
+__device__ __forceinline__ v4f mfma32(u32x4 a, u32x4 b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);
 }

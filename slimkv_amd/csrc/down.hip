@@ -23,13 +23,6 @@ namespace slimkv {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ v4f mfma32(u32x4 a, u32x4 b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-}
-
 struct DownParams {
     const uint16_t* x; int64_t x_sb, x_sl;
     const int64_t* rows; int64_t length;

@@ -33,13 +33,6 @@ namespace slimkv {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ v4f mfma32(u32x4 a, u32x4 b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-}
-
 constexpr int kD = 128;                  // head dim
 constexpr int kQRows = 128;              // query rows per workgroup
 constexpr int kKeys = 64;                // keys per tile
