@@ -95,6 +95,9 @@ int slimkv_attention_forward(const slimkv_attention_args* a, void* workspace,
  *         latent branch then reads only each head's own latent slice.
  * lat_causal: bottom-right causal latent branch (the beacon-insertion step).
  * out [B, Lq, Hq, D] bf16; lse [B, Hq, Lq] fp32 (may be NULL).
+ * up_k_t  optional [Hkv, Rk/Hkv, D] per-head transposed K bases made by
+ *         slimkv_prepare_latent_bases; with block_diagonal the query
+ *         absorption then runs on MFMA in one wavefront per (b, KV head).
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_latent_decode_args {
     const void* q;  int64_t q_sb, q_sl, q_sh;
@@ -117,11 +120,20 @@ typedef struct slimkv_latent_decode_args {
     void* out; int64_t o_sb, o_sl, o_sh;
     float* lse;
     int32_t raw_splits, lat_splits; /* 0 = automatic */
+    const void* up_k_t;
 } slimkv_latent_decode_args;
 
 size_t slimkv_latent_decode_workspace(const slimkv_latent_decode_args* a);
 int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* One-time re-layout of block-diagonal K bases for slimkv_latent_decode (no
+ * counterpart in the reference, whose project_query reads U_K as stored,
+ * slimkv/llama3/fa2_decode.py:41-46): out[h, c, d] = up_k[h*D + d, h*r + c]
+ * with r = rank/kv_heads.  up_k [kv_heads*D, rank] bf16 row-major; out
+ * [kv_heads, r, D] bf16. */
+int slimkv_prepare_latent_bases(const void* up_k, int64_t kv_heads, int64_t head_dim, int64_t rank, void* out,
+                                void* stream);
 
 /* ------------------------------------------------------------------------
  * Beacon reconstruction: the up-projection of latent rows to full-dim K or V.

@@ -58,6 +58,7 @@ LatentDecodeArgs = _struct('slimkv_latent_decode_args', [
     ('out', c_ptr), *_i64s('o_sb', 'o_sl', 'o_sh'),
     ('lse', c_ptr),
     ('raw_splits', c_i32), ('lat_splits', c_i32),
+    ('up_k_t', c_ptr),
 ])
 
 ReconstructArgs = _struct('slimkv_reconstruct_args', [
@@ -155,6 +156,7 @@ SIGNATURES = {
     'slimkv_attention_forward': (ctypes.c_int, [ctypes.POINTER(AttentionArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(LatentDecodeArgs)]),
     'slimkv_latent_decode': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_prepare_latent_bases': (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
     'slimkv_reconstruct': (ctypes.c_int, [ctypes.POINTER(ReconstructArgs), c_ptr]),
     'slimkv_recon_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(ReconDecodeArgs)]),
     'slimkv_recon_decode': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
@@ -168,7 +170,7 @@ SIGNATURES = {
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class SlimKVError(RuntimeError):

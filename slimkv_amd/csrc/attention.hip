@@ -94,6 +94,42 @@ __device__ __forceinline__ u32x4 zero_unless(bool ok, u32x4 v) {
     return u32x4{ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
 }
 
+// Rotate one head_dim-128 query row held as MFMA operand pieces: x[c] holds
+// elements 32c + 8*grp + [0, 8); the rotate-half partner of piece c is c ^ 2.
+// out = bf16(bf16(x * bf16(cos)) + bf16(rotate_half(x) * bf16(sin))), the
+// reference's bf16 operation order (decode_kernels.py:7-51).
+__device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const float* cs, const float* sn, int grp) {
+    float v[4][8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[c][2 * e] = bf16_to_f32(x[c][e] & 0xffffu);
+            v[c][2 * e + 1] = bf16_to_f32(x[c][e] >> 16);
+        }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d0 = 32 * c + 8 * grp;
+        const float4 c0 = *reinterpret_cast<const float4*>(cs + d0), c1 = *reinterpret_cast<const float4*>(cs + d0 + 4);
+        const float4 s0 = *reinterpret_cast<const float4*>(sn + d0), s1 = *reinterpret_cast<const float4*>(sn + d0 + 4);
+        const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            float o[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float partner = c < 2 ? -v[c ^ 2][i + u] : v[c ^ 2][i + u];
+                o[u] = round_bf16(round_bf16(v[c][i + u] * round_bf16(cv[i + u])) +
+                                  round_bf16(partner * round_bf16(sv[i + u])));
+            }
+            w[i / 2] = f32_to_bf16(o[0]) | (f32_to_bf16(o[1]) << 16);
+        }
+        x[c] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+}
+
 template <int KS>
 __device__ __forceinline__ void load_tile(TileRegs<KS>& t, const uint16_t* kbase, const uint16_t* vbase,
                                           int64_t k_sn, int64_t v_sn, int r0, int r_end, int last_row,
@@ -612,6 +648,13 @@ bool combine_fast_ok(const CombineParams& cp) {
            (kCombineThreads % cp.b_w == 0 && cp.b_splits <= kFastLatPer * (kCombineThreads / cp.b_w)));
 }
 
+void launch_combine(const CombineParams& cp, int rows, hipStream_t st) {
+    if (combine_fast_ok(cp))
+        hipLaunchKernelGGL(combine_fast_kernel, dim3(rows), dim3(kCombineThreads), 0, st, cp);
+    else
+        hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kCombineThreads), 0, st, cp);
+}
+
 // ---------------------------------------------------------------------------
 // prologue: query RoPE + absorption into U_K + K-bias shift
 // ---------------------------------------------------------------------------
@@ -627,6 +670,7 @@ struct PrologueParams {
     float* shift;                          // [B][Hq*Lq] or null
     int B, Lq, Hq, Hkv, D, Rk, parts;      // parts: power of two <= 16 dividing D
     float scale;
+    const uint16_t* ut;                    // [Hkv][wq][D] per-head U_K^T (MFMA prologue) or null
 };
 
 constexpr int kMaxRows = 16;
@@ -742,6 +786,74 @@ prologue_kernel(PrologueParams pp) {
                 u32x4{o4[0], o4[1], o4[2], o4[3]};
         }
         __syncthreads();
+    }
+}
+
+// MFMA prologue for block-diagonal bases, one wavefront per (b, KV head): the
+// g*Lq query rows of the head are the MFMA columns (lane col), rotated in
+// registers, and q_lat^T[c][p] = U_K^T[c][:] . q_rot[p][:] comes from NCT
+// 16-row tiles of the prepared per-head U_K^T.  Every load is issued before any
+// result is needed: one memory round trip for q, U_K^T and the position, one
+// more for the RoPE table rows.
+template <int NCT>
+__global__ void __launch_bounds__(64)
+prologue_mfma_kernel(PrologueParams pp) {
+    const int h = blockIdx.x % pp.Hkv;
+    const int b = blockIdx.x / pp.Hkv;
+    const int g = pp.Hq / pp.Hkv;
+    const int rows = g * pp.Lq;
+    const int lane = threadIdx.x, col = lane & 15, grp = lane >> 4;
+    const bool valid = col < rows;
+    const int p = valid ? col : 0;
+    const int jj = p / pp.Lq, l = p % pp.Lq;
+    const int j = h * g + jj;
+    constexpr int D = 128;
+    u32x4 ua[NCT][4];
+    const uint16_t* ub = pp.ut + ((int64_t)h * pp.wq + col) * D + 8 * grp;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ua[ct][c] = *reinterpret_cast<const u32x4*>(ub + (int64_t)16 * ct * D + 32 * c);
+    u32x4 qr[4];
+    const uint16_t* qrow = pp.q + (int64_t)b * pp.q_sb + (int64_t)l * pp.q_sl + (int64_t)j * pp.q_sh + 8 * grp;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * c);
+        qr[c] = valid ? x : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (pp.cos) {
+        const int64_t pos = clamp_i64(pp.pos[(int64_t)b * pp.pos_sb + l], 0, pp.rope_rows - 1);
+        rope_operand(qr, pp.cos + pos * D, pp.sin + pos * D, grp);
+    }
+    const int64_t prow = ((int64_t)b * pp.Lq + l) * pp.Hq + j;
+    if (valid) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) *reinterpret_cast<u32x4*>(pp.q_rot + prow * D + 32 * c + 8 * grp) = qr[c];
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        v4f t4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t4 = mfma32(ua[ct][c], qr[c], t4);
+        if (valid)
+            *reinterpret_cast<u32x2*>(pp.q_lat + prow * pp.wq + 16 * ct + 4 * grp) =
+                u32x2{f32_to_bf16(t4[0]) | (f32_to_bf16(t4[1]) << 16), f32_to_bf16(t4[2]) | (f32_to_bf16(t4[3]) << 16)};
+    }
+    if (pp.shift) {
+        const uint16_t* bk = pp.up_k_bias + (int64_t)h * D + 8 * grp;
+        float dot = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 bb = *reinterpret_cast<const u32x4*>(bk + 32 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dot += bf16_to_f32(qr[c][e] & 0xffffu) * bf16_to_f32(bb[e] & 0xffffu);
+                dot += bf16_to_f32(qr[c][e] >> 16) * bf16_to_f32(bb[e] >> 16);
+            }
+        }
+        dot += shfl_xor_f(dot, 16);
+        dot += shfl_xor_f(dot, 32);
+        if (valid && grp == 0) pp.shift[(int64_t)b * pp.Hq * pp.Lq + j * pp.Lq + l] = dot * pp.scale;
     }
 }
 
@@ -935,7 +1047,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 1; }
+extern "C" int slimkv_abi_version(void) { return 2; }
 
 extern "C" int slimkv_set_profile_events(void* before, void* after) {
     if ((before == nullptr) != (after == nullptr)) return fail(SLIMKV_EINVAL, "set both events or neither");
@@ -992,10 +1104,7 @@ extern "C" int slimkv_attention_forward(const slimkv_attention_args* a, void* wo
     cp.B = prm.B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hk; cp.D = (int)a->width_v;
     cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
     cp.lse = a->lse;
-    if (combine_fast_ok(cp))
-        hipLaunchKernelGGL(combine_fast_kernel, dim3(prm.B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
-    else
-        hipLaunchKernelGGL(combine_kernel, dim3(prm.B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
+    launch_combine(cp, prm.B * Hq * Lq, st);
     return check_hip(hipGetLastError(), "combine kernel launch");
 }
 
@@ -1067,7 +1176,11 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p) {
     const int64_t nl = std::max<int64_t>(a->lat_keys, 1);
     const int has_lat = a->lat_keys > 0;
     const int slots = cu * split_occupancy(has_lat ? lat_ks : 8, has_lat ? 8 : 0);
-    p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, slots);
+    // Raw workgroups sit first in the grid; the latent splits fill the remaining
+    // resident slots so every workgroup starts in the first wave of residency.
+    const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
+    const int raw_wg = (int)B * ((int)(Hkv + kWaves - 1) / kWaves) * raw_req0;
+    p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, std::max(slots - raw_wg, slots / 2));
     // Raw: one column tile per KV head over the full head width, one split per
     // 16 keys so every raw wave issues all of its loads at once (the raw set is
     // sinks + tail + current token).
@@ -1132,7 +1245,18 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
     pp.shift = (has_lat && a->up_k_bias) ? shift : nullptr;
     pp.B = B; pp.Lq = Lq; pp.Hq = Hq; pp.Hkv = Hkv; pp.D = D; pp.Rk = Rk; pp.parts = p.parts;
     pp.scale = (float)a->scale;
-    hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
+    pp.ut = static_cast<const uint16_t*>(a->up_k_t);
+    const int nct = pp.wq / 16;
+    const bool mfma_prologue = has_lat && bd && pp.ut && pp.wq % 16 == 0 && nct >= 1 && nct <= 3 &&
+                               g * Lq <= 16 && ptr_aligned16(pp.ut) && ptr_aligned16(a->q) &&
+                               (!a->up_k_bias || ptr_aligned16(a->up_k_bias));
+    if (mfma_prologue) {
+        if (nct == 1) hipLaunchKernelGGL(prologue_mfma_kernel<1>, dim3(B * Hkv), dim3(64), 0, st, pp);
+        else if (nct == 2) hipLaunchKernelGGL(prologue_mfma_kernel<2>, dim3(B * Hkv), dim3(64), 0, st, pp);
+        else hipLaunchKernelGGL(prologue_mfma_kernel<3>, dim3(B * Hkv), dim3(64), 0, st, pp);
+    } else {
+        hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
+    }
     rc = check_hip(hipGetLastError(), "prologue kernel launch");
     if (rc != SLIMKV_OK) return rc;
 
@@ -1192,10 +1316,7 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
     cp.B = B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hkv; cp.D = D;
     cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
     cp.lse = a->lse;
-    if (combine_fast_ok(cp))
-        hipLaunchKernelGGL(combine_fast_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
-    else
-        hipLaunchKernelGGL(combine_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
+    launch_combine(cp, B * Hq * Lq, st);
     return check_hip(hipGetLastError(), "combine kernel launch");
 }
 
@@ -1340,4 +1461,36 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
     cp.lse = a->lse;
     hipLaunchKernelGGL(combine_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
     return check_hip(hipGetLastError(), "combine kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// per-head transposed K bases for the in-kernel query absorption
+// ---------------------------------------------------------------------------
+
+namespace {
+
+__global__ void __launch_bounds__(256)
+prepare_bases_kernel(const uint16_t* up_k, int Hkv, int D, int R, uint16_t* out) {
+    const int r = R / Hkv;
+    const int64_t total = (int64_t)Hkv * r * D;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int d = (int)(i % D);
+    const int c = (int)((i / D) % r);
+    const int h = (int)(i / ((int64_t)D * r));
+    out[i] = up_k[((int64_t)h * D + d) * R + (int64_t)h * r + c];
+}
+
+}  // namespace
+
+extern "C" int slimkv_prepare_latent_bases(const void* up_k, int64_t kv_heads, int64_t head_dim, int64_t rank,
+                                           void* out, void* stream) {
+    if (!up_k || !out) return fail(SLIMKV_EINVAL, "null pointer");
+    if (kv_heads <= 0 || head_dim <= 0 || rank <= 0 || rank % kv_heads || kv_heads * head_dim * rank > (1LL << 31))
+        return fail(SLIMKV_EINVAL, "invalid base shape");
+    const int64_t total = kv_heads * (rank / kv_heads) * head_dim;
+    hipLaunchKernelGGL(prepare_bases_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(up_k), (int)kv_heads,
+                       (int)head_dim, (int)rank, static_cast<uint16_t*>(out));
+    return check_hip(hipGetLastError(), "prepare bases launch");
 }

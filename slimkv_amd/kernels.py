@@ -136,8 +136,29 @@ def down_project(x, weight, rows=None, *, blocks=1, out=None):
     return out
 
 
+def prepare_latent_bases(up_k, kv_heads):
+    """Per-head transposed K bases [Hkv, Rk/Hkv, D] of a block-diagonal up_k
+    [Hkv*D, Rk], made once per weight version and cached on the tensor."""
+    _need_device(up_k)
+    _need_bf16(up_k)
+    key = (up_k._version, kv_heads, up_k.data_ptr())
+    cached = getattr(up_k, '_slimkv_bases', None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    out_features, rank = up_k.shape
+    if rank % kv_heads or out_features % kv_heads:
+        raise ValueError('bases must split evenly across KV heads')
+    w = up_k.contiguous()
+    bases = torch.empty(kv_heads, rank // kv_heads, out_features // kv_heads, dtype=BF16, device=up_k.device)
+    check(lib().slimkv_prepare_latent_bases(_ptr(w), kv_heads, out_features // kv_heads, rank, _ptr(bases),
+                                            _lib.stream_handle(up_k.device)))
+    up_k._slimkv_bases = (key, bases)
+    return bases
+
+
 def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias, block_diagonal,
-                 lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse):
+                 lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse,
+                 prepared_bases=True):
     _need_device(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v)
     _need_bf16(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, up_k_bias, up_v_bias)
     B, Lq, Hq, D = q.shape
@@ -163,6 +184,10 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
         q_positions = q_positions.to(torch.int64)
         if q_positions.stride(-1) != 1:
             q_positions = q_positions.contiguous()
+    bases = None
+    if prepared_bases and block_diagonal and lat_k is not None and Nl > 0 and Rk % Hkv == 0 \
+            and (Rk // Hkv) % 16 == 0 and D == 128:
+        bases = prepare_latent_bases(up_k, Hkv)
     a = _lib.LatentDecodeArgs(
         _ptr(q), *q.stride()[:3],
         _ptr(q_positions), 0 if q_positions is None else q_positions.stride(0),
@@ -174,26 +199,28 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
         _ptr(lat_lengths), Nl, int(bool(lat_causal)), int(bool(block_diagonal)),
         _ptr(up_k), _ptr(up_k_bias), _ptr(up_v), _ptr(up_v_bias),
         B, Lq, Hq, Hkv, D, Rk, Rv, float(scale),
-        _ptr(out), *out.stride()[:3], _ptr(lse), int(raw_splits), int(lat_splits))
-    keep = (q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, cos, sin, q_positions)
+        _ptr(out), *out.stride()[:3], _ptr(lse), int(raw_splits), int(lat_splits), _ptr(bases))
+    keep = (q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, cos, sin, q_positions, bases)
     return a, out, lse, keep
 
 
 def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias=None, up_v_bias=None,
                   block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
                   raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None,
-                  workspace=None):
+                  workspace=None, prepared_bases=True):
     """Fused latent beacon decode for one layer.
 
     q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given),
     raw_k/raw_v [B,Nr,Hkv,D] with RoPE'd K, lat_k [B,Nl,Rk], lat_v [B,Nl,Rv],
     up_k [Hkv*D,Rk], up_v [Hkv*D,Rv].  Returns (out [B,Lq,Hq,D] bf16, lse [B,Hq,Lq]).
     A caller-provided `workspace` (uint8, at least latent_decode_workspace_bytes)
-    makes the call allocation-free, e.g. under HIP graph capture.
+    makes the call allocation-free, e.g. under HIP graph capture.  With
+    block-diagonal bases the query absorption runs on MFMA from per-head bases
+    prepared once per weight (`prepared_bases`, the default).
     """
     a, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
                                      block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
-                                     lat_lengths, raw_splits, lat_splits, out, lse)
+                                     lat_lengths, raw_splits, lat_splits, out, lse, prepared_bases)
     nbytes = lib().slimkv_latent_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
@@ -256,7 +283,7 @@ def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_pos
     [B, Nl] when given) and V, then attend over [beacons ; raw rows]."""
     base, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
                                         block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
-                                        lat_lengths, raw_splits, lat_splits, out, lse)
+                                        lat_lengths, raw_splits, lat_splits, out, lse, prepared_bases=False)
     if beacon_positions is not None:
         beacon_positions = beacon_positions.to(torch.int64)
         beacon_positions = beacon_positions if beacon_positions.stride(-1) == 1 else beacon_positions.contiguous()

@@ -62,12 +62,18 @@ def _run(case, k_rot_bhsd, block_diagonal=True, rope_in_kernel=True, q_rot=None,
     return out, lse
 
 
-@pytest.mark.parametrize('block_diagonal', [True, False])
-def test_config0_shape(device, block_diagonal):
+# (block_diagonal, prepared_bases): block-diagonal bases with the MFMA
+# absorption from prepared per-head bases, the same with the generic prologue,
+# and general (dense) bases.
+VARIANTS = [(True, True), (True, False), (False, True)]
+
+
+@pytest.mark.parametrize('block_diagonal,prepared', VARIANTS)
+def test_config0_shape(device, block_diagonal, prepared):
     """B1, 32/8 heads, d 128, context 4096, t4, 4 sinks + 124 tail, r 32."""
     case = latent_case(batch=1, context=4096, tail=124, seed=0, device=device)
     q_rot, k_rot = _rotated(case)
-    out, lse = _run(case, k_rot, block_diagonal)
+    out, lse = _run(case, k_rot, block_diagonal, prepared_bases=prepared)
     eo, el = _oracle(case, q_rot, k_rot)
     assert_close(to_np(out.transpose(1, 2)), eo, what='out')
     assert_lse_close(to_np(lse), el, what='lse')
@@ -79,10 +85,10 @@ def test_layer_adaptive_ranks(device, rk, rv):
                        device=device)
     q_rot, k_rot = _rotated(case)
     eo, el = _oracle(case, q_rot, k_rot)
-    for bd in (True, False):
-        out, lse = _run(case, k_rot, bd)
-        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd}')
-        assert_lse_close(to_np(lse), el, what=f'lse bd={bd}')
+    for bd, prep in VARIANTS:
+        out, lse = _run(case, k_rot, bd, prepared_bases=prep)
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd} prepared={prep}')
+        assert_lse_close(to_np(lse), el, what=f'lse bd={bd} prepared={prep}')
 
 
 def test_prerotated_query_and_biases(device):
@@ -94,11 +100,15 @@ def test_prerotated_query_and_biases(device):
     bk = (0.5 * torch.randn(case.up_k.shape[0], generator=gen, device=device)).to(torch.bfloat16)
     bv = (0.5 * torch.randn(case.up_v.shape[0], generator=gen, device=device)).to(torch.bfloat16)
     eo, el = _oracle(case, q_rot, k_rot, up_k_bias=bk, up_v_bias=bv)
-    for bd in (True, False):
+    for bd, prep in VARIANTS:
         out, lse = _run(case, k_rot, bd, rope_in_kernel=False, q_rot=q_rot.transpose(1, 2),
-                        up_k_bias=bk, up_v_bias=bv)
-        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd}')
-        assert_lse_close(to_np(lse), el, what=f'lse bd={bd}')
+                        up_k_bias=bk, up_v_bias=bv, prepared_bases=prep)
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd} prepared={prep}')
+        assert_lse_close(to_np(lse), el, what=f'lse bd={bd} prepared={prep}')
+    for prep in (True, False):          # biases with the query rotated in the prologue
+        out, lse = _run(case, k_rot, True, up_k_bias=bk, up_v_bias=bv, prepared_bases=prep)
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out rope prepared={prep}')
+        assert_lse_close(to_np(lse), el, what=f'lse rope prepared={prep}')
 
 
 def test_insertion_step_two_queries(device):
@@ -112,10 +122,10 @@ def test_insertion_step_two_queries(device):
     case.cos, case.sin = rope_tables(1002, 128, 500000.0, device)
     q_rot, k_rot = _rotated(case)
     eo, el = _oracle(case, q_rot, k_rot, lat_causal=True)
-    for bd in (True, False):
-        out, lse = _run(case, k_rot, bd, lat_causal=True)
-        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd}')
-        assert_lse_close(to_np(lse), el, what=f'lse bd={bd}')
+    for bd, prep in VARIANTS:
+        out, lse = _run(case, k_rot, bd, lat_causal=True, prepared_bases=prep)
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'out bd={bd} prepared={prep}')
+        assert_lse_close(to_np(lse), el, what=f'lse bd={bd} prepared={prep}')
 
 
 def test_empty_latent_branch(device):
@@ -142,3 +152,14 @@ def test_batch16_config1_shape_reduced_context(device):
     eo, el = _oracle(case, q_rot, k_rot)
     assert_close(to_np(out.transpose(1, 2)), eo)
     assert_lse_close(to_np(lse), el)
+
+
+def test_prepared_bases_are_the_per_head_transpose(device):
+    from slimkv_amd import kernels
+    case = latent_case(batch=1, context=300, tail=20, rank_k=48, seed=5, device=device)
+    bases = kernels.prepare_latent_bases(case.up_k, 8)
+    torch.cuda.synchronize()
+    w = case.up_k.view(8, 128, 8, 48)
+    want = torch.stack([w[h, :, h, :].t() for h in range(8)])
+    assert torch.equal(bases, want)
+    assert kernels.prepare_latent_bases(case.up_k, 8) is bases          # cached per weight version
