@@ -135,11 +135,18 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-graph', action='store_true', help='time eager launches instead of graph replay')
+    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged'),
+                    help='latent: the headline decode sweep; prefill / recon / paged: the window prefill, '
+                         'reconstruction decode and paged-cache decode workloads')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: the decode path shards by sequence with no exchange, '
               'so multi-GPU runs are not part of this build (use --gpus 1).', file=sys.stderr)
         sys.exit(2)
+    if args.workload != 'latent':
+        from bench_workloads import run_workload
+        print(json.dumps(run_workload(args)), flush=True)
+        return
 
     import torch
     from slimkv_amd import _lib, kernels

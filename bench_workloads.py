@@ -1,0 +1,277 @@
+"""The non-headline workloads of bench.py (`--workload prefill|recon|paged`).
+
+prefill  Window-chunked prefill at batch 4: an 8192-token prompt in 8 windows of
+         1024 raw tokens + 256 beacons (t4), 32 query / 8 KV heads, head_dim 128,
+         4 sinks, per-head beacon rank 32.  A step runs every window: rebuild
+         the history beacons' K/V (MFMA up-projection), compress the window's
+         beacon rows (MFMA down-projection, per-head bases), causal flash
+         attention over [sinks | history | window] (MFMA).  value = attention
+         TFLOP/s over the whole step.
+recon    Reconstruction decode, Qwen2.5-14B layer shape: batch 8, 40 query / 8 KV
+         heads, 32K context at t4 (8192 beacons, rank 32 per head), 4 sinks +
+         128 tail + current token, beacon K rotated at its slot position; 8
+         layers with their own buffers.  value = algorithmic GB/s (latents,
+         raw rows, q/out, weights once) over the step.
+paged    Paged-cache decode: 64 sequences with contexts drawn in [1024, 131072],
+         t8, BeaconPageLayout(16, 8, 256, 256, 1024) pages scattered over a
+         400K-page pool, sinks + a tail of up to 255 raw tokens in raw pages.
+         A step gathers each sequence's beacon and raw rows out of the pages
+         (the restore_memory semantics) and runs the fused latent decode with
+         per-sequence lengths.  value = algorithmic GB/s of the decode inputs.
+"""
+import os
+import time
+
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def _time_steps(torch, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _result(metric, value, unit, args, seconds, dtype, config, **extra):
+    out = {'metric': metric, 'value': round(value, 2), 'unit': unit, 'n_gpus': 1, 'steps': args.steps,
+           'warmup': args.warmup, 'ms_per_step': round(seconds * 1e3, 4), 'higher_is_better': True,
+           'scaling': 'weak', 'vs_baseline': None, 'dtype': dtype, 'data': 'synthetic', 'config': config}
+    out.update(extra)
+    return out
+
+
+# ----------------------------------------------------------------------------- prefill
+
+def prefill(args):
+    import torch
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+    B, HQ, HKV, D, WIN, NB, S, r, WINDOWS = 4, 32, 8, 128, 1024, 256, 4, 32, 8
+    L, R = WIN + NB, HKV * r
+    dev = torch.device('cuda:0')
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    rnd = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(torch.bfloat16)
+    cpu = torch.Generator().manual_seed(args.seed + 1)
+    up = [block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16) for _ in range(2)]
+    down = [block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).t().contiguous().to(dev, torch.bfloat16)
+            for _ in range(2)]                                  # per-head K_full[128] -> r bases [R, Hkv*D]
+    n_max = S + NB * (WINDOWS - 1) + L
+    work_k = torch.zeros(B, n_max, HKV, D, dtype=torch.bfloat16, device=dev)
+    work_v = torch.zeros_like(work_k)
+    latents = [torch.zeros(B, NB * WINDOWS, R, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    qs = [rnd(B, L, HQ, D) for _ in range(WINDOWS)]
+    cur = [(rnd(B, L, HKV, D), rnd(B, L, HKV, D)) for _ in range(WINDOWS)]
+    sinks = rnd(B, S, HKV, D), rnd(B, S, HKV, D)
+    beacon_rows = torch.arange(4, L, 5, device=dev)             # one beacon after every 4 raw tokens
+    out = torch.empty(B, L, HQ, D, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, HQ, L, dtype=torch.float32, device=dev)
+    scale = D ** -0.5
+
+    def keys(w):
+        return L if w == 0 else S + NB * w + L
+
+    def window(w, timed=None):
+        n = keys(w)
+        base = 0 if w == 0 else S + NB * w
+        if w:
+            work_k[:, :S].copy_(sinks[0])
+            work_v[:, :S].copy_(sinks[1])
+            for j, dst in ((0, work_k), (1, work_v)):
+                kernels.reconstruct(latents[j][:, :NB * w], up[j], kv_heads=HKV, out=dst[:, S:S + NB * w],
+                                    block_diagonal=True)
+        work_k[:, base:base + L].copy_(cur[w][0])
+        work_v[:, base:base + L].copy_(cur[w][1])
+        for j in range(2):
+            kernels.down_project(cur[w][j].view(B, L, HKV * D), down[j], beacon_rows, blocks=HKV,
+                                 out=latents[j][:, NB * w:NB * (w + 1)])
+        if timed:
+            timed[0].record()
+        kernels.prefill_attention(qs[w], work_k[:, :n], work_v[:, :n], scale, True, out=out, lse=lse)
+        if timed:
+            timed[1].record()
+
+    def step():
+        for w in range(WINDOWS):
+            window(w)
+
+    seconds = _time_steps(torch, step, args.steps, args.warmup)
+    pairs = [sum(min(keys(w), i + keys(w) - L + 1) for i in range(L)) for w in range(WINDOWS)]
+    flops = [p * 4 * D * HQ * B for p in pairs]
+    # attention kernel alone, events on the launch stream
+    evs = [_events(torch) for _ in range(WINDOWS)]
+    kernel_s = []
+    for _ in range(3):
+        torch.cuda._sleep(50_000_000)
+        for w in range(WINDOWS):
+            window(w, evs[w])
+        torch.cuda.synchronize()
+        kernel_s.append(sum(a.elapsed_time(b) for a, b in evs) * 1e-3)
+    kernel_s = sorted(kernel_s)[1]
+    achieved = sum(flops) / kernel_s / 1e12
+    result = _result('prefill attention TFLOP/s, 8 windows of 1024+256, b4, 32/8 heads', sum(flops) / seconds / 1e12,
+                     'TFLOP/s', args, seconds, 'bf16',
+                     {'workload': 'window prefill, 8192-token prompt, t4, per-head rank 32', 'batch': B,
+                      'window': WIN, 'beacons_per_window': NB, 'windows': WINDOWS, 'q_heads': HQ, 'kv_heads': HKV,
+                      'head_dim': D, 'sinks': S},
+                     roofline={'bound': 'mfma', 'achieved': round(achieved, 1), 'peak': MFMA_BF16_PEAK_TFLOPS,
+                               'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                               'traffic': None, 'kernel': 'prefill_kernel', 'kernel_ms': round(kernel_s * 1e3, 3)},
+                     attention_tflop=round(sum(flops) / 1e12, 4))
+    if not args.no_cpu:
+        result['cpu_baseline'] = _prefill_cpu(torch, qs[1], work_k, work_v, keys(1), scale, pairs[1] * 4 * D * HQ * B)
+    return result
+
+
+def _prefill_cpu(torch, q, k, v, n, scale, flops):
+    """Reference eager semantics in fp32 on the host for window 1 (torch
+    restatement of the causal attention)."""
+    threads = int(os.environ.get('OMP_NUM_THREADS', '0')) or len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    qc = q.float().cpu().transpose(1, 2)                       # [B, H, L, D]
+    kc = k[:, :n].float().cpu().transpose(1, 2)
+    vc = v[:, :n].float().cpu().transpose(1, 2)
+    g = qc.shape[1] // kc.shape[1]
+    kc, vc = kc.repeat_interleave(g, 1), vc.repeat_interleave(g, 1)
+    L = qc.shape[2]
+    mask = torch.arange(n)[None, :] > (torch.arange(L)[:, None] + n - L)
+    t0 = time.perf_counter()
+    s = (qc @ kc.transpose(-1, -2)) * scale
+    s.masked_fill_(mask, float('-inf'))
+    torch.softmax(s, -1) @ vc
+    dt = time.perf_counter() - t0
+    return {'value': round(flops / dt / 1e12, 4), 'unit': 'TFLOP/s', 'cores': threads, 'kind': 'port',
+            'sample': f'window 1 (1280 queries x {n} keys, b4, 32 heads), torch fp32 eager, one run {dt:.1f}s'}
+
+
+# ----------------------------------------------------------------------------- reconstruction decode
+
+def recon(args):
+    import torch
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
+    B, HQ, HKV, D, NB, S, T, r, LAYERS = 8, 40, 8, 128, 8192, 4, 128, 32, 8
+    R, RAW, CTX = HKV * r, S + T + 1, 32768
+    dev = torch.device('cuda:0')
+    cos, sin = rope_tables(CTX + 1, D, 500000.0, dev)
+    layers = []
+    for i in range(LAYERS):
+        gen = torch.Generator(device=dev).manual_seed(args.seed * 100 + i)
+        rnd = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(torch.bfloat16)
+        cpu = torch.Generator().manual_seed(args.seed * 100 + i + 50)
+        layers.append(dict(
+            q=rnd(B, 1, HQ, D), raw_k=rnd(B, RAW, HKV, D), raw_v=rnd(B, RAW, HKV, D),
+            lat_k=rnd(B, NB, R), lat_v=rnd(B, NB, R),
+            up_k=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+            up_v=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+            out=torch.empty(B, 1, HQ, D, dtype=torch.bfloat16, device=dev)))
+    qpos = torch.full((B, 1), CTX, dtype=torch.long, device=dev)
+    bpos = (S + torch.arange(NB, device=dev))[None].expand(B, -1).contiguous()   # beacon slot positions
+    scale = D ** -0.5
+
+    def step():
+        for L in layers:
+            kernels.recon_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'],
+                                 scale, beacon_positions=bpos, block_diagonal=True, q_positions=qpos, cos=cos,
+                                 sin=sin, out=L['out'])
+
+    seconds = _time_steps(torch, step, args.steps, args.warmup)
+    per_layer = B * (NB * 2 * R * 2 + RAW * HKV * D * 2 * 2 + 2 * HQ * D * 2) + 2 * HKV * D * R * 2
+    materialized = per_layer + 2 * 2 * B * NB * HKV * D * 2        # the rebuilt K/V written and read once
+    gbps = per_layer * LAYERS / seconds / 1e9
+    return _result('reconstruction decode GB/s, Qwen2.5-14B layer shape b8 ctx32K t4', gbps, 'GB/s', args, seconds,
+                   'bf16', {'workload': 'reconstruction decode, 8-layer sweep, 40/8 heads, rank 32, beacon K-RoPE',
+                            'batch': B, 'beacons': NB, 'raw_tokens': RAW},
+                   hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), us_per_layer=round(seconds / LAYERS * 1e6, 2),
+                   bytes_per_layer=per_layer, bytes_per_layer_materialized=materialized,
+                   materialized_gbps=round(materialized * LAYERS / seconds / 1e9, 1))
+
+
+# ----------------------------------------------------------------------------- paged decode
+
+def paged(args):
+    import random
+    import torch
+    from slimkv_amd import _lib, kernels
+    from slimkv_amd.paged_cache import BeaconPageLayout, BeaconPages, RawPages
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
+    NSEQ, HQ, HKV, D, RATIO, S, r, POOL = 64, 32, 8, 128, 8, 4, 32, 400_000
+    R = HKV * r
+    rng = random.Random(args.seed)
+    ctx = [rng.randint(1024, 131072) for _ in range(NSEQ)]
+    tails = [rng.randint(0, 255) for _ in range(NSEQ)]
+    nb = [c // RATIO for c in ctx]
+    layout = BeaconPageLayout(16, RATIO, R, R, HKV * D)
+    dev = torch.device('cuda:0')
+    pool = torch.empty(POOL, layout.page_elements, dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    for i in range(0, POOL, 50_000):
+        pool[i:i + 50_000].normal_(generator=gen)
+    pages_needed = [(n + layout.slots - 1) // layout.slots for n in nb]
+    perm = torch.randperm(POOL, generator=torch.Generator().manual_seed(args.seed))
+    width = max(pages_needed)
+    tables = torch.full((NSEQ, width), 0, dtype=torch.long)
+    off = 0
+    for sidx, n in enumerate(pages_needed):
+        tables[sidx, :n] = perm[off:off + n]
+        off += n
+    tables = tables.to(dev)
+    raw_count = [S + t + 1 for t in tails]                       # sinks + tail + current token
+    raw_blocks = (max(raw_count) + 15) // 16
+    raw_pool = torch.randn(NSEQ * raw_blocks, 16, 2, HKV, D, generator=gen, device=dev).to(torch.bfloat16)
+    raw_tables = torch.randperm(NSEQ * raw_blocks, generator=torch.Generator().manual_seed(args.seed + 1))
+    raw_tables = raw_tables.view(NSEQ, raw_blocks).to(dev)
+    beacons = BeaconPages(pool, layout)
+    raw = RawPages(raw_pool)
+    lat_len = torch.tensor(nb, dtype=torch.int32, device=dev)
+    raw_len = torch.tensor(raw_count, dtype=torch.int32, device=dev)
+    cpu = torch.Generator().manual_seed(args.seed + 2)
+    up_k = block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16)
+    up_v = block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16)
+    q = torch.randn(NSEQ, 1, HQ, D, generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty(NSEQ, 1, HQ, D, dtype=torch.bfloat16, device=dev)
+    scale = D ** -0.5
+    max_nb, max_raw = max(nb), max(raw_count)
+    lat_k = torch.zeros(NSEQ, max_nb, R, dtype=torch.bfloat16, device=dev)
+    lat_v = torch.zeros_like(lat_k)
+    raw_k = torch.zeros(NSEQ, HKV, max_raw, D, dtype=torch.bfloat16, device=dev)
+    raw_v = torch.zeros_like(raw_k)
+    lib = _lib.lib()
+    split_ev = _events(torch)
+
+    def gather():
+        beacons._move(tables, 0, lat_k, lat_v, False, lat_len)
+        kernels.raw_pages(raw.pages, raw_tables, raw_k, raw_v, start=0, count=max_raw, to_pages=False,
+                          lengths=raw_len)
+
+    def decode():
+        kernels.latent_decode(q, raw_k.transpose(1, 2), raw_v.transpose(1, 2), lat_k, lat_v, up_k, up_v, scale,
+                              block_diagonal=True, raw_lengths=raw_len, lat_lengths=lat_len, out=out)
+
+    def step():
+        gather()
+        decode()
+
+    seconds = _time_steps(torch, step, args.steps, args.warmup)
+    decode_s = _time_steps(torch, decode, args.steps, args.warmup)
+    algo = sum(n * 2 * R * 2 + c * HKV * D * 2 * 2 for n, c in zip(nb, raw_count)) + NSEQ * 2 * HQ * D * 2 \
+        + 2 * HKV * D * R * 2
+    gbps = algo / seconds / 1e9
+    return _result('paged latent decode GB/s, 64 seqs ctx U[1K,128K] t8', gbps, 'GB/s', args, seconds, 'bf16',
+                   {'workload': 'paged decode: page gather (restore) + fused latent decode, t8, rank 32',
+                    'sequences': NSEQ, 'page_layout': [16, RATIO, R, R, HKV * D], 'pool_pages': POOL,
+                    'beacons_total': sum(nb)},
+                   hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), bytes_per_step=algo,
+                   decode_only_gbps=round(algo / decode_s / 1e9, 1), decode_only_ms=round(decode_s * 1e3, 4))
+
+
+def run_workload(args):
+    return {'prefill': prefill, 'recon': recon, 'paged': paged}[args.workload](args)
