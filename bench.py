@@ -37,6 +37,14 @@ RAW = SINKS + TAIL + 1              # sinks + tail + current token
 RANKS = (16, 32, 48)
 
 
+# HBM bytes per launch of the split kernel of a rank-r layer, from two rocprofv3
+# --pmc passes (FETCH_SIZE, WRITE_SIZE) over this workload, scaled by the same
+# counters on a plain 256 MiB copy (FETCH_SIZE reads half the bytes read,
+# WRITE_SIZE the bytes written): 2 x fetch + write.
+SPLIT_TRAFFIC_BYTES = {32: 157_975_600 * 1024 // 1000, 16: 85_373_600 * 1024 // 1000}
+TRAFFIC_SOURCE = 'rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, split_kernel, scaled by a 256 MiB copy'
+
+
 def layer_bytes(rk, rv):
     """Algorithmic bytes of one layer step: latent rows, raw rows, q in, out,
     and the two up-projection weights once."""
@@ -222,7 +230,8 @@ def main():
     achieved = split_kernel_bytes(dom, dom) / dur_avg / 1e9
     all_split = sum(sum(v) / len(v) * ranks.count(r) for r, v in durations.items())
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
-                'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
+                'frac': round(achieved / HBM_PEAK_GBPS, 4),
+                'traffic': SPLIT_TRAFFIC_BYTES.get(dom), 'traffic_source': TRAFFIC_SOURCE,
                 'kernel': f'split_kernel (rank-{dom} layers)',
                 'avg_us': round(dur_avg * 1e6, 2),
                 'split_kernel_sweep_frac': round(all_split / (elapsed / args.steps), 3),
