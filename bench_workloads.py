@@ -185,7 +185,9 @@ def recon(args):
 
     seconds = _time_steps(torch, step, args.steps, args.warmup)
     per_layer = B * (NB * 2 * R * 2 + RAW * HKV * D * 2 * 2 + 2 * HQ * D * 2) + 2 * HKV * D * R * 2
-    materialized = per_layer + 2 * 2 * B * NB * HKV * D * 2        # the rebuilt K/V written and read once
+    # the rebuilt (rotated) beacon K is written and read once; V stays latent and is
+    # lifted after the softmax-weighted sum
+    materialized = per_layer + 2 * B * NB * HKV * D * 2
     gbps = per_layer * LAYERS / seconds / 1e9
     return _result('reconstruction decode GB/s, Qwen2.5-14B layer shape b8 ctx32K t4', gbps, 'GB/s', args, seconds,
                    'bf16', {'workload': 'reconstruction decode, 8-layer sweep, 40/8 heads, rank 32, beacon K-RoPE',

@@ -1328,8 +1328,22 @@ namespace {
 
 struct ReconPlan {
     SegPlan raw, rec;
+    int v_latent, v_width;   // V stays latent (width v_width per KV head) and is lifted in the combine
     size_t qrot_off, k_off, v_off, rml_off, racc_off, bml_off, bacc_off, total;
 };
+
+// V is linear in its latent, so sum_n p_n (U_V l_n + b) = U_V (sum_n p_n l_n) + b sum_n p_n:
+// the split kernel can attend over the latent rows and the combine lifts once per
+// (b, head).  K cannot follow when beacon keys are rotated after the
+// up-projection, so only V takes this route; it needs the latent decode's layout.
+bool recon_v_latent(const slimkv_latent_decode_args* a) {
+    if (a->lat_keys <= 0 || !a->lat_v) return false;
+    const bool bd = a->block_diagonal != 0;
+    if (bd && a->rank_v % a->kv_heads) return false;
+    const int64_t w = bd ? a->rank_v / a->kv_heads : a->rank_v;
+    return w > 0 && w <= a->head_dim && aligned8(w) && aligned8(a->rank_v) && aligned8(a->lv_sb) &&
+           aligned8(a->lv_sn) && ptr_aligned16(a->lat_v) && ptr_aligned16(a->up_v);
+}
 
 int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     const slimkv_latent_decode_args* a = &r->base;
@@ -1348,9 +1362,11 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     const int raw_req = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
     p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req, 0);
     size_t off = 0;
+    p->v_latent = recon_v_latent(a) ? 1 : 0;
+    p->v_width = p->v_latent ? (int)(a->block_diagonal ? a->rank_v / Hkv : a->rank_v) : (int)D;
     p->qrot_off = off; off = align256(off + (size_t)B * Lq * Hq * D * 2);
     p->k_off = off; off = align256(off + (size_t)B * nl * Hkv * D * 2);
-    p->v_off = off; off = align256(off + (size_t)B * nl * Hkv * D * 2);
+    p->v_off = off; off = align256(off + (p->v_latent ? 0 : (size_t)B * nl * Hkv * D * 2));
     const size_t rr = (size_t)B * Hq * Lq * p->raw.splits;
     p->rml_off = off; off = align256(off + rr * 8);
     p->racc_off = off; off = align256(off + rr * D * 4);
@@ -1399,9 +1415,9 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
     rc = check_hip(hipGetLastError(), "prologue kernel launch");
     if (rc != SLIMKV_OK) return rc;
 
-    // 2. rebuild beacon K (optionally RoPE'd) and V: [B, Nl, Hkv, D]
+    // 2. rebuild beacon K (optionally RoPE'd) and, unless it stays latent, V: [B, Nl, Hkv, D]
     if (has_lat) {
-        for (int kind = 0; kind < 2; ++kind) {
+        for (int kind = 0; kind < (p.v_latent ? 1 : 2); ++kind) {
             slimkv_reconstruct_args ra{};
             ra.latent = kind ? a->lat_v : a->lat_k;
             ra.l_sb = kind ? a->lv_sb : a->lk_sb;
@@ -1439,7 +1455,13 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
         Seg& bs = prm.seg[0];
         bs = rs;
         bs.k = kbuf; bs.k_sb = (int64_t)a->lat_keys * Hkv * D; bs.k_sn = (int64_t)Hkv * D; bs.k_sh = D;
-        bs.v = vbuf; bs.v_sb = bs.k_sb; bs.v_sn = bs.k_sn; bs.v_sh = D;
+        if (p.v_latent) {
+            bs.v = static_cast<const uint16_t*>(a->lat_v); bs.v_sb = a->lv_sb; bs.v_sn = a->lv_sn;
+            bs.v_sh = a->block_diagonal ? p.v_width : 0;
+            bs.wv = p.v_width; bs.wown = p.v_width;
+        } else {
+            bs.v = vbuf; bs.v_sb = bs.k_sb; bs.v_sn = bs.k_sn; bs.v_sh = D;
+        }
         bs.seqlens = a->lat_lengths; bs.n = (int)a->lat_keys; bs.causal = a->lat_causal ? 1 : 0;
         bs.tiles = p.rec.tiles; bs.cols = p.rec.cols; bs.splits = p.rec.splits; bs.rows_per_split = p.rec.rows_per_split;
         bs.part_ml = reinterpret_cast<float*>(ws + p.bml_off); bs.part_acc = reinterpret_cast<float*>(ws + p.bacc_off);
@@ -1453,13 +1475,20 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
     CombineParams cp{};
     cp.a_ml = rs.part_ml; cp.a_acc = rs.part_acc; cp.a_splits = rs.splits; cp.a_w = D;
     if (has_lat) {
-        cp.b_ml = prm.seg[0].part_ml; cp.b_acc = prm.seg[0].part_acc; cp.b_splits = prm.seg[0].splits; cp.b_w = D;
-        cp.up_v = nullptr;
+        cp.b_ml = prm.seg[0].part_ml; cp.b_acc = prm.seg[0].part_acc; cp.b_splits = prm.seg[0].splits;
+        cp.b_w = prm.seg[0].wown;
+        if (p.v_latent) {
+            cp.up_v = static_cast<const uint16_t*>(a->up_v); cp.up_v_ld = a->rank_v;
+            cp.up_v_bias = static_cast<const uint16_t*>(a->up_v_bias);
+            cp.blockdiag = a->block_diagonal ? 1 : 0;
+        } else {
+            cp.up_v = nullptr;
+        }
     }
     cp.B = B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hkv; cp.D = D;
     cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
     cp.lse = a->lse;
-    hipLaunchKernelGGL(combine_kernel, dim3(B * Hq * Lq), dim3(kCombineThreads), 0, st, cp);
+    launch_combine(cp, B * Hq * Lq, st);
     return check_hip(hipGetLastError(), "combine kernel launch");
 }
 

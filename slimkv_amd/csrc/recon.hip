@@ -99,6 +99,99 @@ recon_kernel(ReconParams p) {
     }
 }
 
+// Streaming variant for narrow contractions (kw <= 64): the wavefront keeps its
+// head's W tile (A operand, 128 x kw) in registers and walks 16-row tiles with
+// the next tile's latent rows already in flight, so W is read once per
+// wavefront instead of once per tile.  Same epilogue as recon_kernel.
+template <int KSTEPS>
+__global__ void __launch_bounds__(kReconWaves * 64)
+recon_stream_kernel(ReconParams p, int segs) {
+    constexpr int D = 128;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int h = blockIdx.x % p.Hkv;
+    const int seg = (blockIdx.x / p.Hkv) % segs;
+    const int b = blockIdx.x / (p.Hkv * segs);
+    const int tiles = (p.n + 15) / 16;
+    const int stride = segs * kReconWaves;
+    const int k_lo = p.blockdiag ? h * p.k_lo_step : 0;
+    u32x2 wa[8][KSTEPS];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+            wa[t][ks] = *reinterpret_cast<const u32x2*>(p.w + ((int64_t)h * D + 16 * t + col) * p.w_ld + k_lo + 16 * ks +
+                                                        4 * grp);
+    float bias[8][4];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            bias[t][i] = p.bias ? bf16_to_f32(p.bias[(int64_t)h * D + 16 * t + 4 * grp + i]) : 0.f;
+    const uint16_t* lbase = p.latent + (int64_t)b * p.l_sb + k_lo + 4 * grp;
+    auto load_rows = [&](u32x2 (&lr)[KSTEPS], int tile) {
+        const int row = min(tile * 16 + col, p.n - 1);
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) lr[ks] = *reinterpret_cast<const u32x2*>(lbase + (int64_t)row * p.l_sn + 16 * ks);
+    };
+    int tile = seg * kReconWaves + wave;
+    if (tile >= tiles) return;
+    u32x2 cur[KSTEPS], nxt[KSTEPS];
+    load_rows(cur, tile);
+    for (; tile < tiles; tile += stride) {
+        const bool more = tile + stride < tiles;
+        load_rows(nxt, more ? tile + stride : tile);
+        v4f acc[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+            const v4s bop = as_v4s(cur[ks].x, cur[ks].y);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] = mfma16(as_v4s(wa[t][ks].x, wa[t][ks].y), bop, acc[t]);
+        }
+        const int row = tile * 16 + col;
+        if (row < p.n) {
+            float x[8][4];
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[t][i] = round_bf16(p.bias ? acc[t][i] + bias[t][i] : acc[t][i]);
+            if (p.positions) {
+                const int64_t pos = clamp_i64(p.positions[(int64_t)b * p.pos_sb + row], 0, p.rope_rows - 1);
+                const float* cr = p.cos + pos * D;
+                const float* sr = p.sin + pos * D;
+                float y[8][4];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const float4 c4 = *reinterpret_cast<const float4*>(cr + 16 * t + 4 * grp);
+                    const float4 s4 = *reinterpret_cast<const float4*>(sr + 16 * t + 4 * grp);
+                    const float cv[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float partner = t < 4 ? -x[t + 4][i] : x[t - 4][i];
+                        y[t][i] = round_bf16(round_bf16(x[t][i] * round_bf16(cv[i])) + round_bf16(partner * round_bf16(sv[i])));
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) x[t][i] = y[t][i];
+            }
+            const int64_t dst = p.dst_rows ? p.dst_rows[row] : row;
+            uint16_t* orow = p.out + (int64_t)b * p.o_sb + dst * p.o_sn + (int64_t)h * p.o_sh;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t lo = f32_to_bf16(x[t][0]) | (f32_to_bf16(x[t][1]) << 16);
+                const uint32_t hi = f32_to_bf16(x[t][2]) | (f32_to_bf16(x[t][3]) << 16);
+                *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * grp) = u32x2{lo, hi};
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) cur[ks] = nxt[ks];
+    }
+}
+
 namespace {
 bool al4(int64_t x) { return (x & 3) == 0; }
 bool pal8(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7) == 0; }
@@ -106,6 +199,12 @@ bool pal8(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7) == 0;
 template <int K>
 hipError_t launch_recon(const ReconParams& p, int grid, hipStream_t st) {
     hipLaunchKernelGGL((recon_kernel<K>), dim3(grid), dim3(kReconWaves * 64), 0, st, p);
+    return hipGetLastError();
+}
+
+template <int K>
+hipError_t launch_stream(const ReconParams& p, int segs, hipStream_t st) {
+    hipLaunchKernelGGL((recon_stream_kernel<K>), dim3(p.B * p.Hkv * segs), dim3(kReconWaves * 64), 0, st, p, segs);
     return hipGetLastError();
 }
 }  // namespace
@@ -133,9 +232,25 @@ int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
     p.positions = a->positions; p.pos_sb = a->pos_sb;
     p.B = (int)a->batch; p.n = (int)a->rows; p.R = (int)a->rank; p.Hkv = (int)a->kv_heads;
     p.blockdiag = bd ? 1 : 0; p.k_lo_step = (int)kw;
+    hipError_t e;
+    const bool tables16 = !a->positions || (((reinterpret_cast<uintptr_t>(a->cos) | reinterpret_cast<uintptr_t>(a->sin)) & 15) == 0);
+    if (kw <= 64 && tables16) {
+        // streaming kernel: about 1024 workgroups, each wavefront at least one tile
+        const int row_tiles = (p.n + 15) / 16;
+        const int64_t heads = (int64_t)p.B * p.Hkv;
+        const int segs = (int)std::max<int64_t>(1, std::min<int64_t>((row_tiles + kReconWaves - 1) / kReconWaves,
+                                                                     (1024 + heads - 1) / heads));
+        if ((int64_t)p.B * p.Hkv * segs > 0x7fffffff) return fail(SLIMKV_EINVAL, "reconstruction grid too large");
+        switch (kw / 16) {
+            case 1: e = launch_stream<1>(p, segs, st); break;
+            case 2: e = launch_stream<2>(p, segs, st); break;
+            case 3: e = launch_stream<3>(p, segs, st); break;
+            default: e = launch_stream<4>(p, segs, st); break;
+        }
+        return check_hip(e, "reconstruction kernel launch");
+    }
     const int tiles = (p.n + 16 * kReconWaves - 1) / (16 * kReconWaves);
     const int grid = p.B * tiles * p.Hkv;
-    hipError_t e;
     switch (kw / 16) {
         case 1: e = launch_recon<1>(p, grid, st); break;
         case 2: e = launch_recon<2>(p, grid, st); break;

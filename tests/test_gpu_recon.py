@@ -38,11 +38,16 @@ def _neighbour_of_exact(actual, exact, rounded, abs_terms):
     assert (a == np.asarray(rounded, np.float64)).mean() > 0.98
 
 
-@pytest.mark.parametrize('bd,rank,bias', [(True, 32, False), (True, 48, True), (False, 256, True), (True, 16, False)])
-def test_reconstruct_matches_oracle_gemm(device, bd, rank, bias):
+@pytest.mark.parametrize('bd,rank,bias,B,n', [(True, 32, False, 2, 203), (True, 48, True, 2, 203),
+                                              (False, 256, True, 2, 203), (True, 16, False, 2, 203),
+                                              (True, 32, True, 4, 4099), (True, 64, False, 3, 1111)])
+def test_reconstruct_matches_oracle_gemm(device, bd, rank, bias, B, n):
+    """Per-head widths up to 64 take the streaming kernel (several 16-row tiles per
+    wavefront once B * Hkv * rows / 64 exceeds its workgroup budget, ragged last
+    tile); wider contractions the per-tile kernel."""
     from slimkv_amd import kernels
-    gen = torch.Generator(device=device).manual_seed(rank)
-    B, n, Hkv, D = 2, 203, 8, 128
+    gen = torch.Generator(device=device).manual_seed(rank + n)
+    Hkv, D = 8, 128
     R = Hkv * rank if bd else rank
     lat = torch.randn(B, n, R, generator=gen, device=device).to(torch.bfloat16)
     if bd:
@@ -60,10 +65,11 @@ def test_reconstruct_matches_oracle_gemm(device, bd, rank, bias):
     _neighbour_of_exact(to_np(out).transpose(0, 2, 1, 3), exact, rounded, abs_terms)
 
 
-def test_reconstruct_scatter_and_rope_epilogue(device):
+@pytest.mark.parametrize('n', [37, 4099])
+def test_reconstruct_scatter_and_rope_epilogue(device, n):
     from slimkv_amd import kernels
     gen = torch.Generator(device=device).manual_seed(7)
-    B, n, Hkv, D, r = 2, 37, 8, 128, 32
+    B, Hkv, D, r = 2, 8, 128, 32
     lat = torch.randn(B, n, Hkv * r, generator=gen, device=device).to(torch.bfloat16)
     w = block_diagonal([orthonormal_columns(D, r, torch.Generator().manual_seed(10 + i)) for i in range(Hkv)])
     w = w.to(device, torch.bfloat16)
@@ -144,12 +150,19 @@ def test_recon_decode_qwen14b_layer_shape(device, beacon_rope):
     assert_lse_close(to_np(lse), lse_e)
 
 
-def test_recon_decode_insertion_step_with_biases_general_weights(device):
+@pytest.mark.parametrize('rank', [256, 64])
+def test_recon_decode_insertion_step_with_biases_general_weights(device, rank):
+    """General (not block-diagonal) bases: rank 256 rebuilds V, rank 64 keeps V
+    latent (shared by every head) and lifts it in the combine."""
     from slimkv_amd import kernels
     case = latent_case(batch=2, context=900, tail=40, seed=5, device=device)
     gen = torch.Generator(device=device).manual_seed(6)
-    case.up_k = (torch.randn(1024, 256, generator=gen, device=device) / 16).to(torch.bfloat16)
-    case.up_v = (torch.randn(1024, 256, generator=gen, device=device) / 16).to(torch.bfloat16)
+    if rank != case.lat_k.shape[-1]:
+        shape = case.lat_k.shape[:-1] + (rank,)
+        case.lat_k = torch.randn(shape, generator=gen, device=device).to(torch.bfloat16)
+        case.lat_v = torch.randn(shape, generator=gen, device=device).to(torch.bfloat16)
+    case.up_k = (torch.randn(1024, rank, generator=gen, device=device) / rank ** 0.5).to(torch.bfloat16)
+    case.up_v = (torch.randn(1024, rank, generator=gen, device=device) / rank ** 0.5).to(torch.bfloat16)
     bk = (0.3 * torch.randn(1024, generator=gen, device=device)).to(torch.bfloat16)
     bv = (0.3 * torch.randn(1024, generator=gen, device=device)).to(torch.bfloat16)
     case.q = torch.randn(2, 2, 32, 128, generator=gen, device=device).to(torch.bfloat16)
