@@ -127,6 +127,36 @@ size_t slimkv_latent_decode_workspace(const slimkv_latent_decode_args* a);
 int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Paged latent decode: slimkv_latent_decode with the beacon rows read straight
+ * out of beacon pages, no restore/gather step.  Replaces the page gather of
+ *   restore_memory (slimkv/vllm_plugin/paged_model.py:36-52, through
+ *   BeaconPages.read, slimkv/vllm_plugin/paged_cache.py:60-87) followed by the
+ *   latent decode of the gathered rows (slimkv/llama3/fa2_decode.py:77-166).
+ * Page format (BeaconPageLayout, paged_cache.py:27-44): page = [sink_elements
+ * | slots x (rank_k + rank_v)] bf16; beacon i of sequence b sits in page
+ * table[b * t_sb + i / slots] (t_cols entries per row, at least
+ * ceil(lat_keys / slots), like the reference's IndexError) at column sink_elements + (i % slots) *
+ * (rank_k + rank_v), K first, then V.  Page ids are clamped into
+ * [0, num_pages).  base.lat_k / lat_v and their strides are ignored;
+ * base.lat_lengths (beacons per sequence) is required and base.lat_keys is
+ * the largest count.  rows_total: the sum of lat_lengths when the host knows
+ * it (sizes the key splits; 0 = unknown), never needed for correctness.
+ * With the same base.lat_splits the result is bit-identical to gathering the
+ * rows and calling slimkv_latent_decode.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_paged_latent_decode_args {
+    slimkv_latent_decode_args base;
+    const void* pages; int64_t num_pages, page_stride;
+    const int64_t* table; int64_t t_sb, t_cols;
+    int64_t slots, sink_elements;
+    int64_t rows_total;
+} slimkv_paged_latent_decode_args;
+
+size_t slimkv_paged_latent_decode_workspace(const slimkv_paged_latent_decode_args* a);
+int slimkv_paged_latent_decode(const slimkv_paged_latent_decode_args* a, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* One-time re-layout of block-diagonal K bases for slimkv_latent_decode (no
  * counterpart in the reference, whose project_query reads U_K as stored,
  * slimkv/llama3/fa2_decode.py:41-46): out[h, c, d] = up_k[h*D + d, h*r + c]

@@ -77,6 +77,13 @@ ReconDecodeArgs = _struct('slimkv_recon_decode_args', [
     ('beacon_positions', c_ptr), ('bpos_sb', c_i64),
 ])
 
+PagedLatentDecodeArgs = _struct('slimkv_paged_latent_decode_args', [
+    ('base', LatentDecodeArgs),
+    ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
+    ('table', c_ptr), *_i64s('t_sb', 't_cols'),
+    *_i64s('slots', 'sink_elements', 'rows_total'),
+])
+
 RopeDecodeArgs = _struct('slimkv_rope_decode_args', [
     ('q', c_ptr), *_i64s('q_sb', 'q_sh', 'q_ss'),
     ('k', c_ptr), *_i64s('k_sb', 'k_sh', 'k_ss'),
@@ -156,6 +163,9 @@ SIGNATURES = {
     'slimkv_attention_forward': (ctypes.c_int, [ctypes.POINTER(AttentionArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(LatentDecodeArgs)]),
     'slimkv_latent_decode': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_paged_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(PagedLatentDecodeArgs)]),
+    'slimkv_paged_latent_decode': (ctypes.c_int, [ctypes.POINTER(PagedLatentDecodeArgs), c_ptr, ctypes.c_size_t,
+                                                  c_ptr]),
     'slimkv_prepare_latent_bases': (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
     'slimkv_reconstruct': (ctypes.c_int, [ctypes.POINTER(ReconstructArgs), c_ptr]),
     'slimkv_recon_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(ReconDecodeArgs)]),
@@ -170,7 +180,7 @@ SIGNATURES = {
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class SlimKVError(RuntimeError):

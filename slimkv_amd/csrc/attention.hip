@@ -53,6 +53,13 @@ struct Seg {
     float* part_acc;                                 // [B][Hq*Lq][splits][wown]
     int wown;
     int nwg;
+    // Paged rows (PAGED instances): row i of batch b starts at
+    // k / v + clamp(table[b][i / slots]) * page_stride + (i % slots) * k_sn.
+    const int64_t* table; int64_t t_sb, page_stride, num_pages;
+    int slots, slots_shift;                          // slots_shift = log2(slots) or -1
+    // Compact schedule: workgroup items enumerate only the non-empty splits of
+    // each batch entry (needs seqlens); items past the last one exit at once.
+    int compact, batch;
 };
 
 struct SplitParams {
@@ -161,11 +168,87 @@ __device__ __forceinline__ void load_tile(TileRegs<KS>& t, const uint16_t* kbase
     }
 }
 
+// Compact schedule: item -> (b, s) over the non-empty splits of every batch
+// entry, splits of b = ceil(len_b / rps).  Wave-uniform; false past the end.
+__device__ __forceinline__ bool locate_split(int item, const int32_t* lens, int B, int n, int rps, int& b, int& s) {
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+        const int bi = b0 + lane;
+        int len = bi < B ? lens[bi] : 0;
+        len = len < 0 ? 0 : (len > n ? n : len);
+        const int cnt = (len + rps - 1) / rps;
+        int inc = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += y;
+        }
+        const int tot = __shfl(inc, 63, 64);
+        if (item < base + tot) {
+            const unsigned long long m = __ballot(base + inc > item);
+            const int first = __ffsll(m) - 1;
+            const int excl = __shfl(inc - cnt, first, 64);
+            b = b0 + first;
+            s = item - base - excl;
+            return true;
+        }
+        base += tot;
+    }
+    return false;
+}
+
+// Page ids of one tile's rows for the lanes' K row and V pieces (PAGED): the
+// low words of the int64 table entries (the host limits pools to 2^31 pages;
+// any other value is clamped into the pool like an out-of-range id).
+template <int KS>
+struct TilePages {
+    int32_t k;
+    int32_t v[KS / 2];
+};
+
+// Paged variant of load_tile: the same lane/piece mapping, each row's base
+// taken from its page id.  Any page id is clamped into the pool, so every
+// address is inside it whatever the table holds.
+template <int KS>
+__device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages<KS>& pg, const Seg& sg,
+                                                const uint16_t* kpage, const uint16_t* vpage, int r0, int r_end,
+                                                int last_valid, int span_k, int span_v, int col, int grp, int lane,
+                                                bool act) {
+    constexpr int VT = KS;
+    auto row_base = [&](int32_t pid, int row) -> int64_t {
+        pid = pid < 0 ? 0 : (pid >= sg.num_pages ? (int32_t)sg.num_pages - 1 : pid);
+        const int r = min(row, last_valid);
+        const int slot = sg.slots_shift >= 0 ? (r & (sg.slots - 1)) : r % sg.slots;
+        return pid * sg.page_stride + (int64_t)slot * sg.k_sn;
+    };
+    {
+        const int row = r0 + col;
+        const bool rv = act && row < r_end;
+        const uint16_t* src = kpage + row_base(pg.k, row);
+#pragma unroll
+        for (int c = 0; c < KS / 2; ++c) {
+            const int kk = 32 * c + 8 * grp;
+            const bool ok = rv && kk + 8 <= span_k;
+            t.k[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src + (ok ? kk : 0)));
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < VT / 2; ++c) {
+        const int p = 64 * c + lane;
+        const int row = r0 + p / (2 * VT);
+        const int pc = p % (2 * VT);
+        const bool ok = act && row < r_end && 8 * pc + 8 <= span_v;
+        const uint16_t* src = vpage + row_base(pg.v[c], row) + (ok ? 8 * pc : 0);
+        t.v[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src));
+    }
+}
+
 // A workgroup owns (batch b, group of 4 tile slots, key split s); a slot is a
 // (KV head, column tile) pair and each wave takes one slot.  The four waves
 // therefore stream the same keys' rows at the same time (whole DRAM pages),
 // never exchange data, and write their own partials.
-template <int KS, bool PIPE>
+template <int KS, bool PIPE, bool PAGED = false>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int Hq,
                                               float scale_log2, char* lds) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
@@ -177,10 +260,16 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
 
     const int slots = sg.hk * sg.tiles;
     const int groups = (slots + kWaves - 1) / kWaves;
-    const int s = w % sg.splits;
-    int rem = w / sg.splits;
-    const int sgp = rem % groups;
-    const int b = rem / groups;
+    int s, sgp, b;
+    if (sg.compact) {
+        sgp = w % groups;
+        if (!locate_split(w / groups, sg.seqlens, sg.batch, sg.n, sg.rows_per_split, b, s)) return;
+    } else {
+        s = w % sg.splits;
+        const int rem = w / sg.splits;
+        sgp = rem % groups;
+        b = rem / groups;
+    }
     const int slot = sgp * kWaves + wave;
     if (slot >= slots) return;               // waves never synchronise, so an idle one may leave
     const int h = slot / sg.tiles;
@@ -233,9 +322,36 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         load_tile<KS>(tr, kbase, vbase, sg.k_sn, sg.v_sn, r0, act ? r_end : r_begin, last_row, span_k, span_v,
                       col, grp, lane, act);
     };
+    // Paged rows: the page ids of a tile are loaded two tiles ahead of its data.
+    const int32_t* tab = PAGED ? reinterpret_cast<const int32_t*>(sg.table + (int64_t)b * sg.t_sb) : nullptr;
+    const int last_valid = Nb > 0 ? Nb - 1 : 0;
+    auto page_of = [&](int row) -> int32_t {
+        const int r = min(row, last_valid);
+        return tab[2 * (sg.slots_shift >= 0 ? (r >> sg.slots_shift) : r / sg.slots)];   // low word
+    };
+    auto load_pages = [&](TilePages<KS>& pg, int it) {
+        const int r0 = it < ntile ? r_begin + it * 16 : r_begin;
+        pg.k = page_of(r0 + col);
+#pragma unroll
+        for (int c = 0; c < VT / 2; ++c) pg.v[c] = page_of(r0 + (64 * c + lane) / (2 * VT));
+    };
+    auto fetch_paged = [&](TileRegs<KS>& tr, const TilePages<KS>& pg, int it) {
+        const bool act = it < ntile;
+        const int r0 = act ? r_begin + it * 16 : r_begin;
+        load_tile_paged<KS>(tr, pg, sg, kbase, vbase, r0, act ? r_end : r_begin, last_valid, span_k, span_v, col,
+                            grp, lane, act);
+    };
+    TilePages<KS> pcur, poth;
     // First tile in flight before the query operand is fetched.
     TileRegs<KS> cur;
-    fetch(cur, 0);
+    if constexpr (PAGED) {
+        load_pages(pcur, 0);
+        load_pages(poth, 1);
+        fetch_paged(cur, pcur, 0);
+        load_pages(pcur, 2);
+    } else {
+        fetch(cur, 0);
+    }
 
     // Query operand (B of the score MFMA), same k permutation as the K tile:
     // step 2c+e holds elements 32c + 8*grp + 4e + [0,4).
@@ -317,7 +433,18 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         wave_lds_fence();
     };
 
-    if constexpr (PIPE) {
+    if constexpr (PAGED) {
+        TileRegs<KS> other;
+        for (int it = 0; it < ntile; it += 2) {
+            fetch_paged(other, poth, it + 1);
+            load_pages(poth, it + 3);
+            consume(cur, it);
+            if (it + 1 >= ntile) break;
+            fetch_paged(cur, pcur, it + 2);
+            load_pages(pcur, it + 4);
+            consume(other, it + 1);
+        }
+    } else if constexpr (PIPE) {
         // Ping-pong between two register sets so a tile's loads stay in flight
         // while the previous tile is consumed (no register copy on the back
         // edge).  Loads past the last tile are issued anyway (clamped, zeroed)
@@ -372,7 +499,7 @@ struct SplitWaves {
     static constexpr int value = KA <= 4 ? 4 : (KA <= 6 ? 3 : 1);
 };
 
-template <int KA, int KB>
+template <int KA, int KB, bool PAGED = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SplitWaves<KA>::value)))
 split_kernel(SplitParams prm) {
     constexpr int LA = SplitLds<KA>::bytes;
@@ -386,7 +513,7 @@ split_kernel(SplitParams prm) {
         }
         w -= prm.seg[1].nwg;
     }
-    split_segment<KA, true>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+    split_segment<KA, true, PAGED>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -399,6 +526,8 @@ struct CombineParams {
     const uint16_t* up_v; int64_t up_v_ld; const uint16_t* up_v_bias;
     int blockdiag;                                               // latent acc holds the own block slice
     const float* b_shift;                                        // [B][Hq*Lq] natural-log units or null
+    const int32_t* b_len; int b_rps, b_n;                        // compact latent schedule: splits of b =
+                                                                 // ceil(min(len_b, b_n) / b_rps); null = all
     int B, Lq, Hq, Hkv, D;                                       // D = output width
     uint16_t* out; int64_t o_sb, o_sl, o_sh;
     float* lse;                                                  // [B, Hq, Lq] or null
@@ -428,6 +557,14 @@ __device__ __forceinline__ float block_sum128(float v, float* red) {
     return v;
 }
 
+// Latent splits written for batch entry b (all of them unless the schedule was compact).
+__device__ __forceinline__ int live_b_splits(const CombineParams& cp, int b) {
+    if (!cp.b_len || !cp.b_splits) return cp.b_splits;
+    int len = cp.b_len[b];
+    len = len < 0 ? 0 : (len > cp.b_n ? cp.b_n : len);
+    return min(cp.b_splits, (len + cp.b_rps - 1) / cp.b_rps);
+}
+
 // One workgroup per (b, query head, query): LSE-merge the split partials of
 // both segments, lift the latent accumulator through U_V, fold the biases.
 __global__ void __launch_bounds__(kCombineThreads)
@@ -445,7 +582,8 @@ combine_kernel(CombineParams cp) {
     const float* aml = cp.a_ml + row * cp.a_splits * 2;
     const float* bml = cp.b_splits ? cp.b_ml + row * cp.b_splits * 2 : nullptr;
     const float shift = (cp.b_splits && cp.b_shift) ? cp.b_shift[row] * kLog2e : 0.f;
-    const int total = cp.a_splits + cp.b_splits;
+    const int bsp = live_b_splits(cp, b);
+    const int total = cp.a_splits + bsp;
 
     // Split maxima and masses, one split per thread.
     float mloc = kNegInf;
@@ -477,7 +615,7 @@ combine_kernel(CombineParams cp) {
             const int k = threadIdx.x % cp.b_w, gsel = threadIdx.x / cp.b_w;
             float sum = 0.f;
             if (gsel < groups)
-                for (int s = gsel; s < cp.b_splits; s += groups) sum += bacc[(int64_t)s * cp.b_w + k] * wb[s];
+                for (int s = gsel; s < bsp; s += groups) sum += bacc[(int64_t)s * cp.b_w + k] * wb[s];
             __shared__ float part[kCombineThreads];
             part[threadIdx.x] = sum;
             __syncthreads();
@@ -489,7 +627,7 @@ combine_kernel(CombineParams cp) {
         } else {
             for (int k = threadIdx.x; k < cp.b_w; k += kCombineThreads) {
                 float sum = 0.f;
-                for (int s = 0; s < cp.b_splits; ++s) sum += bacc[(int64_t)s * cp.b_w + k] * wb[s];
+                for (int s = 0; s < bsp; ++s) sum += bacc[(int64_t)s * cp.b_w + k] * wb[s];
                 accb[k] = sum;
             }
         }
@@ -547,7 +685,8 @@ combine_fast_kernel(CombineParams cp) {
     const int lq = pr % cp.Lq;
     const int h = j / (cp.Hq / cp.Hkv);
     const int64_t row = (int64_t)b * HL + pr;
-    const int total = cp.a_splits + cp.b_splits;
+    const int bsp = live_b_splits(cp, b);
+    const int total = cp.a_splits + bsp;
     const float* aml = cp.a_ml + row * cp.a_splits * 2;
     const float* bml = cp.b_splits ? cp.b_ml + row * cp.b_splits * 2 : nullptr;
 
@@ -574,7 +713,7 @@ combine_fast_kernel(CombineParams cp) {
 #pragma unroll
     for (int i = 0; i < kFastLatPer; ++i) {
         const int s = s0 + i * sstep;
-        lb[i] = (bacc && s < cp.b_splits && s0 < sstep) ? bacc[(int64_t)s * cp.b_w + kcol] : 0.f;
+        lb[i] = (bacc && s < bsp && s0 < sstep) ? bacc[(int64_t)s * cp.b_w + kcol] : 0.f;
     }
     u32x4 wv[kFastLatW / 8];
     const uint16_t* wr = nullptr;
@@ -603,7 +742,7 @@ combine_fast_kernel(CombineParams cp) {
 #pragma unroll
         for (int i = 0; i < kFastLatPer; ++i) {
             const int s = s0 + i * sstep;
-            if (s < cp.b_splits && s0 < sstep) sum += lb[i] * wts[cp.a_splits + s];
+            if (s < bsp && s0 < sstep) sum += lb[i] * wts[cp.a_splits + s];
         }
         part[t] = sum;
         __syncthreads();
@@ -869,12 +1008,23 @@ thread_local hipEvent_t g_after = nullptr;
 
 // Launch the split kernel bracketed by the caller's profiling events, if set.
 hipError_t dispatch_split(int ka, int kb, const struct SplitParams& prm, int grid, hipStream_t st);
-hipError_t timed_split(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st) {
+hipError_t dispatch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
+    switch (ka) {
+        case 2: hipLaunchKernelGGL((split_kernel<2, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 4: hipLaunchKernelGGL((split_kernel<4, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 6: hipLaunchKernelGGL((split_kernel<6, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 8: hipLaunchKernelGGL((split_kernel<8, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t timed_split(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st, bool paged = false) {
     if (g_before) {
         hipError_t e = hipEventRecord(g_before, st);
         if (e != hipSuccess) return e;
     }
-    hipError_t e = dispatch_split(ka, kb, prm, grid, st);
+    hipError_t e = paged ? dispatch_split_paged(ka, prm, grid, st) : dispatch_split(ka, kb, prm, grid, st);
     if (e == hipSuccess && g_after) e = hipEventRecord(g_after, st);
     return e;
 }
@@ -1047,7 +1197,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 2; }
+extern "C" int slimkv_abi_version(void) { return 3; }
 
 extern "C" int slimkv_set_profile_events(void* before, void* after) {
     if ((before == nullptr) != (after == nullptr)) return fail(SLIMKV_EINVAL, "set both events or neither");
@@ -1122,9 +1272,36 @@ struct LatentPlan {
     size_t prologue_lds;
 };
 
-int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p) {
+// Beacon rows read straight out of pages (slimkv_paged_latent_decode).
+struct PagedRows {
+    const uint16_t* pages; int64_t num_pages, page_stride;
+    const int64_t* table; int64_t t_sb, t_cols;
+    int64_t slots, sink, rows_total;
+};
+
+int check_paged(const slimkv_latent_decode_args* a, const PagedRows* pg) {
+    if (!pg->pages || !pg->table || !a->lat_lengths) return fail(SLIMKV_EINVAL, "paged decode needs pages, table and lengths");
+    if (pg->num_pages <= 0 || pg->slots <= 0 || pg->sink < 0 || pg->t_cols <= 0 || pg->t_sb < pg->t_cols)
+        return fail(SLIMKV_EINVAL, "invalid page geometry or block-table shape");
+    if (pg->num_pages >= ((int64_t)1 << 31) || pg->num_pages > ((int64_t)1 << 40) / std::max<int64_t>(pg->page_stride, 1))
+        return fail(SLIMKV_EINVAL, "page pool too large");
+    if (!aligned8(pg->page_stride) || !aligned8(pg->sink) || !ptr_aligned16(pg->pages))
+        return fail(SLIMKV_EINVAL, "page stride and sink must be multiples of 8 elements, pages 16-byte aligned");
+    if (pg->sink + pg->slots * (a->rank_k + a->rank_v) > pg->page_stride)
+        return fail(SLIMKV_EINVAL, "beacon slots do not fit in a page");
+    if (a->lat_keys > 0 && (a->lat_keys + pg->slots - 1) / pg->slots > pg->t_cols)
+        return fail(SLIMKV_EINVAL, "block table narrower than the beacon count");
+    if (pg->slots > (1 << 20) || pg->rows_total < 0) return fail(SLIMKV_EINVAL, "invalid page geometry");
+    return SLIMKV_OK;
+}
+
+int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRows* pg = nullptr) {
     if (!a || !a->q || !a->raw_k || !a->raw_v || !a->out || !a->up_k || !a->up_v)
         return fail(SLIMKV_EINVAL, "null tensor pointer");
+    if (pg) {
+        const int rc = check_paged(a, pg);
+        if (rc != SLIMKV_OK) return rc;
+    }
     const int64_t B = a->batch, Lq = a->queries, Hq = a->heads, Hkv = a->kv_heads, D = a->head_dim;
     const int64_t Rk = a->rank_k, Rv = a->rank_v;
     if (B <= 0 || Lq <= 0 || Lq > 2 || Hq <= 0 || Hkv <= 0 || Hq % Hkv)
@@ -1137,7 +1314,7 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p) {
     if (a->raw_keys < 0 || a->lat_keys < 0 || a->raw_keys + a->lat_keys <= 0)
         return fail(SLIMKV_EINVAL, "invalid key counts");
     if (a->raw_keys <= 0) return fail(SLIMKV_EINVAL, "the raw branch always holds the current token");
-    if (a->lat_keys > 0 && (!a->lat_k || !a->lat_v)) return fail(SLIMKV_EINVAL, "null latent pointer");
+    if (!pg && a->lat_keys > 0 && (!a->lat_k || !a->lat_v)) return fail(SLIMKV_EINVAL, "null latent pointer");
     if (a->cos && (!a->sin || !a->q_positions || a->rope_rows <= 0))
         return fail(SLIMKV_EINVAL, "RoPE needs sin, positions and a table size");
     const int64_t strides[] = {a->q_sb, a->q_sl, a->q_sh, a->rk_sb, a->rk_sn, a->rk_sh, a->rv_sb, a->rv_sn,
@@ -1180,7 +1357,20 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p) {
     // resident slots so every workgroup starts in the first wave of residency.
     const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
     const int raw_wg = (int)B * ((int)(Hkv + kWaves - 1) / kWaves) * raw_req0;
-    p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, std::max(slots - raw_wg, slots / 2));
+    const int lat_target = std::max(slots - raw_wg, slots / 2);
+    p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, lat_target);
+    if (pg && a->lat_splits <= 0) {
+        // Compact schedule: size the splits from the total row count so the
+        // non-empty splits of all sequences fill the resident slots once.
+        const int64_t total = pg->rows_total > 0 ? pg->rows_total : B * nl;
+        int64_t rps = (total + lat_target - 1) / lat_target;
+        rps = std::max<int64_t>(rps, (nl + kMaxSplits - 1) / kMaxSplits);
+        rps = std::max<int64_t>(16, (rps + 15) / 16 * 16);
+        const int groups = p->lat.nwg / p->lat.splits;
+        p->lat.rows_per_split = (int)rps;
+        p->lat.splits = (int)((nl + rps - 1) / rps);
+        p->lat.nwg = groups * p->lat.splits;
+    }
     // Raw: one column tile per KV head over the full head width, one split per
     // 16 keys so every raw wave issues all of its loads at once (the raw set is
     // sinks + tail + current token).
@@ -1214,10 +1404,12 @@ extern "C" size_t slimkv_latent_decode_workspace(const slimkv_latent_decode_args
     return p.total;
 }
 
-extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
-                                    size_t workspace_bytes, void* stream) {
+namespace {
+
+int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, void* workspace,
+                      size_t workspace_bytes, void* stream) {
     LatentPlan p{};
-    int rc = plan_latent(a, &p);
+    int rc = plan_latent(a, &p, pg);
     if (rc != SLIMKV_OK) return rc;
     if (!workspace || workspace_bytes < p.total) return fail(SLIMKV_EWORKSPACE, "workspace too small");
     char* ws = static_cast<char*>(workspace);
@@ -1296,11 +1488,21 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
         l.part_acc = reinterpret_cast<float*>(ws + p.lacc_off);
         l.wown = bd ? Rv / Hkv : Rv;
         l.nwg = p.lat.nwg;
+        if (pg) {
+            l.k = pg->pages + pg->sink; l.v = pg->pages + pg->sink + Rk;
+            l.k_sb = l.v_sb = 0; l.k_sn = l.v_sn = Rk + Rv;
+            l.table = pg->table; l.t_sb = pg->t_sb; l.page_stride = pg->page_stride; l.num_pages = pg->num_pages;
+            l.slots = (int)pg->slots;
+            l.slots_shift = (pg->slots & (pg->slots - 1)) == 0 ? __builtin_ctzll((unsigned long long)pg->slots) : -1;
+            l.compact = 1; l.batch = B;
+        }
         ka = p.lat.ks;
         kb = 8;
     }
+    const bool paged = pg && has_lat;
+    if (paged && ka > 8) return fail(SLIMKV_EUNSUP, "paged decode handles latent tiles up to 128 wide");
     const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
-    rc = check_hip(timed_split(ka, kb, prm, grid, st), "split kernel launch");
+    rc = check_hip(timed_split(ka, kb, prm, grid, st, paged), "split kernel launch");
     if (rc != SLIMKV_OK) return rc;
 
     CombineParams cp{};
@@ -1312,12 +1514,42 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
         cp.up_v_bias = static_cast<const uint16_t*>(a->up_v_bias);
         cp.blockdiag = bd ? 1 : 0;
         cp.b_shift = pp.shift;
+        if (prm.seg[0].compact) {
+            cp.b_len = a->lat_lengths; cp.b_rps = prm.seg[0].rows_per_split; cp.b_n = prm.seg[0].n;
+        }
     }
     cp.B = B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hkv; cp.D = D;
     cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
     cp.lse = a->lse;
     launch_combine(cp, B * Hq * Lq, st);
     return check_hip(hipGetLastError(), "combine kernel launch");
+}
+
+PagedRows paged_rows(const slimkv_paged_latent_decode_args* a) {
+    return PagedRows{static_cast<const uint16_t*>(a->pages), a->num_pages, a->page_stride, a->table, a->t_sb,
+                     a->t_cols, a->slots, a->sink_elements, a->rows_total};
+}
+
+}  // namespace
+
+extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+    return latent_decode_run(a, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t slimkv_paged_latent_decode_workspace(const slimkv_paged_latent_decode_args* a) {
+    if (!a) return 0;
+    const PagedRows pg = paged_rows(a);
+    LatentPlan p{};
+    if (plan_latent(&a->base, &p, &pg) != SLIMKV_OK) return 0;
+    return p.total;
+}
+
+extern "C" int slimkv_paged_latent_decode(const slimkv_paged_latent_decode_args* a, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    if (!a) return fail(SLIMKV_EINVAL, "null arguments");
+    const PagedRows pg = paged_rows(a);
+    return latent_decode_run(&a->base, &pg, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------

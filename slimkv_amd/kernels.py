@@ -158,13 +158,13 @@ def prepare_latent_bases(up_k, kv_heads):
 
 def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias, block_diagonal,
                  lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse,
-                 prepared_bases=True):
+                 prepared_bases=True, lat_rows=None):
     _need_device(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v)
     _need_bf16(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, up_k_bias, up_v_bias)
     B, Lq, Hq, D = q.shape
     Nr, Hkv = raw_k.shape[1], raw_k.shape[2]
     Rk, Rv = up_k.shape[1], up_v.shape[1]
-    Nl = 0 if lat_k is None else lat_k.shape[1]
+    Nl = (0 if lat_rows is None else int(lat_rows)) if lat_k is None else lat_k.shape[1]
     q, raw_k, raw_v = (_last_contiguous(x) for x in (q, raw_k, raw_v))
     if lat_k is not None:
         lat_k, lat_v = _last_contiguous(lat_k), _last_contiguous(lat_v)
@@ -185,7 +185,7 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
         if q_positions.stride(-1) != 1:
             q_positions = q_positions.contiguous()
     bases = None
-    if prepared_bases and block_diagonal and lat_k is not None and Nl > 0 and Rk % Hkv == 0 \
+    if prepared_bases and block_diagonal and Nl > 0 and Rk % Hkv == 0 \
             and (Rk // Hkv) % 16 == 0 and D == 128:
         bases = prepare_latent_bases(up_k, Hkv)
     a = _lib.LatentDecodeArgs(
@@ -227,6 +227,43 @@ def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias
     if workspace is None or workspace.numel() < nbytes:
         workspace = _workspace(nbytes, q.device)
     check(lib().slimkv_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    del keep
+    return out, lse
+
+
+def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, layout, up_k, up_v, scale, *,
+                        rows_total=0, up_k_bias=None, up_v_bias=None, block_diagonal=False, lat_causal=False,
+                        q_positions=None, cos=None, sin=None, raw_lengths=None, raw_splits=0, lat_splits=0,
+                        out=None, lse=None, workspace=None):
+    """latent_decode with the beacon rows read straight out of beacon pages.
+
+    pages [num_pages, layout.page_elements] bf16 in BeaconPageLayout format;
+    table [B, >= ceil(lat_keys / slots)] int64 page ids; lat_lengths [B] int32
+    beacons per sequence (<= lat_keys).  rows_total = sum of lat_lengths when
+    known on the host (sizes the key splits only).  Same result as gathering
+    the rows (BeaconPages.read_batch) and calling latent_decode.
+    """
+    _need_device(pages, table, lat_lengths)
+    _need_bf16(pages)
+    if up_k.shape[1] != layout.key_rank or up_v.shape[1] != layout.value_rank:
+        raise ValueError('page layout ranks differ from the up-projection ranks')
+    if pages.dim() != 2 or pages.stride(1) != 1 or pages.shape[1] < layout.page_elements:
+        raise ValueError('pages must be [num_pages, page_elements] with contiguous rows')
+    if table.dtype != torch.int64 or table.dim() != 2 or lat_lengths.dtype != torch.int32:
+        raise ValueError('table must be int64 [B, pages], lat_lengths int32 [B]')
+    table = table if table.stride(1) == 1 else table.contiguous()
+    lat_lengths = lat_lengths.contiguous()
+    base, out, lse, keep = _latent_args(q, raw_k, raw_v, None, None, up_k, up_v, scale, up_k_bias, up_v_bias,
+                                        block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
+                                        lat_lengths, raw_splits, lat_splits, out, lse, True, lat_rows=lat_keys)
+    a = _lib.PagedLatentDecodeArgs(base, _ptr(pages), pages.shape[0], pages.stride(0), _ptr(table), table.stride(0),
+                                   table.shape[1], layout.slots, layout.sink_elements, int(rows_total))
+    nbytes = lib().slimkv_paged_latent_decode_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = _workspace(nbytes, q.device)
+    check(lib().slimkv_paged_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
     del keep
     return out, lse
 

@@ -1,0 +1,119 @@
+"""Paged latent decode (slimkv_paged_latent_decode): the fused latent decode
+reading beacon rows straight out of BeaconPageLayout pages through the block
+table, instead of restore_memory's gather (slimkv/vllm_plugin/paged_model.py:
+36-52 via BeaconPages.read, paged_cache.py:60-87) followed by the decode.
+
+Index handling is checked bit-exactly: with the same key splits the paged
+decode equals gather + dense decode bit for bit (same rows, same arithmetic),
+for power-of-two and other slot counts, ragged lengths including empty
+sequences, and table entries past a sequence's pages that hold garbage.  The
+automatic compact schedule (splits sized from the total row count, only
+non-empty splits launched) is checked against the oracle's float64 attention
+within the bf16 bar.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+from tests.helpers import assert_close, to_np
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D = 32, 8, 128
+
+
+def _case(device, layout_args, lengths, raw_lengths, seed=0, pool_extra=7, garbage=True):
+    from slimkv_amd.paged_cache import BeaconPageLayout
+    layout = BeaconPageLayout(*layout_args)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cpu = torch.Generator().manual_seed(seed + 1)
+    B = len(lengths)
+    pages_needed = [(n + layout.slots - 1) // layout.slots for n in lengths]
+    width = max(max(pages_needed), 1) + 2
+    pool = sum(pages_needed) + pool_extra
+    pages = torch.randn(pool, layout.page_elements, generator=gen, device=device).to(torch.bfloat16)
+    perm = torch.randperm(pool, generator=cpu)
+    tables = torch.full((B, width), -1, dtype=torch.long)
+    if garbage:   # entries past each sequence's pages hold ids far outside the pool
+        tables = torch.randint(-(1 << 40), 1 << 40, (B, width), generator=cpu)
+    off = 0
+    for b, n in enumerate(pages_needed):
+        tables[b, :n] = perm[off:off + n]
+        off += n
+    r_k, r_v = layout.key_rank // HKV, layout.value_rank // HKV
+    up_k = block_diagonal([orthonormal_columns(D, r_k, cpu) for _ in range(HKV)]).to(device, torch.bfloat16)
+    up_v = block_diagonal([orthonormal_columns(D, r_v, cpu) for _ in range(HKV)]).to(device, torch.bfloat16)
+    max_raw = max(raw_lengths)
+    raw_k = torch.randn(B, max_raw, HKV, D, generator=gen, device=device).to(torch.bfloat16)
+    raw_v = torch.randn(B, max_raw, HKV, D, generator=gen, device=device).to(torch.bfloat16)
+    q = torch.randn(B, 1, HQ, D, generator=gen, device=device).to(torch.bfloat16)
+    return dict(layout=layout, pages=pages, tables=tables.to(device), up_k=up_k, up_v=up_v, raw_k=raw_k,
+                raw_v=raw_v, q=q, lengths=torch.tensor(lengths, dtype=torch.int32, device=device),
+                raw_lengths=torch.tensor(raw_lengths, dtype=torch.int32, device=device), lat_keys=max(lengths))
+
+
+def _dense(c):
+    from slimkv_amd.paged_cache import BeaconPages
+    return BeaconPages(c['pages'], c['layout']).read_batch(c['tables'], c['lengths'], count=c['lat_keys'])
+
+
+@pytest.mark.parametrize('layout_args,lengths', [
+    ((16, 8, 256, 256, 1024), [1000, 0, 37, 1, 777, 16, 15, 1024]),     # 2 slots per page (t8)
+    ((16, 4, 256, 256, 1024), [333, 1024, 5, 0, 64, 900]),              # 4 slots per page (t4)
+    ((12, 4, 256, 256, 1024), [301, 2, 299, 150]),                      # 3 slots: non-power-of-two
+    ((16, 8, 128, 384, 1024), [513, 77, 1, 240]),                       # rank 16 K, rank 48 V
+])
+@pytest.mark.parametrize('splits', [3, 8])
+def test_paged_equals_gather_then_decode_bitwise(device, layout_args, lengths, splits):
+    from slimkv_amd import kernels
+    raw_lengths = [5 + (7 * i) % 40 for i in range(len(lengths))]
+    c = _case(device, layout_args, lengths, raw_lengths, seed=len(lengths) + splits)
+    lat_k, lat_v = _dense(c)
+    scale = D ** -0.5
+    want, want_lse = kernels.latent_decode(c['q'], c['raw_k'], c['raw_v'], lat_k, lat_v, c['up_k'], c['up_v'],
+                                           scale, block_diagonal=True, raw_lengths=c['raw_lengths'],
+                                           lat_lengths=c['lengths'], lat_splits=splits)
+    got, got_lse = kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'],
+                                               c['lengths'], c['lat_keys'], c['layout'], c['up_k'], c['up_v'],
+                                               scale, block_diagonal=True, raw_lengths=c['raw_lengths'],
+                                               lat_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(got_lse, want_lse)
+
+
+@pytest.mark.parametrize('rows_total', ['exact', 0, 'low', 'high'])
+def test_compact_schedule_matches_oracle(device, rows_total):
+    """Automatic splits: rows_total only sizes them, so an exact, unknown,
+    too-low or too-high hint gives the same (correct) result."""
+    from slimkv_amd import kernels
+    lengths = [4100, 0, 1, 2047, 16, 3000, 255, 8191]
+    raw_lengths = [1, 133, 64, 17, 4, 100, 2, 129]
+    c = _case(device, (16, 8, 256, 256, 1024), lengths, raw_lengths, seed=11)
+    hint = {'exact': sum(lengths), 0: 0, 'low': 100, 'high': 10 * sum(lengths)}[rows_total]
+    scale = D ** -0.5
+    got, lse = kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'], c['lengths'],
+                                           c['lat_keys'], c['layout'], c['up_k'], c['up_v'], scale,
+                                           rows_total=hint, block_diagonal=True, raw_lengths=c['raw_lengths'])
+    lat_k, lat_v = _dense(c)
+    torch.cuda.synchronize()
+    q = to_np(c['q'].transpose(1, 2))                                  # [B, H, 1, D]
+    raw_k, raw_v = to_np(c['raw_k'].transpose(1, 2)), to_np(c['raw_v'].transpose(1, 2))
+    up_k, up_v = to_np(c['up_k']), to_np(c['up_v'])
+    for b, (n, nr) in enumerate(zip(lengths, raw_lengths)):
+        ref, ref_lse = oa.latent_layer(q[b:b + 1], raw_k[b:b + 1, :, :nr], raw_v[b:b + 1, :, :nr],
+                                       to_np(lat_k)[b:b + 1, None, :n], to_np(lat_v)[b:b + 1, None, :n],
+                                       up_k, up_v, scale, HKV)
+        assert_close(to_np(got.transpose(1, 2))[b:b + 1], ref, what=f'sequence {b}')
+        np.testing.assert_allclose(to_np(lse)[b:b + 1], ref_lse, atol=2e-3, rtol=1e-4)
+
+
+def test_rejects_tables_narrower_than_the_beacon_count(device):
+    from slimkv_amd import kernels
+    c = _case(device, (16, 8, 256, 256, 1024), [100, 40], [3, 3], seed=3)
+    with pytest.raises(ValueError, match='block table'):
+        kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'][:, :10], c['lengths'],
+                                    c['lat_keys'], c['layout'], c['up_k'], c['up_v'], D ** -0.5,
+                                    block_diagonal=True, raw_lengths=c['raw_lengths'])
