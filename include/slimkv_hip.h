@@ -201,12 +201,28 @@ int slimkv_reconstruct(const slimkv_reconstruct_args* a, void* stream);
  *   (tools/benchmark/context_decode_runtime.py:298-344).
  * Argument meaning as slimkv_latent_decode; lat_causal makes the beacon
  * segment bottom-right causal (the raw query of an insertion step does not
- * see the new beacon).  The workspace holds the rebuilt K/V.
+ * see the new beacon).  With block-diagonal bases (per-head K rank 16..48, V
+ * rank 32 or 64) each K tile is rebuilt and rotated inside the attention
+ * kernel and V is lifted after the weighted sum; rotated beacon keys then
+ * need rope_pairs (slimkv_prepare_rope_pairs of the same cos/sin tables) and
+ * rope_repeats = 1 (rotate-half tables, cos/sin = cat(f, f): the reference's
+ * RotaryEmbedding, modeling_utils.py:369-376).  Otherwise the workspace holds
+ * the rebuilt K (and V).
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_recon_decode_args {
     slimkv_latent_decode_args base;
     const int64_t* beacon_positions; int64_t bpos_sb;   /* [B, Nl] or NULL */
+    const uint32_t* rope_pairs;                          /* [rope_rows, 128] or NULL */
+    int32_t rope_repeats;                                /* 1: every cos/sin row is its first half twice */
 } slimkv_recon_decode_args;
+
+/* One-time packing of RoPE tables for the fused reconstruction decode (no
+ * counterpart in the reference, whose RoPE reads cos/sin and rounds them to
+ * bf16 at every use, slimkv/llama3/decode_kernels.py:7-51):
+ * out[r, d] = bf16(cos[r, d]) | bf16(sin[r, d]) << 16.  cos, sin [rows, dim]
+ * fp32 contiguous; out [rows, dim] uint32. */
+int slimkv_prepare_rope_pairs(const float* cos, const float* sin, int64_t rows, int64_t dim, uint32_t* out,
+                              void* stream);
 
 size_t slimkv_recon_decode_workspace(const slimkv_recon_decode_args* a);
 int slimkv_recon_decode(const slimkv_recon_decode_args* a, void* workspace, size_t workspace_bytes, void* stream);

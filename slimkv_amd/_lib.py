@@ -75,6 +75,7 @@ ReconstructArgs = _struct('slimkv_reconstruct_args', [
 ReconDecodeArgs = _struct('slimkv_recon_decode_args', [
     ('base', LatentDecodeArgs),
     ('beacon_positions', c_ptr), ('bpos_sb', c_i64),
+    ('rope_pairs', c_ptr), ('rope_repeats', c_i32),
 ])
 
 PagedLatentDecodeArgs = _struct('slimkv_paged_latent_decode_args', [
@@ -167,6 +168,7 @@ SIGNATURES = {
     'slimkv_paged_latent_decode': (ctypes.c_int, [ctypes.POINTER(PagedLatentDecodeArgs), c_ptr, ctypes.c_size_t,
                                                   c_ptr]),
     'slimkv_prepare_latent_bases': (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
+    'slimkv_prepare_rope_pairs': (ctypes.c_int, [c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr]),
     'slimkv_reconstruct': (ctypes.c_int, [ctypes.POINTER(ReconstructArgs), c_ptr]),
     'slimkv_recon_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(ReconDecodeArgs)]),
     'slimkv_recon_decode': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
@@ -180,7 +182,7 @@ SIGNATURES = {
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class SlimKVError(RuntimeError):

@@ -517,6 +517,311 @@ split_kernel(SplitParams prm) {
 }
 
 // ---------------------------------------------------------------------------
+// fused reconstruction decode: beacon K rebuilt and rotated per 16-key tile
+// ---------------------------------------------------------------------------
+
+// Beacon segment of the reconstruction decode with block-diagonal bases.  A
+// wavefront owns (b, KV head h, key split) with the head's g*Lq query rows as
+// MFMA columns.  Per 16-key tile it rebuilds K^T[d, n] = U_K[h*128 + d, :] .
+// l_k[n, h-slice] on the MFMA with U_K's tile held in registers (lane (n, grp)
+// ends with d = 16t + 4grp + i, so d and d + 64 share a lane), adds the bias,
+// rounds to bf16 and rotates at the beacon's position with the reference's
+// bf16 steps -- the same bits the up-projection kernel writes -- and feeds the
+// result straight in as the A operand of the score MFMA.  V stays latent: the
+// P.V MFMA accumulates the rv-wide latent sum that the combine lifts through
+// W_V.  RoPE reads (bf16 cos | bf16 sin << 16) pairs prepared once per table,
+// only the first half of each row: the fused route is taken for rotate-half
+// tables whose rows repeat their first half (cos[d] = cos[d + 64]), which the
+// caller checks once per table.
+struct ReconSeg {
+    const uint16_t* q; int64_t q_sb, q_sl, q_sh;        // rotated queries [B, Lq, Hq, 128]
+    const uint16_t* lk; int64_t lk_sb, lk_sn;           // latent K rows, head h at [h*rk, (h+1)*rk)
+    const uint16_t* lv; int64_t lv_sb, lv_sn;           // latent V rows, head h at [h*rv, (h+1)*rv)
+    const uint16_t* w; const uint16_t* bias; int64_t w_ld;   // U_K [Hkv*128, Rk] (nn.Linear), bias or null
+    const uint32_t* pairs; int64_t rope_rows;           // [rope_rows][128] or null (no beacon RoPE)
+    const int64_t* pos; int64_t pos_sb;                 // beacon positions [B, Nl]
+    const int32_t* seqlens;
+    int n, hk, g, causal;
+    int splits, rows_per_split, nwg;
+    float* part_ml; float* part_acc;                    // partials, rv wide
+};
+
+// One 16-key tile of latent rows in registers, with the key position of the
+// lane's row (its RoPE pairs are fetched two tiles before the tile is used).
+template <int KSR, int VL>
+struct ReconTile {
+    u32x2 k[KSR];         // latent K pieces of the lane's key (B operand of the rebuild)
+    u32x4 v[VL];          // latent V pieces on their way to LDS
+    int64_t pos;
+};
+
+// Tiles in flight per wavefront: the rebuild's arithmetic is long enough that
+// two tiles do not cover the memory latency at two waves per SIMD.
+constexpr int kReconRing = 4;
+
+template <int KSR, int VL, bool ROPE>
+__device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq, int Hq, float scale_log2,
+                                              char* lds) {
+    constexpr int D = 128;
+    constexpr int RV = 32 * VL;
+    constexpr int RSV = RV + 8;
+    constexpr int PPR = RV / 8;                        // 16-byte V pieces per row
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int groups = (sg.hk + kWaves - 1) / kWaves;
+    const int s = w % sg.splits;
+    const int rem = w / sg.splits;
+    const int b = rem / groups;
+    const int h = (rem % groups) * kWaves + wave;
+    if (h >= sg.hk) return;
+    const int P = Lq * sg.g;
+    const bool colv = col < P;
+    const int jj = colv ? col / Lq : 0, lq = colv ? col % Lq : 0;
+    const int j = h * sg.g + jj;
+    const int rk = 16 * KSR;
+
+    int Nb = sg.n;
+    if (sg.seqlens) {
+        const int sl = sg.seqlens[b];
+        Nb = sl < 0 ? 0 : (sl < sg.n ? sl : sg.n);
+    }
+    const int lim = !colv ? 0 : (sg.causal ? Nb - Lq + lq + 1 : Nb);
+    const int r_begin = s * sg.rows_per_split;
+    const int r_end = min(r_begin + sg.rows_per_split, Nb);
+    const int ntile = r_end > r_begin ? (r_end - r_begin + 15) / 16 : 0;
+    const int vis = min(lim, r_end);
+    const int last_row = sg.n - 1;
+
+    const uint16_t* kbase = sg.lk + (int64_t)b * sg.lk_sb + (int64_t)h * rk + 4 * grp;
+    const uint16_t* vbase = sg.lv + (int64_t)b * sg.lv_sb + (int64_t)h * RV;
+    const int64_t* pbase = ROPE ? sg.pos + (int64_t)b * sg.pos_sb : nullptr;
+
+    // Raw loads only (clamped in-bounds addresses, no selects on the data), so
+    // nothing waits for them before the tile is consumed: keys outside the
+    // split are masked in the scores and their V rows are zeroed on the way
+    // to LDS, where the tile is used.
+    auto fetch = [&](ReconTile<KSR, VL>& t, int it) {
+        const int r0 = it < ntile ? r_begin + it * 16 : r_begin;
+        const uint16_t* src = kbase + (int64_t)min(r0 + col, last_row) * sg.lk_sn;
+#pragma unroll
+        for (int ks = 0; ks < KSR; ++ks) t.k[ks] = *reinterpret_cast<const u32x2*>(src + 16 * ks);
+#pragma unroll
+        for (int c = 0; c < VL; ++c) {
+            const int p = 64 * c + lane;
+            t.v[c] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)min(r0 + p / PPR, last_row) * sg.lv_sn +
+                                                     8 * (p % PPR));
+        }
+        if constexpr (ROPE) t.pos = pbase[min(r0 + col, last_row)];
+    };
+    // RoPE pairs of the lane's key for d = 16t + 4grp + [0, 4), t < 4 (rows
+    // repeat their first half, so d + 64 uses the same pair).
+    auto fetch_pairs = [&](u32x4 (&cs)[4], int64_t pos) {
+        const uint32_t* src = sg.pairs + clamp_i64(pos, 0, sg.rope_rows - 1) * D + 4 * grp;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) cs[tt] = *reinterpret_cast<const u32x4*>(src + 16 * tt);
+    };
+
+    // U_K tile of this head (A operand of the rebuild) and the bias, once.
+    u32x2 wa[8][KSR];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int ks = 0; ks < KSR; ++ks)
+            wa[tt][ks] = *reinterpret_cast<const u32x2*>(sg.w + ((int64_t)h * D + 16 * tt + col) * sg.w_ld + h * rk +
+                                                         16 * ks + 4 * grp);
+    uint32_t bias2[8][2];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+        const u32x2 bb = sg.bias ? *reinterpret_cast<const u32x2*>(sg.bias + (int64_t)h * D + 16 * tt + 4 * grp)
+                                 : u32x2{0u, 0u};
+        bias2[tt][0] = bb.x;
+        bias2[tt][1] = bb.y;
+    }
+    // Rotated query of the column (B operand of the scores): d = 16t + 4grp + [0, 4).
+    u32x2 qop[8];
+    {
+        const uint16_t* qrow = sg.q + (int64_t)b * sg.q_sb + (int64_t)lq * sg.q_sl + (int64_t)j * sg.q_sh + 4 * grp;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) {
+            const u32x2 x = *reinterpret_cast<const u32x2*>(qrow + 16 * tt);
+            qop[tt] = u32x2{colv ? x.x : 0u, colv ? x.y : 0u};
+        }
+    }
+
+    ReconTile<KSR, VL> ring[kReconRing];
+    u32x4 pairs[2][4];
+#pragma unroll
+    for (int u = 0; u < kReconRing; ++u) fetch(ring[u], u);
+    if constexpr (ROPE) {
+        fetch_pairs(pairs[0], ring[0].pos);
+        fetch_pairs(pairs[1], ring[1].pos);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    float m = kNegInf, lsum = 0.f;
+    v4f acc[2 * VL];
+#pragma unroll
+    for (int i = 0; i < 2 * VL; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+    uint16_t* vbuf = reinterpret_cast<uint16_t*>(lds) + wave * 2 * 16 * RSV;
+
+    auto consume = [&](const ReconTile<KSR, VL>& t, const u32x4 (&cs)[4], int it) {
+        const int r0 = r_begin + it * 16;
+        const int re = it < ntile ? r_end : r_begin;
+        uint16_t* vb = vbuf + (it & 1) * 16 * RSV;
+#pragma unroll
+        for (int c = 0; c < VL; ++c) {
+            const int p = 64 * c + lane;
+            *reinterpret_cast<u32x4*>(vb + (p / PPR) * RSV + 8 * (p % PPR)) = zero_unless(r0 + p / PPR < re, t.v[c]);
+        }
+        // rebuild the K tile
+        v4f kc[8];
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) kc[tt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KSR; ++ks) {
+            const v4s bop = as_v4s(t.k[ks].x, t.k[ks].y);
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) kc[tt] = mfma16(as_v4s(wa[tt][ks].x, wa[tt][ks].y), bop, kc[tt]);
+        }
+        // bias add and bf16 rounding, two features per packed conversion
+        uint32_t xb[8][2];
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                // a missing bias is held as +0: x + 0 is x except that -0 becomes +0
+                xb[tt][hh] = pack_bf16(kc[tt][2 * hh] + lo_bf16(bias2[tt][hh]), kc[tt][2 * hh + 1] + hi_bf16(bias2[tt][hh]));
+            }
+        u32x2 kop[8];
+        if constexpr (ROPE) {
+            // rotate_half pairs d with d + 64 (t with t + 4) under the same (c, s):
+            //   y[d]      = bf16(bf16(x[d] * c) + bf16(-x[d + 64] * s))
+            //   y[d + 64] = bf16(bf16(x[d + 64] * c) + bf16(x[d] * s))
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const uint32_t cw[4] = {cs[tt].x, cs[tt].y, cs[tt].z, cs[tt].w};
+                uint32_t ya[2], yb[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float a[2], bq[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float xa = e ? hi_bf16(xb[tt][hh]) : lo_bf16(xb[tt][hh]);
+                        const float xz = e ? hi_bf16(xb[tt + 4][hh]) : lo_bf16(xb[tt + 4][hh]);
+                        const float c = lo_bf16(cw[2 * hh + e]), sn = hi_bf16(cw[2 * hh + e]);
+                        const uint32_t pa = pack_bf16(xa * c, -xz * sn);
+                        const uint32_t pb = pack_bf16(xz * c, xa * sn);
+                        a[e] = lo_bf16(pa) + hi_bf16(pa);
+                        bq[e] = lo_bf16(pb) + hi_bf16(pb);
+                    }
+                    ya[hh] = pack_bf16(a[0], a[1]);
+                    yb[hh] = pack_bf16(bq[0], bq[1]);
+                }
+                kop[tt] = u32x2{ya[0], ya[1]};
+                kop[tt + 4] = u32x2{yb[0], yb[1]};
+            }
+        } else {
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) kop[tt] = u32x2{xb[tt][0], xb[tt][1]};
+        }
+        // scores S^T[key, col]
+        v4f sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < 8; tt += 2) {
+            sc0 = mfma16(as_v4s(kop[tt].x, kop[tt].y), as_v4s(qop[tt].x, qop[tt].y), sc0);
+            sc1 = mfma16(as_v4s(kop[tt + 1].x, kop[tt + 1].y), as_v4s(qop[tt + 1].x, qop[tt + 1].y), sc1);
+        }
+        const v4f sc = sc0 + sc1;
+        float sv[4];
+        float tmax = kNegInf;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int nn = r0 + 4 * grp + i;
+            const float xv = nn < vis ? sc[i] * scale_log2 : kNegInf;
+            sv[i] = xv;
+            tmax = fmaxf(tmax, xv);
+        }
+        tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
+        tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+        const float mnew = fmaxf(m, tmax);
+        const float mref = mnew == kNegInf ? 0.f : mnew;
+        const float alpha = fast_exp2(m - mref);
+        float pr[4];
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pr[i] = fast_exp2(sv[i] - mref);
+            psum += pr[i];
+        }
+        lsum = lsum * alpha + psum;
+        m = mnew;
+#pragma unroll
+        for (int i = 0; i < 2 * VL; ++i) acc[i] *= alpha;
+        const v4s pb = as_v4s(f32_to_bf16(pr[0]) | (f32_to_bf16(pr[1]) << 16),
+                              f32_to_bf16(pr[2]) | (f32_to_bf16(pr[3]) << 16));
+        wave_lds_fence();
+#pragma unroll
+        for (int u = 0; u < VL; ++u) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w4[i] = *reinterpret_cast<const uint32_t*>(vb + (4 * grp + i) * RSV + 32 * u + 2 * col);
+            const v4s lo = as_v4s((w4[0] & 0xffffu) | (w4[1] << 16), (w4[2] & 0xffffu) | (w4[3] << 16));
+            const v4s hi = as_v4s((w4[0] >> 16) | (w4[1] & 0xffff0000u), (w4[2] >> 16) | (w4[3] & 0xffff0000u));
+            acc[2 * u] = mfma16(lo, pb, acc[2 * u]);
+            acc[2 * u + 1] = mfma16(hi, pb, acc[2 * u + 1]);
+        }
+        wave_lds_fence();
+    };
+
+    // Whole rounds of the ring, branch-free: tiles past the split's end are
+    // loaded clamped and zeroed and every key in them is masked, so they leave
+    // the running softmax unchanged.
+    for (int it = 0; it < ntile; it += kReconRing) {
+#pragma unroll
+        for (int u = 0; u < kReconRing; ++u) {
+            consume(ring[u], pairs[u & 1], it + u);
+            fetch(ring[u], it + u + kReconRing);
+            if constexpr (ROPE) fetch_pairs(pairs[u & 1], ring[(u + 2) % kReconRing].pos);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    lsum += shfl_xor_f(lsum, 16);
+    lsum += shfl_xor_f(lsum, 32);
+    if (!colv) return;
+    const int prow = j * Lq + lq;
+    const int64_t slot_out = ((int64_t)b * Hq * Lq + prow) * sg.splits + s;
+    if (grp == 0) {
+        sg.part_ml[slot_out * 2] = m;
+        sg.part_ml[slot_out * 2 + 1] = lsum;
+    }
+    float* dst = sg.part_acc + slot_out * RV;
+#pragma unroll
+    for (int u = 0; u < VL; ++u) {
+        float4* d4 = reinterpret_cast<float4*>(dst + 32 * u + 8 * grp);
+        d4[0] = make_float4(acc[2 * u][0], acc[2 * u + 1][0], acc[2 * u][1], acc[2 * u + 1][1]);
+        d4[1] = make_float4(acc[2 * u][2], acc[2 * u + 1][2], acc[2 * u][3], acc[2 * u + 1][3]);
+    }
+}
+
+// Raw rows (split_segment, head_dim 128) first in the grid, then the beacon splits.
+template <int KSR, int VL, bool ROPE>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+recon_split_kernel(SplitParams prm, ReconSeg rs) {
+    constexpr int LA = kWaves * 2 * 16 * (32 * VL + 8) * 2;
+    constexpr int LB = SplitLds<8>::bytes;
+    __shared__ __attribute__((aligned(16))) char lds[LA > LB ? LA : LB];
+    int w = blockIdx.x;
+    if (w < prm.seg[0].nwg) {
+        split_segment<8, false>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+        return;
+    }
+    w -= prm.seg[0].nwg;
+    recon_segment<KSR, VL, ROPE>(rs, w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+}
+
+// ---------------------------------------------------------------------------
 // combine kernel
 // ---------------------------------------------------------------------------
 
@@ -1197,7 +1502,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 3; }
+extern "C" int slimkv_abi_version(void) { return 4; }
 
 extern "C" int slimkv_set_profile_events(void* before, void* after) {
     if ((before == nullptr) != (after == nullptr)) return fail(SLIMKV_EINVAL, "set both events or neither");
@@ -1561,8 +1866,31 @@ namespace {
 struct ReconPlan {
     SegPlan raw, rec;
     int v_latent, v_width;   // V stays latent (width v_width per KV head) and is lifted in the combine
+    int fused, ksr, vl;      // K rebuilt per tile inside the split kernel (recon_split_kernel<ksr, vl>)
     size_t qrot_off, k_off, v_off, rml_off, racc_off, bml_off, bacc_off, total;
 };
+
+// The fused route: block-diagonal bases, per-head K rank 16..48 and V rank 32
+// or 64, the alignment its 8- and 16-byte loads need, and prepared RoPE pairs
+// when the beacon keys are rotated.
+bool recon_fused_ok(const slimkv_recon_decode_args* r) {
+    const slimkv_latent_decode_args* a = &r->base;
+    if (a->lat_keys <= 0 || !a->block_diagonal) return false;
+    const int64_t Hkv = a->kv_heads;
+    if (a->rank_k % Hkv || a->rank_v % Hkv) return false;
+    const int64_t rk = a->rank_k / Hkv, rv = a->rank_v / Hkv;
+    if (rk % 16 || rk < 16 || rk > 48 || (rv != 32 && rv != 64) || (rk == 48 && rv == 64)) return false;
+    auto al = [](const void* ptr, uintptr_t m) { return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0; };
+    if (!al(a->lat_k, 8) || (a->lk_sb & 3) || (a->lk_sn & 3) || !al(a->up_k, 8) || (a->rank_k & 3)) return false;
+    if (a->up_k_bias && !al(a->up_k_bias, 8)) return false;
+    if (!al(a->lat_v, 16) || !aligned8(a->lv_sb) || !aligned8(a->lv_sn)) return false;
+    if (!al(a->up_v, 16) || !aligned8(a->rank_v)) return false;
+    if (r->beacon_positions && (!r->rope_pairs || !r->rope_repeats || !al(r->rope_pairs, 16) || a->rope_rows <= 0))
+        return false;
+    return true;
+}
+
+int recon_occupancy(int ksr, int vl);
 
 // V is linear in its latent, so sum_n p_n (U_V l_n + b) = U_V (sum_n p_n l_n) + b sum_n p_n:
 // the split kernel can attend over the latent rows and the combine lifts once per
@@ -1589,15 +1917,25 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     if (g * Lq > kMaxRows) return fail(SLIMKV_EUNSUP, "more than 16 query rows per KV head");
     const int cu = device_cu_count();
     const int nl = (int)std::max<int64_t>(a->lat_keys, 1);
-    p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, (int)D, a->lat_splits,
-                          cu * split_occupancy(8, 8));
     const int raw_req = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
     p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req, 0);
+    p->fused = recon_fused_ok(r) ? 1 : 0;
+    if (p->fused) {
+        p->ksr = (int)(a->rank_k / Hkv / 16);
+        p->vl = (int)(a->rank_v / Hkv / 32);
+        // The beacon splits are arithmetic-bound (rebuild + RoPE per tile), so
+        // they take every resident slot; the short raw workgroups run ahead of them.
+        const int slots = cu * recon_occupancy(p->ksr, p->vl);
+        p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, 32 * p->vl, a->lat_splits, slots);
+    } else {
+        p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, (int)D, a->lat_splits,
+                              cu * split_occupancy(8, 8));
+    }
     size_t off = 0;
-    p->v_latent = recon_v_latent(a) ? 1 : 0;
+    p->v_latent = (p->fused || recon_v_latent(a)) ? 1 : 0;
     p->v_width = p->v_latent ? (int)(a->block_diagonal ? a->rank_v / Hkv : a->rank_v) : (int)D;
     p->qrot_off = off; off = align256(off + (size_t)B * Lq * Hq * D * 2);
-    p->k_off = off; off = align256(off + (size_t)B * nl * Hkv * D * 2);
+    p->k_off = off; off = align256(off + (p->fused ? 0 : (size_t)B * nl * Hkv * D * 2));
     p->v_off = off; off = align256(off + (p->v_latent ? 0 : (size_t)B * nl * Hkv * D * 2));
     const size_t rr = (size_t)B * Hq * Lq * p->raw.splits;
     p->rml_off = off; off = align256(off + rr * 8);
@@ -1607,6 +1945,92 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     p->bacc_off = off; off = align256(off + br * D * 4);
     p->total = off;
     return SLIMKV_OK;
+}
+
+int recon_occupancy(int ksr, int vl) {
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const int key = (dev << 8) | (ksr << 4) | vl;
+    std::lock_guard<std::mutex> lock(mu);
+    for (auto& kv : cache)
+        if (kv.first == key) return kv.second;
+    const void* fn = nullptr;
+#define SLIMKV_FN(K, V) if (ksr == K && vl == V) fn = reinterpret_cast<const void*>(&recon_split_kernel<K, V, true>);
+    SLIMKV_FN(1, 1) SLIMKV_FN(2, 1) SLIMKV_FN(3, 1) SLIMKV_FN(1, 2) SLIMKV_FN(2, 2)
+#undef SLIMKV_FN
+    int blocks = 0;
+    if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, 0) != hipSuccess || blocks < 1)
+        blocks = 1;
+    cache.push_back({key, blocks});
+    return blocks;
+}
+
+// Raw rows and rebuilt-per-tile beacon rows in one launch, then the combine
+// with the latent V lift.  q_rot already holds the rotated queries.
+int recon_fused_run(const slimkv_recon_decode_args* r, const ReconPlan& p, char* ws, uint16_t* q_rot, hipStream_t st) {
+    const slimkv_latent_decode_args* a = &r->base;
+    const int B = (int)a->batch, Lq = (int)a->queries, Hq = (int)a->heads, Hkv = (int)a->kv_heads, D = (int)a->head_dim;
+    const int g = Hq / Hkv;
+    SplitParams prm{};
+    prm.B = B; prm.Lq = Lq; prm.Hq = Hq;
+    prm.scale_log2 = (float)(a->scale * 1.4426950408889634);
+    prm.nseg = 1;
+    Seg& rs = prm.seg[0];
+    rs.q = q_rot; rs.q_sb = (int64_t)Lq * Hq * D; rs.q_sl = (int64_t)Hq * D; rs.q_sh = D;
+    rs.k = static_cast<const uint16_t*>(a->raw_k); rs.k_sb = a->rk_sb; rs.k_sn = a->rk_sn; rs.k_sh = a->rk_sh;
+    rs.v = static_cast<const uint16_t*>(a->raw_v); rs.v_sb = a->rv_sb; rs.v_sn = a->rv_sn; rs.v_sh = a->rv_sh;
+    rs.seqlens = a->raw_lengths; rs.n = (int)a->raw_keys;
+    rs.hk = Hkv; rs.g = g; rs.wk = D; rs.wv = D; rs.causal = 0;
+    rs.tiles = p.raw.tiles; rs.cols = p.raw.cols; rs.splits = p.raw.splits; rs.rows_per_split = p.raw.rows_per_split;
+    rs.part_ml = reinterpret_cast<float*>(ws + p.rml_off); rs.part_acc = reinterpret_cast<float*>(ws + p.racc_off);
+    rs.wown = D; rs.nwg = p.raw.nwg;
+
+    ReconSeg bs{};
+    bs.q = q_rot; bs.q_sb = rs.q_sb; bs.q_sl = rs.q_sl; bs.q_sh = rs.q_sh;
+    bs.lk = static_cast<const uint16_t*>(a->lat_k); bs.lk_sb = a->lk_sb; bs.lk_sn = a->lk_sn;
+    bs.lv = static_cast<const uint16_t*>(a->lat_v); bs.lv_sb = a->lv_sb; bs.lv_sn = a->lv_sn;
+    bs.w = static_cast<const uint16_t*>(a->up_k); bs.bias = static_cast<const uint16_t*>(a->up_k_bias);
+    bs.w_ld = a->rank_k;
+    if (r->beacon_positions) {
+        bs.pairs = r->rope_pairs; bs.rope_rows = a->rope_rows;
+        bs.pos = r->beacon_positions; bs.pos_sb = r->bpos_sb;
+    }
+    bs.seqlens = a->lat_lengths; bs.n = (int)a->lat_keys; bs.hk = Hkv; bs.g = g; bs.causal = a->lat_causal ? 1 : 0;
+    bs.splits = p.rec.splits; bs.rows_per_split = p.rec.rows_per_split; bs.nwg = p.rec.nwg;
+    bs.part_ml = reinterpret_cast<float*>(ws + p.bml_off); bs.part_acc = reinterpret_cast<float*>(ws + p.bacc_off);
+
+    const int grid = rs.nwg + bs.nwg;
+    if (g_before) {
+        const hipError_t e = hipEventRecord(g_before, st);
+        if (e != hipSuccess) return check_hip(e, "profile event");
+    }
+#define SLIMKV_LAUNCH(K, V)                                                                                       \
+    if (p.ksr == K && p.vl == V) {                                                                                \
+        if (bs.pairs) hipLaunchKernelGGL((recon_split_kernel<K, V, true>), dim3(grid), dim3(kThreads), 0, st, prm, bs); \
+        else hipLaunchKernelGGL((recon_split_kernel<K, V, false>), dim3(grid), dim3(kThreads), 0, st, prm, bs);       \
+    }
+    SLIMKV_LAUNCH(1, 1) SLIMKV_LAUNCH(2, 1) SLIMKV_LAUNCH(3, 1) SLIMKV_LAUNCH(1, 2) SLIMKV_LAUNCH(2, 2)
+#undef SLIMKV_LAUNCH
+    int rc = check_hip(hipGetLastError(), "reconstruction split kernel launch");
+    if (rc != SLIMKV_OK) return rc;
+    if (g_after) {
+        rc = check_hip(hipEventRecord(g_after, st), "profile event");
+        if (rc != SLIMKV_OK) return rc;
+    }
+
+    CombineParams cp{};
+    cp.a_ml = rs.part_ml; cp.a_acc = rs.part_acc; cp.a_splits = rs.splits; cp.a_w = D;
+    cp.b_ml = bs.part_ml; cp.b_acc = bs.part_acc; cp.b_splits = bs.splits; cp.b_w = 32 * p.vl;
+    cp.up_v = static_cast<const uint16_t*>(a->up_v); cp.up_v_ld = a->rank_v;
+    cp.up_v_bias = static_cast<const uint16_t*>(a->up_v_bias);
+    cp.blockdiag = 1;
+    cp.B = B; cp.Lq = Lq; cp.Hq = Hq; cp.Hkv = Hkv; cp.D = D;
+    cp.out = static_cast<uint16_t*>(a->out); cp.o_sb = a->o_sb; cp.o_sl = a->o_sl; cp.o_sh = a->o_sh;
+    cp.lse = a->lse;
+    launch_combine(cp, B * Hq * Lq, st);
+    return check_hip(hipGetLastError(), "combine kernel launch");
 }
 
 }  // namespace
@@ -1646,6 +2070,8 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
     hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
     rc = check_hip(hipGetLastError(), "prologue kernel launch");
     if (rc != SLIMKV_OK) return rc;
+
+    if (p.fused) return recon_fused_run(r, p, ws, q_rot, st);
 
     // 2. rebuild beacon K (optionally RoPE'd) and, unless it stays latent, V: [B, Nl, Hkv, D]
     if (has_lat) {
@@ -1743,6 +2169,23 @@ prepare_bases_kernel(const uint16_t* up_k, int Hkv, int D, int R, uint16_t* out)
 }
 
 }  // namespace
+
+__global__ void __launch_bounds__(256)
+prepare_pairs_kernel(const float* cos, const float* sin, int64_t total, uint32_t* out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    out[i] = f32_to_bf16(cos[i]) | (f32_to_bf16(sin[i]) << 16);
+}
+
+extern "C" int slimkv_prepare_rope_pairs(const float* cos, const float* sin, int64_t rows, int64_t dim, uint32_t* out,
+                                         void* stream) {
+    if (!cos || !sin || !out) return fail(SLIMKV_EINVAL, "null pointer");
+    if (rows <= 0 || dim <= 0 || rows > ((int64_t)1 << 40) / dim) return fail(SLIMKV_EINVAL, "invalid table size");
+    const int64_t total = rows * dim;
+    hipLaunchKernelGGL(prepare_pairs_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), cos, sin, total, out);
+    return check_hip(hipGetLastError(), "pair preparation launch");
+}
 
 extern "C" int slimkv_prepare_latent_bases(const void* up_k, int64_t kv_heads, int64_t head_dim, int64_t rank,
                                            void* out, void* stream) {

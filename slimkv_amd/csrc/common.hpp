@@ -36,6 +36,17 @@ __device__ __forceinline__ float round_bf16(float x) {
     return bf16_to_f32(f32_to_bf16(x));
 }
 
+// bf16(a) | bf16(b) << 16 with the gfx950 packed conversion (round to nearest
+// even, identical to f32_to_bf16 for every non-NaN input; a NaN keeps its
+// payload, quieted, instead of becoming 0x7fc0).
+typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_hw{a, b}, bf16x2_hw));
+}
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 // Four bf16 held in two dwords, as the MFMA operand wants them.
 __device__ __forceinline__ v4s as_v4s(uint32_t lo, uint32_t hi) {
     u32x2 t = {lo, hi};

@@ -321,11 +321,16 @@ def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_pos
     base, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
                                         block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
                                         lat_lengths, raw_splits, lat_splits, out, lse, prepared_bases=False)
+    pairs = None
     if beacon_positions is not None:
         beacon_positions = beacon_positions.to(torch.int64)
         beacon_positions = beacon_positions if beacon_positions.stride(-1) == 1 else beacon_positions.contiguous()
+        if cos is None:
+            raise ValueError('beacon RoPE needs the cos/sin tables')
+        pairs, repeats = prepare_rope_pairs(cos, sin)
     a = _lib.ReconDecodeArgs(base, _ptr(beacon_positions),
-                             0 if beacon_positions is None else beacon_positions.stride(0))
+                             0 if beacon_positions is None else beacon_positions.stride(0), _ptr(pairs),
+                             int(pairs is not None and repeats))
     nbytes = lib().slimkv_recon_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
@@ -334,6 +339,28 @@ def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_pos
     check(lib().slimkv_recon_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
     del keep
     return out, lse
+
+
+def prepare_rope_pairs(cos, sin):
+    """((bf16 cos | bf16 sin << 16) as int32 [rows, dim], repeats) built once
+    per table pair and cached on `cos` (keyed by both tables' versions and
+    pointers).  repeats: every row is its first half twice (rotate-half
+    tables), checked once here (one host synchronisation per table)."""
+    _need_device(cos, sin)
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape or cos.dim() != 2:
+        raise ValueError('RoPE tables must be fp32 [rows, dim] of equal shape')
+    key = (cos._version, sin._version, cos.data_ptr(), sin.data_ptr())
+    cached = getattr(cos, '_slimkv_pairs', None)
+    if cached is not None and cached[0] == key:
+        return cached[1], cached[2]
+    c, s_ = cos.contiguous(), sin.contiguous()
+    out = torch.empty(cos.shape, dtype=torch.int32, device=cos.device)
+    check(lib().slimkv_prepare_rope_pairs(_ptr(c), _ptr(s_), cos.shape[0], cos.shape[1], _ptr(out),
+                                          _lib.stream_handle(cos.device)))
+    half = cos.shape[1] // 2
+    repeats = bool(cos.shape[1] % 2 == 0 and torch.equal(out[:, :half], out[:, half:]))
+    cos._slimkv_pairs = (key, out, repeats)
+    return out, repeats
 
 
 def rope_decode(q, k, cos, sin, query_positions, raw_indices, sink, history):

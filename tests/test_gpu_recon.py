@@ -178,3 +178,88 @@ def test_recon_decode_insertion_step_with_biases_general_weights(device, rank):
     assert_close(got, exact)
     assert_close(got, eager)
     assert_lse_close(to_np(lse), lse_e)
+
+
+@pytest.mark.parametrize('rk,rv,bias,insertion', [(32, 32, True, True), (16, 64, False, False), (48, 32, True, False),
+                                                  (32, 64, False, True)])
+def test_recon_decode_fused_block_diagonal_variants(device, rk, rv, bias, insertion):
+    """Block-diagonal bases take the fused route (K rebuilt and rotated per tile
+    inside the attention kernel, V lifted after the sum): K ranks 16/32/48, V
+    ranks 32/64, K/V biases, the two-query insertion step with a causal beacon
+    segment, beacon K-RoPE at slot positions."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=3, heads=32, context=2048 + 132, tail=128, rank_k=rk, rank_v=rv, seed=rk + rv,
+                       device=device)
+    gen = torch.Generator(device=device).manual_seed(rk)
+    bk = bv = None
+    if bias:
+        bk = (0.3 * torch.randn(case.up_k.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+        bv = (0.3 * torch.randn(case.up_v.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+    if insertion:
+        case.q = torch.cat([case.q, torch.randn(case.q.shape, generator=gen, device=device).to(torch.bfloat16)], 1)
+        case.q_positions = torch.cat([case.q_positions, case.q_positions + 1], 1)
+        case.cos, case.sin = rope_tables(int(case.q_positions.max()) + 1, 128, 500000.0, device)
+    q_rot, k_rot = _rotate(case)
+    nl = case.lat_k.shape[1]
+    bpos = (torch.arange(nl, device=device) * 4 + 4)[None].expand(3, -1).contiguous()
+    out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                    case.up_v, case.scale, beacon_positions=bpos, up_k_bias=bk, up_v_bias=bv,
+                                    block_diagonal=True, lat_causal=insertion, q_positions=case.q_positions,
+                                    cos=case.cos, sin=case.sin)
+    torch.cuda.synchronize()
+    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, insertion, bk, bv)
+    got = to_np(out.transpose(1, 2))
+    assert_close(got, exact, what='vs float64')
+    assert_close(got, eager, what='vs bf16 eager')
+    assert_lse_close(to_np(lse), lse_e)
+
+
+def test_recon_decode_fused_ragged_lengths(device):
+    """Per-sequence beacon and raw lengths on the fused route."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=4, heads=32, context=3000, tail=100, seed=77, device=device)
+    q_rot, k_rot = _rotate(case)
+    nl, nr = case.lat_k.shape[1], case.raw_k.shape[1]
+    lat_len = torch.tensor([nl, 0, 1, nl // 3], dtype=torch.int32, device=device)
+    raw_len = torch.tensor([nr, 7, nr - 3, 1], dtype=torch.int32, device=device)
+    bpos = (torch.arange(nl, device=device) * 4 + 4)[None].expand(4, -1).contiguous()
+    out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                    case.up_v, case.scale, beacon_positions=bpos, block_diagonal=True,
+                                    q_positions=case.q_positions, cos=case.cos, sin=case.sin,
+                                    lat_lengths=lat_len, raw_lengths=raw_len)
+    torch.cuda.synchronize()
+    from types import SimpleNamespace
+    for b in range(4):
+        nb, rb = int(lat_len[b]), int(raw_len[b])
+        sub = SimpleNamespace(kv_heads=case.kv_heads, scale=case.scale, cos=case.cos, sin=case.sin,
+                              lat_k=case.lat_k[b:b + 1, :nb], lat_v=case.lat_v[b:b + 1, :nb],
+                              up_k=case.up_k, up_v=case.up_v, raw_v=case.raw_v[b:b + 1, :rb])
+        exact, _, lse_e = _recon_oracles(sub, q_rot[b:b + 1], k_rot[b:b + 1, :, :rb], bpos[b:b + 1, :nb], False)
+        assert_close(to_np(out.transpose(1, 2))[b:b + 1], exact, what=f'sequence {b}')
+        assert_lse_close(to_np(lse)[b:b + 1], lse_e)
+
+
+def test_recon_decode_general_rope_tables_take_the_materialising_route(device):
+    """RoPE tables whose rows do not repeat their first half cannot use the
+    fused route's half-row pairs; the call rebuilds rotated K into the
+    workspace instead and still matches the oracle."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=2, heads=32, context=1500, tail=64, seed=91, device=device)
+    gen = torch.Generator(device=device).manual_seed(92)
+    rows = case.cos.shape[0]
+    ang = torch.rand(rows, 128, generator=gen, device=device) * 6.28
+    case.cos, case.sin = torch.cos(ang), torch.sin(ang)          # no repeated halves
+    _, repeats = kernels.prepare_rope_pairs(case.cos, case.sin)
+    assert not repeats
+    q_rot, k_rot = _rotate(case)
+    nl = case.lat_k.shape[1]
+    bpos = (torch.arange(nl, device=device) * 4 + 4)[None].expand(2, -1).contiguous()
+    out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                    case.up_v, case.scale, beacon_positions=bpos, block_diagonal=True,
+                                    q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    torch.cuda.synchronize()
+    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, False)
+    got = to_np(out.transpose(1, 2))
+    assert_close(got, exact, what='vs float64')
+    assert_close(got, eager, what='vs bf16 eager')
+    assert_lse_close(to_np(lse), lse_e)
