@@ -683,46 +683,44 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
 #pragma unroll
             for (int tt = 0; tt < 8; ++tt) kc[tt] = mfma16(as_v4s(wa[tt][ks].x, wa[tt][ks].y), bop, kc[tt]);
         }
-        // bias add and bf16 rounding, two features per packed conversion
-        uint32_t xb[8][2];
-#pragma unroll
-        for (int tt = 0; tt < 8; ++tt)
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                // a missing bias is held as +0: x + 0 is x except that -0 becomes +0
-                xb[tt][hh] = pack_bf16(kc[tt][2 * hh] + lo_bf16(bias2[tt][hh]), kc[tt][2 * hh + 1] + hi_bf16(bias2[tt][hh]));
-            }
         u32x2 kop[8];
         if constexpr (ROPE) {
-            // rotate_half pairs d with d + 64 (t with t + 4) under the same (c, s):
+            // x = bf16(acc + bias) as floats (a missing bias is held as +0: x + 0
+            // is x except that -0 becomes +0).  rotate_half pairs d with d + 64
+            // (t with t + 4) under the same (c, s):
             //   y[d]      = bf16(bf16(x[d] * c) + bf16(-x[d + 64] * s))
             //   y[d + 64] = bf16(bf16(x[d + 64] * c) + bf16(x[d] * s))
+            float x[8][4];
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t bw = bias2[tt][i >> 1];
+                    x[tt][i] = round_bf16_hw(kc[tt][i] + ((i & 1) ? hi_bf16(bw) : lo_bf16(bw)));
+                }
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
                 const uint32_t cw[4] = {cs[tt].x, cs[tt].y, cs[tt].z, cs[tt].w};
-                uint32_t ya[2], yb[2];
+                float ya[4], yb[4];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    float a[2], bq[2];
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        const float xa = e ? hi_bf16(xb[tt][hh]) : lo_bf16(xb[tt][hh]);
-                        const float xz = e ? hi_bf16(xb[tt + 4][hh]) : lo_bf16(xb[tt + 4][hh]);
-                        const float c = lo_bf16(cw[2 * hh + e]), sn = hi_bf16(cw[2 * hh + e]);
-                        const uint32_t pa = pack_bf16(xa * c, -xz * sn);
-                        const uint32_t pb = pack_bf16(xz * c, xa * sn);
-                        a[e] = lo_bf16(pa) + hi_bf16(pa);
-                        bq[e] = lo_bf16(pb) + hi_bf16(pb);
-                    }
-                    ya[hh] = pack_bf16(a[0], a[1]);
-                    yb[hh] = pack_bf16(bq[0], bq[1]);
+                for (int i = 0; i < 4; ++i) {
+                    const float c = lo_bf16(cw[i]), sn = hi_bf16(cw[i]);
+                    const float xa = x[tt][i], xz = x[tt + 4][i];
+                    ya[i] = round_bf16_hw(xa * c) + round_bf16_hw(-xz * sn);
+                    yb[i] = round_bf16_hw(xz * c) + round_bf16_hw(xa * sn);
                 }
-                kop[tt] = u32x2{ya[0], ya[1]};
-                kop[tt + 4] = u32x2{yb[0], yb[1]};
+                kop[tt] = u32x2{pack_bf16(ya[0], ya[1]), pack_bf16(ya[2], ya[3])};
+                kop[tt + 4] = u32x2{pack_bf16(yb[0], yb[1]), pack_bf16(yb[2], yb[3])};
             }
         } else {
 #pragma unroll
-            for (int tt = 0; tt < 8; ++tt) kop[tt] = u32x2{xb[tt][0], xb[tt][1]};
+            for (int tt = 0; tt < 8; ++tt) {
+                uint32_t w2[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+                    w2[hh] = pack_bf16(kc[tt][2 * hh] + lo_bf16(bias2[tt][hh]), kc[tt][2 * hh + 1] + hi_bf16(bias2[tt][hh]));
+                kop[tt] = u32x2{w2[0], w2[1]};
+            }
         }
         // scores S^T[key, col]
         v4f sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};

@@ -44,6 +44,8 @@ typedef float f32x2_hw __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_hw{a, b}, bf16x2_hw));
 }
+// bf16(x) as a float in one packed conversion: bf16(0) lands in the low half.
+__device__ __forceinline__ float round_bf16_hw(float x) { return __uint_as_float(pack_bf16(0.f, x)); }
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
