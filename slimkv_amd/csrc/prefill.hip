@@ -7,9 +7,11 @@
 //
 // Work split.  A workgroup is 4 waves and owns 128 query rows of one head;
 // each wave owns 32 rows (two 16-column MFMA tiles).  Keys stream through LDS
-// in tiles of 64: K row-major ([key][d]) and V transposed ([d][key]), both
-// prefetched into registers one tile ahead so global latency hides under the
-// current tile's MFMAs.
+// in tiles of 64: K row-major ([key][d]) and V transposed ([d][key]), double
+// buffered so one barrier per tile separates writing tile t+1 from reading
+// tile t, and prefetched into registers two tiles ahead so global latency
+// hides under the MFMAs.  Tiles that every query of the wave sees in full
+// skip the mask.
 //
 // Layouts (lane l, col = l % 16, grp = l / 16; the 16x16x32 MFMA takes
 // A[col][8*grp + j], B[8*grp + j][col] and returns D[4*grp + i][col]):
@@ -37,7 +39,7 @@ constexpr int kD = 128;                  // head dim
 constexpr int kQRows = 128;              // query rows per workgroup
 constexpr int kKeys = 64;                // keys per tile
 constexpr int kKStride = kD + 8;         // K tile row (bf16), 272 B
-constexpr int kVStride = kKeys + 4;      // V^T tile row (bf16), 136 B
+constexpr int kVStride = kKeys + 8;      // V^T tile row (bf16), 144 B: 16-byte aligned reads
 constexpr int kXcds = 8;
 
 struct PrefillParams {
@@ -52,8 +54,14 @@ struct PrefillParams {
     float scale_log2;
 };
 
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16(lo, hi); }
+
+// V^T keeps, per 32-key step, the keys a lane group reads together side by
+// side: key 16h + 4g + j of the step sits at 8g + 4h + j, so the eight keys of
+// lane group g (4g + j and 16 + 4g + j, the P^T contraction order) are one
+// 16-byte read.
+__device__ __forceinline__ int vt_pos(int kq) {       // kq: group of 4 keys in the 64-key tile
+    return 32 * (kq >> 3) + 8 * (kq & 3) + 4 * ((kq >> 2) & 1);
 }
 
 __device__ __forceinline__ uint32_t half_of(const u32x4& v, int e) {
@@ -96,14 +104,14 @@ __device__ __forceinline__ void store_tile(const TileRegs& t, uint16_t* ks, uint
         u32x2 w;
         w.x = half_of(t.v[0], e) | (half_of(t.v[1], e) << 16);
         w.y = half_of(t.v[2], e) | (half_of(t.v[3], e) << 16);
-        *reinterpret_cast<u32x2*>(vts + (8 * cp + e) * kVStride + 4 * kq) = w;
+        *reinterpret_cast<u32x2*>(vts + (8 * cp + e) * kVStride + vt_pos(kq)) = w;
     }
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_kernel(PrefillParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t ks[kKeys * kKStride];
-    __shared__ __attribute__((aligned(16))) uint16_t vts[kD * kVStride];
+    __shared__ __attribute__((aligned(16))) uint16_t ks_buf[2][kKeys * kKStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vts_buf[2][kD * kVStride];
 
     const int g = p.Hq / p.Hk;
     const int xcd = blockIdx.x % kXcds;
@@ -153,14 +161,20 @@ prefill_kernel(PrefillParams p) {
     const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)kvh * p.k_sh;
     const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
     TileRegs tr;
-    if (ntiles > 0) load_tile(tr, kb, vb, p.k_sn, p.v_sn, 0, n);
+    if (ntiles > 0) {
+        load_tile(tr, kb, vb, p.k_sn, p.v_sn, 0, n);
+        store_tile(tr, ks_buf[0], vts_buf[0]);
+        if (ntiles > 1) load_tile(tr, kb, vb, p.k_sn, p.v_sn, kKeys, n);
+        __syncthreads();
+    }
+    // the wave's earliest query sees keys up to q0 + shift
+    const int wave_last = p.causal ? q0 + shift : n - 1;
 
     for (int t = 0; t < ntiles; ++t) {
         const int k0 = t * kKeys;
-        __syncthreads();
-        store_tile(tr, ks, vts);
-        __syncthreads();
-        if (t + 1 < ntiles) load_tile(tr, kb, vb, p.k_sn, p.v_sn, k0 + kKeys, n);
+        const uint16_t* ks = ks_buf[t & 1];
+        const uint16_t* vts = vts_buf[t & 1];
+        const bool full = k0 + kKeys - 1 <= min(wave_last, n - 1);
 
         // S^T = K . Q^T for 64 keys x 32 queries
         v4f s[4][2];
@@ -185,18 +199,25 @@ prefill_kernel(PrefillParams p) {
             const int qi = q0 + 16 * nt + col;
             const int last = p.causal ? min(qi + shift, n - 1) : n - 1;
             float mx = kNegInf;
+            // raw scores: the scale (> 0) is applied inside the exponent's FMA
+            if (full) {
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
+                for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int kj = k0 + 16 * mt + 4 * grp + i;
-                    const float x = kj <= last ? s[mt][nt][i] * p.scale_log2 : kNegInf;
-                    s[mt][nt][i] = x;
-                    mx = fmaxf(mx, x);
-                }
+                    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
+            } else {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float x = k0 + 16 * mt + 4 * grp + i <= last ? s[mt][nt][i] : kNegInf;
+                        s[mt][nt][i] = x;
+                        mx = fmaxf(mx, x);
+                    }
+            }
             mx = fmaxf(mx, shfl_xor_f(mx, 16));
             mx = fmaxf(mx, shfl_xor_f(mx, 32));
-            const float m_new = fmaxf(m[nt], mx);
+            const float m_new = fmaxf(m[nt], mx * p.scale_log2);
             const float base = m_new == kNegInf ? 0.f : m_new;
             const float alpha = fast_exp2(m[nt] - base);
             m[nt] = m_new;
@@ -205,13 +226,17 @@ prefill_kernel(PrefillParams p) {
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float e = fast_exp2(s[mt][nt][i] - base);
+                    const float e = fast_exp2(__builtin_fmaf(s[mt][nt][i], p.scale_log2, -base));
                     s[mt][nt][i] = e;
                     sum += e;
                 }
             l[nt] = l[nt] * alpha + sum;
+            // once the running maxima settle (most tiles of a long window) no
+            // column's alpha moves off 1, and the wave skips the rescale
+            if (__ballot(alpha != 1.f)) {
 #pragma unroll
-            for (int md = 0; md < 8; ++md) o[md][nt] *= alpha;
+                for (int md = 0; md < 8; ++md) o[md][nt] *= alpha;
+            }
 #pragma unroll
             for (int ss = 0; ss < 2; ++ss)
                 pb[ss][nt] = u32x4{pack2(s[2 * ss][nt][0], s[2 * ss][nt][1]), pack2(s[2 * ss][nt][2], s[2 * ss][nt][3]),
@@ -224,14 +249,19 @@ prefill_kernel(PrefillParams p) {
         for (int ss = 0; ss < 2; ++ss) {
 #pragma unroll
             for (int md = 0; md < 8; ++md) {
-                const uint16_t* row = vts + (16 * md + col) * kVStride + 32 * ss + 4 * grp;
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(row);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(row + 16);
-                const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+                const u32x4 a = *reinterpret_cast<const u32x4*>(vts + (16 * md + col) * kVStride + 32 * ss + 8 * grp);
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) o[md][nt] = mfma32(a, pb[ss][nt], o[md][nt]);
             }
         }
+        // tile t + 1 (in registers) into the other buffer, then fetch tile t + 2;
+        // the barrier orders this write after every wave's reads of tile t - 1
+        // and before every wave's reads of tile t + 1
+        if (t + 1 < ntiles) {
+            store_tile(tr, ks_buf[(t + 1) & 1], vts_buf[(t + 1) & 1]);
+            if (t + 2 < ntiles) load_tile(tr, kb, vb, p.k_sn, p.v_sn, k0 + 2 * kKeys, n);
+        }
+        __syncthreads();
     }
 
 #pragma unroll
@@ -274,6 +304,7 @@ extern "C" int slimkv_prefill_attention(const slimkv_prefill_attention_args* a, 
         if (s % 8) return fail(SLIMKV_EINVAL, "strides must be multiples of 8 elements");
     if (!al16(a->q) || !al16(a->k) || !al16(a->v) || !al16(a->out))
         return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
+    if (!(a->scale > 0.0)) return fail(SLIMKV_EINVAL, "the softmax scale must be positive");
     if (a->batch == 0 || a->queries == 0) return SLIMKV_OK;
     PrefillParams p{};
     p.q = static_cast<const uint16_t*>(a->q); p.q_sb = a->q_sb; p.q_sl = a->q_sl; p.q_sh = a->q_sh;

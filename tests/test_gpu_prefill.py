@@ -51,6 +51,36 @@ def test_causal_prefill_matches_oracle(device, B, Lq, N, Hq, Hk):
     _run(device, B, Lq, N, Hq, Hk, True, seed=Lq + N)
 
 
+@pytest.mark.parametrize('B,Lq,N,Hq,Hk,seqlens', [
+    (4, 1280, 1540, 32, 8, None),           # the window-prefill benchmark shape
+    (8, 300, 700, 64, 8, [700, 1, 0, 333, 700, 64, 650, 2]),   # ragged keys, partial last block
+])
+def test_wide_query_tiles_on_sampled_heads(device, B, Lq, N, Hq, Hk, seqlens):
+    """Full-size grids (hundreds of workgroups, ragged key lengths, a partial
+    last query block); the oracle checks a sample of (batch, head) slices."""
+    from slimkv_amd import kernels
+    gen = torch.Generator(device=device).manual_seed(Lq)
+    q = torch.randn(B, Lq, Hq, 128, generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn(B, N, Hk, 128, generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn(B, N, Hk, 128, generator=gen, device=device).to(torch.bfloat16)
+    scale = 128 ** -0.5
+    lens = None if seqlens is None else torch.tensor(seqlens, dtype=torch.int32, device=device)
+    out, lse = kernels.prefill_attention(q, k, v, scale, True, seqlens_k=lens)
+    torch.cuda.synchronize()
+    g = Hq // Hk
+    for b, h in [(0, 0), (B - 1, Hq - 1), (1, g), (B // 2, Hq // 2 + 1), (3, 5)]:
+        n = N if seqlens is None else seqlens[b]
+        got = to_np(out[b:b + 1, :, h:h + 1])
+        if n == 0:
+            assert not got.any() and np.isneginf(to_np(lse[b, h])).all()
+            continue
+        qn = to_np(q[b:b + 1, :, h:h + 1])
+        kn, vn = to_np(k[b:b + 1, :n, h // g:h // g + 1]), to_np(v[b:b + 1, :n, h // g:h // g + 1])
+        o, l = oa.eager_forward(qn, kn, vn, scale, True)
+        assert_close(got, o, what=f'batch {b} head {h}')
+        assert_lse_close(to_np(lse[b:b + 1, h:h + 1]), l)
+
+
 def test_non_causal_and_strided_kv(device):
     _run(device, 2, 90, 250, 8, 2, False, seed=1, strided=True)
 
