@@ -10,9 +10,12 @@
 // These copies are HBM-bound byte moves: one thread moves one 16-byte piece
 // (VEC = 8 bf16) whenever every row start and width allows it, else one
 // element.  blockIdx.y is the request, so a request's rows are contiguous in
-// the grid and neighbouring threads touch neighbouring bytes of a row.
+// the grid and neighbouring threads touch neighbouring bytes of a row; a raw
+// token is one workgroup (its block looked up once, 32-bit index math).
 
 #include "common.hpp"
+
+#include <algorithm>
 
 namespace slimkv {
 
@@ -45,29 +48,30 @@ beacon_pages_kernel(slimkv_beacon_pages_args a) {
     else copy_piece<VEC>(dn, pg);
 }
 
+// One workgroup per (token, request): the token's block is looked up once and
+// the 2 * Hkv * D elements of its K and V rows are moved with 32-bit index math.
 template <int VEC>
 __global__ void __launch_bounds__(256)
 raw_pages_kernel(slimkv_raw_pages_args a) {
     const int64_t b = blockIdx.y;
-    const int64_t D = a.head_dim, H = a.kv_heads;
-    const int64_t per_tok = 2 * H * D / VEC;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= a.count * per_tok) return;
-    const int64_t r = gid / per_tok;
-    const int64_t e = (gid % per_tok) * VEC;
-    const int64_t kind = e / (H * D);
-    const int64_t h = (e / D) % H;
-    const int64_t d = e % D;
+    const int64_t r = blockIdx.x;
     const int64_t t = a.start + r;
     if (a.lengths && t >= a.lengths[b]) return;
     const int64_t block = a.table[b * a.t_sb + t / a.block_size];
     if (block < 0 || block >= a.num_blocks) return;
-    uint16_t* pg = static_cast<uint16_t*>(a.pages) + block * a.p_sblk + (t % a.block_size) * a.p_stok +
-                   kind * a.p_skind + h * a.p_sh + d;
-    uint16_t* dn = kind ? static_cast<uint16_t*>(a.dense_v) + b * a.dv_sb + h * a.dv_sh + r * a.dv_sn + d
-                        : static_cast<uint16_t*>(a.dense_k) + b * a.dk_sb + h * a.dk_sh + r * a.dk_sn + d;
-    if (a.to_pages) copy_piece<VEC>(pg, dn);
-    else copy_piece<VEC>(dn, pg);
+    const int dv = (int)a.head_dim / VEC, hd = (int)a.kv_heads * dv;
+    uint16_t* pg = static_cast<uint16_t*>(a.pages) + block * a.p_sblk + (t % a.block_size) * a.p_stok;
+    for (int i = threadIdx.x; i < 2 * hd; i += blockDim.x) {
+        const int kind = i >= hd;
+        const int rem = i - kind * hd;
+        const int h = rem / dv;
+        const int d = (rem - h * dv) * VEC;
+        uint16_t* pe = pg + kind * a.p_skind + h * a.p_sh + d;
+        uint16_t* dn = kind ? static_cast<uint16_t*>(a.dense_v) + b * a.dv_sb + h * a.dv_sh + r * a.dv_sn + d
+                            : static_cast<uint16_t*>(a.dense_k) + b * a.dk_sb + h * a.dk_sh + r * a.dk_sn + d;
+        if (a.to_pages) copy_piece<VEC>(pe, dn);
+        else copy_piece<VEC>(dn, pe);
+    }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -111,12 +115,14 @@ extern "C" int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream) {
         a->batch < 0 || a->batch > 65535 || a->num_blocks < 0)
         return fail(SLIMKV_EINVAL, "invalid raw page layout");
     if (a->count == 0 || a->batch == 0) return SLIMKV_OK;
-    const int64_t items = a->count * 2 * a->kv_heads * a->head_dim;
+    if (a->count > ((int64_t)1 << 31) - 1 || a->kv_heads * a->head_dim > (1 << 20))
+        return fail(SLIMKV_EINVAL, "raw copy too large");
     const bool vec = all_multiple_of_8({a->head_dim, a->p_sblk, a->p_stok, a->p_skind, a->p_sh, a->dk_sb, a->dk_sh,
                                         a->dk_sn, a->dv_sb, a->dv_sh, a->dv_sn}) &&
                      aligned16(a->pages) && aligned16(a->dense_k) && aligned16(a->dense_v);
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    if (vec) hipLaunchKernelGGL(raw_pages_kernel<8>, io_grid(items / 8, a->batch), dim3(256), 0, st, *a);
-    else hipLaunchKernelGGL(raw_pages_kernel<1>, io_grid(items, a->batch), dim3(256), 0, st, *a);
+    const dim3 grid((unsigned)a->count, (unsigned)a->batch);
+    if (vec) hipLaunchKernelGGL(raw_pages_kernel<8>, grid, dim3(256), 0, st, *a);
+    else hipLaunchKernelGGL(raw_pages_kernel<1>, grid, dim3(256), 0, st, *a);
     return check_hip(hipGetLastError(), "raw page kernel launch");
 }
