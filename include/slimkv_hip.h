@@ -340,6 +340,27 @@ size_t slimkv_down_project_workspace(const slimkv_down_project_args* a);
 int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* The down-projection with its epilogue writing the latents straight into
+ * beacon pages (no dense staging, no separate append).  Replaces the
+ * projection of the window's beacon rows (modeling_llama.py:1347-1367)
+ * followed by flush_memory's BeaconPages.append of those rows
+ * (slimkv/vllm_plugin/paged_model.py:55-84, paged_cache.py:69-87).
+ * Row i of request b is beacon start + i: page table[b*t_sb + (start+i)/slots]
+ * (t_cols entries per row), columns sink_elements + ((start+i) % slots) *
+ * slot_width + column + [0, out_features); column is 0 for the K latent and
+ * key_rank for the V latent (BeaconPageLayout, paged_cache.py:27-44).  Rows
+ * whose table index or page id falls outside the table or pool are skipped.
+ * a->out / o_sb / o_sn are ignored; workspace as slimkv_down_project. */
+typedef struct slimkv_page_rows {
+    void* pages; int64_t num_pages, page_stride;
+    const int64_t* table; int64_t t_sb, t_cols;
+    int64_t slots, sink_elements, slot_width, column;
+    int64_t start;
+} slimkv_page_rows;
+
+int slimkv_down_project_to_pages(const slimkv_down_project_args* a, const slimkv_page_rows* dst, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Beacon-page I/O: exact bf16 copies between engine-owned pages and dense
  * latent rows, for `batch` requests at once.

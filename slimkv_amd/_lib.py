@@ -135,6 +135,13 @@ DownProjectArgs = _struct('slimkv_down_project_args', [
     *_i64s('batch', 'in_features', 'out_features', 'blocks'),
 ])
 
+PageRows = _struct('slimkv_page_rows', [
+    ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
+    ('table', c_ptr), *_i64s('t_sb', 't_cols'),
+    *_i64s('slots', 'sink_elements', 'slot_width', 'column'),
+    ('start', c_i64),
+])
+
 BeaconPagesArgs = _struct('slimkv_beacon_pages_args', [
     ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
     ('table', c_ptr), ('t_sb', c_i64),
@@ -178,11 +185,13 @@ SIGNATURES = {
     'slimkv_prefill_attention': (ctypes.c_int, [ctypes.POINTER(PrefillAttentionArgs), c_ptr]),
     'slimkv_down_project_workspace': (ctypes.c_size_t, [ctypes.POINTER(DownProjectArgs)]),
     'slimkv_down_project': (ctypes.c_int, [ctypes.POINTER(DownProjectArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_down_project_to_pages': (ctypes.c_int, [ctypes.POINTER(DownProjectArgs), ctypes.POINTER(PageRows), c_ptr,
+                                                    ctypes.c_size_t, c_ptr]),
     'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class SlimKVError(RuntimeError):

@@ -1500,7 +1500,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 4; }
+extern "C" int slimkv_abi_version(void) { return 5; }
 
 extern "C" int slimkv_set_profile_events(void* before, void* after) {
     if ((before == nullptr) != (after == nullptr)) return fail(SLIMKV_EINVAL, "set both events or neither");

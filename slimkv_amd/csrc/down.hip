@@ -30,7 +30,22 @@ struct DownParams {
     uint16_t* out; int64_t o_sb, o_sn;
     float* part;                 // [splits, M, N] when splits > 1
     int B, n, N, K, blocks, splits, kchunk;
+    // Page destination (table != null): row i of request b is beacon start + i,
+    // written at out + page * page_stride + ((start + i) % slots) * slot_width
+    // with page = table[b * t_sb + (start + i) / slots]; rows whose table
+    // entry lies outside [0, t_cols) or whose page lies outside the pool are skipped.
+    const int64_t* table; int64_t t_sb, t_cols, slots, page_stride, num_pages, slot_width, start;
 };
+
+__device__ __forceinline__ uint16_t* dst_row(const DownParams& p, int b, int i) {
+    if (!p.table) return p.out + (int64_t)b * p.o_sb + (int64_t)i * p.o_sn;
+    const int64_t beacon = p.start + i;
+    const int64_t idx = beacon / p.slots;
+    if (idx >= p.t_cols) return nullptr;
+    const int64_t page = p.table[(int64_t)b * p.t_sb + idx];
+    if (page < 0 || page >= p.num_pages) return nullptr;
+    return p.out + page * p.page_stride + (beacon % p.slots) * p.slot_width;
+}
 
 constexpr int kMFrags = 4;       // 64 rows per wave
 
@@ -88,7 +103,8 @@ __global__ void __launch_bounds__(256) down_kernel(DownParams p) {
             u32x2 w;
             w.x = f32_to_bf16(acc[f][0]) | (f32_to_bf16(acc[f][1]) << 16);
             w.y = f32_to_bf16(acc[f][2]) | (f32_to_bf16(acc[f][3]) << 16);
-            *reinterpret_cast<u32x2*>(p.out + (int64_t)b * p.o_sb + (int64_t)i * p.o_sn + nn) = w;
+            uint16_t* dst = dst_row(p, b, i);
+            if (dst) *reinterpret_cast<u32x2*>(dst + nn) = w;
         } else {
             *reinterpret_cast<v4f*>(p.part + ((int64_t)s * M_ + m) * p.N + nn) = acc[f];
         }
@@ -109,7 +125,8 @@ __global__ void __launch_bounds__(256) down_reduce_kernel(DownParams p) {
     u32x2 w;
     w.x = f32_to_bf16(sum[0]) | (f32_to_bf16(sum[1]) << 16);
     w.y = f32_to_bf16(sum[2]) | (f32_to_bf16(sum[3]) << 16);
-    *reinterpret_cast<u32x2*>(p.out + (int64_t)b * p.o_sb + (int64_t)i * p.o_sn + nn) = w;
+    uint16_t* dst = dst_row(p, b, i);
+    if (dst) *reinterpret_cast<u32x2*>(dst + nn) = w;
 }
 
 bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -157,8 +174,10 @@ extern "C" size_t slimkv_down_project_workspace(const slimkv_down_project_args* 
     return std::max<size_t>(plan.bytes, 1);
 }
 
-extern "C" int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+namespace {
+
+int down_run(const slimkv_down_project_args* a, const slimkv_page_rows* pg, void* workspace, size_t workspace_bytes,
+             void* stream) {
     DownPlan plan{};
     int rc = plan_down(a, &plan);
     if (rc != SLIMKV_OK) return rc;
@@ -174,6 +193,12 @@ extern "C" int slimkv_down_project(const slimkv_down_project_args* a, void* work
     p.part = static_cast<float*>(workspace);
     p.B = (int)a->batch; p.n = (int)a->row_count; p.N = (int)a->out_features; p.K = (int)a->in_features;
     p.blocks = (int)a->blocks; p.splits = plan.splits; p.kchunk = plan.kchunk;
+    if (pg) {
+        p.out = static_cast<uint16_t*>(pg->pages) + pg->sink_elements + pg->column;
+        p.table = pg->table; p.t_sb = pg->t_sb; p.t_cols = pg->t_cols; p.slots = pg->slots;
+        p.page_stride = pg->page_stride; p.num_pages = pg->num_pages; p.slot_width = pg->slot_width;
+        p.start = pg->start;
+    }
     const int64_t grid = (p.N + 63) / 64 * ((M + 63) / 64) * p.splits;
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(down_kernel, dim3((unsigned)grid), dim3(256), 0, st, p);
@@ -182,4 +207,26 @@ extern "C" int slimkv_down_project(const slimkv_down_project_args* a, void* work
     const int64_t quads = M * (p.N / 4);
     hipLaunchKernelGGL(down_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, p);
     return check_hip(hipGetLastError(), "down-projection reduce launch");
+}
+
+}  // namespace
+
+extern "C" int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    return down_run(a, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int slimkv_down_project_to_pages(const slimkv_down_project_args* a, const slimkv_page_rows* dst,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+    if (!a || !dst || !dst->pages || !dst->table) return fail(SLIMKV_EINVAL, "null pointer");
+    if (dst->num_pages < 0 || dst->slots <= 0 || dst->t_cols <= 0 || dst->t_sb < dst->t_cols || dst->start < 0 ||
+        dst->sink_elements < 0 || dst->column < 0 || dst->column + a->out_features > dst->slot_width ||
+        dst->page_stride < dst->sink_elements + dst->slots * dst->slot_width)
+        return fail(SLIMKV_EINVAL, "invalid page destination");
+    if ((dst->page_stride | dst->sink_elements | dst->column | dst->slot_width) % 4 ||
+        (reinterpret_cast<uintptr_t>(dst->pages) & 7))
+        return fail(SLIMKV_EINVAL, "page rows must be 8-byte aligned");
+    slimkv_down_project_args b = *a;
+    b.out = dst->pages; b.o_sb = 0; b.o_sn = 0;
+    return down_run(&b, dst, workspace, workspace_bytes, stream);
 }

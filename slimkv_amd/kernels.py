@@ -136,6 +136,47 @@ def down_project(x, weight, rows=None, *, blocks=1, out=None):
     return out
 
 
+def down_project_to_pages(x, weight, pages, table, layout, start, kind, rows=None, *, blocks=1):
+    """down_project with the latents written straight into beacon pages:
+    row i of request b becomes beacon `start + i` of that request (its K
+    latent when kind == 'k', V latent when 'v'), at the BeaconPageLayout
+    position table[b, (start + i) // slots].  pages [num_pages, >= page
+    elements] bf16, table [B, T] int64.  Rows mapping outside the table or
+    pool are skipped."""
+    _need_device(x, weight, rows, pages, table)
+    _need_bf16(x, weight, pages)
+    if kind not in ('k', 'v'):
+        raise ValueError("kind must be 'k' or 'v'")
+    if x.dim() != 3 or weight.dim() != 2 or weight.shape[1] != x.shape[2]:
+        raise ValueError('x must be [B, L, K] and weight [N, K]')
+    if pages.dim() != 2 or pages.stride(1) != 1 or pages.shape[1] < layout.page_elements:
+        raise ValueError('pages must be [num_pages, page_elements] with contiguous rows')
+    if table.dtype != torch.int64 or table.dim() != 2 or table.shape[0] != x.shape[0]:
+        raise ValueError('table must be int64 [B, T]')
+    N = weight.shape[0]
+    if N != (layout.key_rank if kind == 'k' else layout.value_rank):
+        raise ValueError('weight rows differ from the layout rank')
+    x = _last_contiguous(x)
+    weight = weight.contiguous()
+    table = table if table.stride(1) == 1 else table.contiguous()
+    B, L, K = x.shape
+    if rows is not None:
+        rows = rows.to(dtype=torch.long).contiguous()
+    n = L if rows is None else rows.numel()
+    a = _lib.DownProjectArgs(_ptr(x), x.stride(0), x.stride(1), _ptr(rows), n, L, _ptr(weight),
+                             _ptr(pages), 0, 0, B, K, N, int(blocks))
+    dst = _lib.PageRows(_ptr(pages), pages.shape[0], pages.stride(0), _ptr(table), table.stride(0), table.shape[1],
+                        layout.slots, layout.sink_elements, layout.width, 0 if kind == 'k' else layout.key_rank,
+                        int(start))
+    nbytes = lib().slimkv_down_project_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    ws = _workspace(nbytes, x.device)
+    check(lib().slimkv_down_project_to_pages(ctypes.byref(a), ctypes.byref(dst), _ptr(ws), nbytes,
+                                             _lib.stream_handle(x.device)))
+    return pages
+
+
 def prepare_latent_bases(up_k, kv_heads):
     """Per-head transposed K bases [Hkv, Rk/Hkv, D] of a block-diagonal up_k
     [Hkv*D, Rk], made once per weight version and cached on the tensor."""

@@ -117,3 +117,37 @@ def test_rejects_tables_narrower_than_the_beacon_count(device):
         kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'][:, :10], c['lengths'],
                                     c['lat_keys'], c['layout'], c['up_k'], c['up_v'], D ** -0.5,
                                     block_diagonal=True, raw_lengths=c['raw_lengths'])
+
+
+@pytest.mark.parametrize('layout_args,start,blocks', [((16, 8, 256, 256, 1024), 3, 8), ((16, 4, 256, 256, 1024), 0, 8),
+                                                      ((12, 4, 128, 384, 1024), 5, 1)])
+def test_down_projection_into_pages_equals_project_then_append(device, layout_args, start, blocks):
+    """The down-projection epilogue writing beacon latents straight into pages
+    leaves every page element exactly as projecting to a dense buffer and
+    appending it (BeaconPages.append_batch) does, untouched elements included."""
+    from slimkv_amd import kernels
+    from slimkv_amd.paged_cache import BeaconPageLayout, BeaconPages
+    layout = BeaconPageLayout(*layout_args)
+    gen = torch.Generator(device=device).manual_seed(start + blocks)
+    B, L, K, n = 3, 300, 1024, 70
+    x = torch.randn(B, L, K, generator=gen, device=device).to(torch.bfloat16)
+    rows = torch.randperm(L, generator=torch.Generator().manual_seed(4))[:n].sort().values.to(device)
+    wk = (torch.randn(layout.key_rank, K, generator=gen, device=device) / 32).to(torch.bfloat16)
+    wv = (torch.randn(layout.value_rank, K, generator=gen, device=device) / 32).to(torch.bfloat16)
+    if blocks > 1:   # block-diagonal per-head bases
+        mk = torch.block_diag(*[torch.ones(layout.key_rank // blocks, K // blocks)] * blocks).to(device)
+        mv = torch.block_diag(*[torch.ones(layout.value_rank // blocks, K // blocks)] * blocks).to(device)
+        wk, wv = (wk * mk).to(torch.bfloat16), (wv * mv).to(torch.bfloat16)
+    pages_per_seq = (start + n + layout.slots - 1) // layout.slots
+    pool = B * pages_per_seq + 5
+    table = torch.randperm(pool, generator=torch.Generator().manual_seed(5))[:B * pages_per_seq]
+    table = table.view(B, pages_per_seq).to(device)
+    base = torch.randn(pool, layout.page_elements + 8, generator=gen, device=device).to(torch.bfloat16)
+    want, got = base.clone(), base.clone()
+    k = kernels.down_project(x, wk, rows, blocks=blocks)
+    v = kernels.down_project(x, wv, rows, blocks=blocks)
+    BeaconPages(want[:, :layout.page_elements], layout).append_batch(table, start, k, v)
+    kernels.down_project_to_pages(x, wk, got, table, layout, start, 'k', rows, blocks=blocks)
+    kernels.down_project_to_pages(x, wv, got, table, layout, start, 'v', rows, blocks=blocks)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
