@@ -1911,6 +1911,9 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     if (D != 128) return fail(SLIMKV_EUNSUP, "reconstruction decode is built for head_dim 128");
     if (a->raw_keys <= 0 || a->lat_keys < 0) return fail(SLIMKV_EINVAL, "invalid key counts");
     if (a->lat_keys > 0 && (!a->lat_k || !a->lat_v)) return fail(SLIMKV_EINVAL, "null latent pointer");
+    if (r->beacon_positions && B > 1 && r->bpos_sb < a->lat_keys)
+        return fail(SLIMKV_EINVAL, "beacon position rows are shorter than the beacon count");
+    if (r->beacon_positions && !a->cos) return fail(SLIMKV_EINVAL, "beacon RoPE needs the tables");
     const int g = (int)(Hq / Hkv);
     if (g * Lq > kMaxRows) return fail(SLIMKV_EUNSUP, "more than 16 query rows per KV head");
     const int cu = device_cu_count();

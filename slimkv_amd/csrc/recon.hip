@@ -223,6 +223,8 @@ int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
         if (!al4(s)) return fail(SLIMKV_EINVAL, "strides must be multiples of 4 elements");
     if (!pal8(a->latent) || !pal8(a->weight) || !pal8(a->out)) return fail(SLIMKV_EINVAL, "tensors must be 8-byte aligned");
     if (a->positions && (!a->cos || !a->sin || a->rope_rows <= 0)) return fail(SLIMKV_EINVAL, "RoPE needs tables");
+    if (a->positions && a->batch > 1 && a->pos_sb < a->rows)
+        return fail(SLIMKV_EINVAL, "positions rows are shorter than the row count");
     ReconParams p{};
     p.latent = static_cast<const uint16_t*>(a->latent); p.l_sb = a->l_sb; p.l_sn = a->l_sn;
     p.w = static_cast<const uint16_t*>(a->weight); p.bias = static_cast<const uint16_t*>(a->bias); p.w_ld = a->rank;
