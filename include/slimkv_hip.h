@@ -86,6 +86,9 @@ int slimkv_attention_forward(const slimkv_attention_args* a, void* workspace,
  *   (merge_attention :57-66) -- all under one online softmax.
  * q       [B, Lq, Hq, D] bf16; rotated in-kernel at q_positions [B, Lq] when
  *         `cos`/`sin` ([rope_rows, D] fp32) are given, else already rotated.
+ *         With cos/sin but no q_positions, the tables are the rows already
+ *         taken at the query positions: row b * Lq + l (rope_rows >= B * Lq),
+ *         as a model's rotary embedding returns them once per decode step.
  * raw_k/v [B, Nr, Hkv, D] bf16, K already rotated (sinks, tail, current token).
  * lat_k   [B, Nl, Rk] bf16 and lat_v [B, Nl, Rv] bf16: global latent rows.
  * up_k    [Hkv*D, Rk], up_v [Hkv*D, Rv]: nn.Linear weights of the beacon

@@ -1085,9 +1085,11 @@ combine_fast_kernel(CombineParams cp) {
 
 bool combine_fast_ok(const CombineParams& cp) {
     if (cp.b_splits && !cp.up_v) return false;
+    // Latent widths that do not divide the block (48) leave the threads past
+    // (128 / b_w) * b_w idle in the weighted sum.
     return cp.D <= kCombineThreads && cp.a_splits <= kFastRawSplits && cp.a_splits + cp.b_splits <= kCombineThreads &&
            cp.b_w <= kFastLatW && (cp.b_splits == 0 ||
-           (kCombineThreads % cp.b_w == 0 && cp.b_splits <= kFastLatPer * (kCombineThreads / cp.b_w)));
+           (cp.b_w % 8 == 0 && cp.b_splits <= kFastLatPer * (kCombineThreads / cp.b_w)));
 }
 
 void launch_combine(const CombineParams& cp, int rows, hipStream_t st) {
@@ -1117,6 +1119,14 @@ struct PrologueParams {
 
 constexpr int kMaxRows = 16;
 constexpr int kMaxD = 256;
+
+// RoPE table row of query (b, l): its position, or -- without positions --
+// row b * Lq + l of tables already taken at the query positions (one gather
+// per decode step serves every layer).
+__device__ __forceinline__ int64_t query_rope_row(const PrologueParams& pp, int b, int l) {
+    if (!pp.pos) return (int64_t)b * pp.Lq + l;
+    return clamp_i64(pp.pos[(int64_t)b * pp.pos_sb + l], 0, pp.rope_rows - 1);
+}
 
 // One workgroup per (b, KV head).  Rows r = jj*Lq + l of the head's query group
 // are rotated into LDS; thread (k8, part) then forms 8 consecutive q_lat
@@ -1149,7 +1159,7 @@ prologue_kernel(PrologueParams pp) {
             const int pd = dd < half ? dd + half : dd - half;
             const u32x4 pv = *reinterpret_cast<const u32x4*>(qrow + pd);
             const uint32_t ps[4] = {pv.x, pv.y, pv.z, pv.w};
-            const int64_t pos = clamp_i64(pp.pos[(int64_t)b * pp.pos_sb + l], 0, pp.rope_rows - 1);
+            const int64_t pos = query_rope_row(pp, b, l);
             const float4* c4 = reinterpret_cast<const float4*>(pp.cos + pos * D + dd);
             const float4* s4 = reinterpret_cast<const float4*>(pp.sin + pos * D + dd);
             const float4 ca = c4[0], cb = c4[1], sa = s4[0], sb = s4[1];
@@ -1264,7 +1274,7 @@ prologue_mfma_kernel(PrologueParams pp) {
         qr[c] = valid ? x : u32x4{0u, 0u, 0u, 0u};
     }
     if (pp.cos) {
-        const int64_t pos = clamp_i64(pp.pos[(int64_t)b * pp.pos_sb + l], 0, pp.rope_rows - 1);
+        const int64_t pos = query_rope_row(pp, b, l);
         rope_operand(qr, pp.cos + pos * D, pp.sin + pos * D, grp);
     }
     const int64_t prow = ((int64_t)b * pp.Lq + l) * pp.Hq + j;
@@ -1618,8 +1628,9 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
         return fail(SLIMKV_EINVAL, "invalid key counts");
     if (a->raw_keys <= 0) return fail(SLIMKV_EINVAL, "the raw branch always holds the current token");
     if (!pg && a->lat_keys > 0 && (!a->lat_k || !a->lat_v)) return fail(SLIMKV_EINVAL, "null latent pointer");
-    if (a->cos && (!a->sin || !a->q_positions || a->rope_rows <= 0))
-        return fail(SLIMKV_EINVAL, "RoPE needs sin, positions and a table size");
+    if (a->cos && (!a->sin || a->rope_rows <= 0)) return fail(SLIMKV_EINVAL, "RoPE needs sin and a table size");
+    if (a->cos && !a->q_positions && a->rope_rows < B * Lq)
+        return fail(SLIMKV_EINVAL, "without query positions the RoPE tables hold one row per query");
     const int64_t strides[] = {a->q_sb, a->q_sl, a->q_sh, a->rk_sb, a->rk_sn, a->rk_sh, a->rv_sb, a->rv_sn,
                                a->rv_sh, a->lk_sb, a->lk_sn, a->lv_sb, a->lv_sn};
     for (int64_t st : strides)
@@ -1914,6 +1925,9 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     if (r->beacon_positions && B > 1 && r->bpos_sb < a->lat_keys)
         return fail(SLIMKV_EINVAL, "beacon position rows are shorter than the beacon count");
     if (r->beacon_positions && !a->cos) return fail(SLIMKV_EINVAL, "beacon RoPE needs the tables");
+    if (a->cos && (!a->sin || a->rope_rows <= 0)) return fail(SLIMKV_EINVAL, "RoPE needs sin and a table size");
+    if (a->cos && !a->q_positions && (r->beacon_positions || a->rope_rows < B * Lq))
+        return fail(SLIMKV_EINVAL, "beacon RoPE needs the full tables and query positions");
     const int g = (int)(Hq / Hkv);
     if (g * Lq > kMaxRows) return fail(SLIMKV_EUNSUP, "more than 16 query rows per KV head");
     const int cu = device_cu_count();

@@ -219,12 +219,18 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
     if lse is None:
         lse = torch.empty(B, Hq, Lq, dtype=torch.float32, device=q.device)
     if cos is not None:
-        if cos.dtype != torch.float32 or sin.dtype != torch.float32 or q_positions is None:
-            raise ValueError('RoPE tables must be fp32 with int64 query positions')
+        if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+            raise ValueError('RoPE tables must be fp32')
+        if q_positions is None:
+            # tables already taken at the query positions (query_rope_rows)
+            cos, sin = cos.reshape(-1, D), sin.reshape(-1, D)
+            if cos.shape[0] < B * Lq or sin.shape != cos.shape:
+                raise ValueError('RoPE rows at the query positions must cover [B, Lq, D]')
+        else:
+            q_positions = q_positions.to(torch.int64)
+            if q_positions.stride(-1) != 1:
+                q_positions = q_positions.contiguous()
         cos, sin = cos.contiguous(), sin.contiguous()
-        q_positions = q_positions.to(torch.int64)
-        if q_positions.stride(-1) != 1:
-            q_positions = q_positions.contiguous()
     bases = None
     if prepared_bases and block_diagonal and Nl > 0 and Rk % Hkv == 0 \
             and (Rk // Hkv) % 16 == 0 and D == 128:
@@ -245,13 +251,28 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
     return a, out, lse, keep
 
 
+def query_rope_rows(cos, sin, q_positions):
+    """cos/sin rows at the query positions [B, Lq] -> ([B*Lq, D], [B*Lq, D]).
+
+    Every layer of a decode step rotates its queries at the same positions, so
+    the rows are gathered once per step (as a model's rotary embedding returns
+    them) and passed to each layer's latent_decode with q_positions=None; the
+    rotation is then the same, without the position lookup in every layer.
+    Positions are clamped into the tables like the kernels clamp them."""
+    _need_device(cos, sin, q_positions)
+    idx = q_positions.reshape(-1).to(torch.int64).clamp(0, cos.shape[0] - 1)
+    return cos.index_select(0, idx), sin.index_select(0, idx)
+
+
 def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias=None, up_v_bias=None,
                   block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
                   raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None,
                   workspace=None, prepared_bases=True):
     """Fused latent beacon decode for one layer.
 
-    q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given),
+    q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given;
+    without q_positions, cos/sin are the rows at the query positions, see
+    query_rope_rows),
     raw_k/raw_v [B,Nr,Hkv,D] with RoPE'd K, lat_k [B,Nl,Rk], lat_v [B,Nl,Rv],
     up_k [Hkv*D,Rk], up_v [Hkv*D,Rv].  Returns (out [B,Lq,Hq,D] bf16, lse [B,Hq,Lq]).
     A caller-provided `workspace` (uint8, at least latent_decode_workspace_bytes)

@@ -163,3 +163,35 @@ def test_prepared_bases_are_the_per_head_transpose(device):
     want = torch.stack([w[h, :, h, :].t() for h in range(8)])
     assert torch.equal(bases, want)
     assert kernels.prepare_latent_bases(case.up_k, 8) is bases          # cached per weight version
+
+
+@pytest.mark.parametrize('block_diagonal,prepared', VARIANTS)
+def test_rope_rows_gathered_once_per_step_equal_positions(device, block_diagonal, prepared):
+    """cos/sin rows taken at the query positions once (query_rope_rows) and
+    passed without positions give the same bits as the positions and full
+    tables, for per-sequence positions, two queries per step and a position
+    past the table (clamped by both routes)."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=4, context=1500, tail=70, seed=41, device=device)
+    _, k_rot = _rotated(case)
+    gen = torch.Generator(device=device).manual_seed(42)
+    case.q = torch.randn(4, 2, 32, 128, generator=gen, device=device).to(torch.bfloat16)
+    pos = torch.tensor([[1500, 1501], [9, 10], [70000, 3], [0, 1]], device=device)
+    rows = kernels.query_rope_rows(case.cos, case.sin, pos)
+    common = dict(block_diagonal=block_diagonal, lat_causal=True, prepared_bases=prepared)
+    want = kernels.latent_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                 case.up_v, case.scale, q_positions=pos, cos=case.cos, sin=case.sin, **common)
+    got = kernels.latent_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                case.up_v, case.scale, cos=rows[0], sin=rows[1], **common)
+    torch.cuda.synchronize()
+    assert torch.equal(got[0], want[0])
+    assert torch.equal(got[1], want[1])
+
+
+def test_rope_rows_without_positions_must_cover_every_query(device):
+    from slimkv_amd import kernels
+    case = latent_case(batch=3, context=300, tail=20, seed=43, device=device)
+    _, k_rot = _rotated(case)
+    with pytest.raises(ValueError, match='query positions'):
+        kernels.latent_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                              case.up_v, case.scale, block_diagonal=True, cos=case.cos[:2], sin=case.sin[:2])
