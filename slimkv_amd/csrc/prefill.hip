@@ -74,21 +74,44 @@ struct TileRegs {
     u32x4 v[4];     // 4 keys (4*kq + r) x 8 d (d-piece cp) of V
 };
 
-__device__ __forceinline__ void load_tile(TileRegs& t, const uint16_t* kb, const uint16_t* vb, int64_t k_sn,
-                                          int64_t v_sn, int k0, int n) {
+// Tile loads go through a buffer resource built per tile on the scalar unit:
+// base = the tile's first key row, range = its rows below n.  Each lane's byte
+// offset into the tile is loop-invariant (no per-tile address arithmetic), and
+// rows past n read as zero -- their scores are masked and their P is zero.
+struct TileOffsets {
+    uint32_t k[4], v[4];    // bytes from the tile's first key row
+};
+
+__device__ __forceinline__ TileOffsets tile_offsets(int64_t k_sn, int64_t v_sn) {
+    TileOffsets o;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < 4; ++r) {   // K pieces tid + 256 r -> (row p / 16, d-piece p % 16)
         const int p = tid + 256 * r;
-        const int key = min(k0 + (p >> 4), n - 1);
-        t.k[r] = *reinterpret_cast<const u32x4*>(kb + (int64_t)key * k_sn + 8 * (p & 15));
+        o.k[r] = (uint32_t)(2 * ((p >> 4) * k_sn + 8 * (p & 15)));
     }
     const int kq = tid & 15, cp = tid >> 4;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int key = min(k0 + 4 * kq + r, n - 1);
-        t.v[r] = *reinterpret_cast<const u32x4*>(vb + (int64_t)key * v_sn + 8 * cp);
-    }
+    for (int r = 0; r < 4; ++r) o.v[r] = (uint32_t)(2 * ((4 * kq + r) * v_sn + 8 * cp));   // keys 4kq + r, d-piece cp
+    return o;
+}
+
+constexpr int kBufferWord3 = 0x00020000;   // raw buffer, 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_resource(const uint16_t* base, int64_t sn, int k0, int n) {
+    const int rows = min(n - k0, kKeys);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + (int64_t)k0 * sn), 0, rows * (int)(2 * sn),
+                                             kBufferWord3);
+}
+
+__device__ __forceinline__ void load_tile(TileRegs& t, const uint16_t* kb, const uint16_t* vb, int64_t k_sn,
+                                          int64_t v_sn, int k0, int n, const TileOffsets& o) {
+    const __amdgpu_buffer_rsrc_t rk = tile_resource(kb, k_sn, k0, n);
+    const __amdgpu_buffer_rsrc_t rv = tile_resource(vb, v_sn, k0, n);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) t.k[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, o.k[r], 0, 0));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) t.v[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, o.v[r], 0, 0));
 }
 
 __device__ __forceinline__ void store_tile(const TileRegs& t, uint16_t* ks, uint16_t* vts) {
@@ -160,11 +183,12 @@ prefill_kernel(PrefillParams p) {
 
     const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)kvh * p.k_sh;
     const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
+    const TileOffsets toff = tile_offsets(p.k_sn, p.v_sn);
     TileRegs tr;
     if (ntiles > 0) {
-        load_tile(tr, kb, vb, p.k_sn, p.v_sn, 0, n);
+        load_tile(tr, kb, vb, p.k_sn, p.v_sn, 0, n, toff);
         store_tile(tr, ks_buf[0], vts_buf[0]);
-        if (ntiles > 1) load_tile(tr, kb, vb, p.k_sn, p.v_sn, kKeys, n);
+        if (ntiles > 1) load_tile(tr, kb, vb, p.k_sn, p.v_sn, kKeys, n, toff);
         __syncthreads();
     }
     // the wave's earliest query sees keys up to q0 + shift
@@ -259,7 +283,7 @@ prefill_kernel(PrefillParams p) {
         // and before every wave's reads of tile t + 1
         if (t + 1 < ntiles) {
             store_tile(tr, ks_buf[(t + 1) & 1], vts_buf[(t + 1) & 1]);
-            if (t + 2 < ntiles) load_tile(tr, kb, vb, p.k_sn, p.v_sn, k0 + 2 * kKeys, n);
+            if (t + 2 < ntiles) load_tile(tr, kb, vb, p.k_sn, p.v_sn, k0 + 2 * kKeys, n, toff);
         }
         __syncthreads();
     }
@@ -305,6 +329,10 @@ extern "C" int slimkv_prefill_attention(const slimkv_prefill_attention_args* a, 
     if (!al16(a->q) || !al16(a->k) || !al16(a->v) || !al16(a->out))
         return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
     if (!(a->scale > 0.0)) return fail(SLIMKV_EINVAL, "the softmax scale must be positive");
+    // tile loads hold a tile's byte offsets and range in 32 bits; a key row
+    // holds at least its own head's 128 elements
+    if (a->k_sn < kD || a->v_sn < kD || a->k_sn >= (1 << 23) || a->v_sn >= (1 << 23))
+        return fail(SLIMKV_EUNSUP, "K/V key strides must be in [128, 2^23) elements");
     if (a->batch == 0 || a->queries == 0) return SLIMKV_OK;
     PrefillParams p{};
     p.q = static_cast<const uint16_t*>(a->q); p.q_sb = a->q_sb; p.q_sl = a->q_sl; p.q_sh = a->q_sh;
