@@ -20,7 +20,7 @@
 //   O^T = V^T . P^T P^T comes straight from S^T's accumulator layout with the
 //                   contraction order of the 32 keys of a step permuted to
 //                   (4*grp + j | 16 + 4*grp + j); V^T is read from LDS in the
-//                   same order (two 8-byte reads).  The query stays in the
+//                   same order (one 16-byte read).  The query stays in the
 //                   lane, so softmax statistics never cross lanes except for
 //                   the two-step max/sum over grp.
 //
@@ -64,9 +64,10 @@ __device__ __forceinline__ int vt_pos(int kq) {       // kq: group of 4 keys in 
     return 32 * (kq >> 3) + 8 * (kq & 3) + 4 * ((kq >> 2) & 1);
 }
 
-__device__ __forceinline__ uint32_t half_of(const u32x4& v, int e) {
-    const uint32_t w = v[e >> 1];
-    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+// bf16 element e of a and of b side by side: (a_e | b_e << 16), one byte
+// permute (selector bytes 0-3 pick from a, 4-7 from b).
+__device__ __forceinline__ uint32_t pair_of(const u32x4& a, const u32x4& b, int e) {
+    return __builtin_amdgcn_perm(b[e >> 1], a[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
 }
 
 struct TileRegs {
@@ -125,8 +126,8 @@ __device__ __forceinline__ void store_tile(const TileRegs& t, uint16_t* ks, uint
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         u32x2 w;
-        w.x = half_of(t.v[0], e) | (half_of(t.v[1], e) << 16);
-        w.y = half_of(t.v[2], e) | (half_of(t.v[3], e) << 16);
+        w.x = pair_of(t.v[0], t.v[1], e);
+        w.y = pair_of(t.v[2], t.v[3], e);
         *reinterpret_cast<u32x2*>(vts + (8 * cp + e) * kVStride + vt_pos(kq)) = w;
     }
 }
