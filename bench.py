@@ -59,6 +59,37 @@ def split_kernel_bytes(rk, rv):
     return B * (BEACONS * HKV * (rk + rv) * 2 + RAW * HKV * D * 2 * 2 + HQ * D * 2)
 
 
+REPLAYS = 50
+
+
+def replay_median_ms(torch, step, replays):
+    """Median of `replays` single steps, each bracketed by HIP events."""
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    for a, b in pairs:
+        a.record()
+        step()
+        b.record()
+    torch.cuda.synchronize()
+    times = sorted(a.elapsed_time(b) for a, b in pairs)
+    return times[len(times) // 2]
+
+
+def gpu_clocks():
+    """Current shader and memory clocks as rocm-smi reports them (None if unavailable)."""
+    import re
+    import subprocess
+    try:
+        text = subprocess.run(['rocm-smi', '--showclocks'], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    found = {}
+    for key in ('sclk', 'mclk', 'fclk', 'socclk'):
+        m = re.search(r'\b' + key + r' clock level: \d+: \(([^)]*)\)', text)
+        if m:
+            found[key] = m.group(1)
+    return found or None
+
+
 def draw_ranks(layers, seed):
     import random
     rng = random.Random(seed)
@@ -213,6 +244,7 @@ def main():
     sweep_bytes = sum(layer_bytes(r, r) for r in ranks)
     gbps = sweep_bytes / (elapsed / args.steps) / 1e9
     print(f'bench: sweep {ms_per_step:.3f} ms, {gbps:.1f} GB/s', file=sys.stderr, flush=True)
+    replay_ms = replay_median_ms(torch, step, REPLAYS)
 
     # Split-K kernel alone: the library records HIP events immediately before and
     # after each split launch.  A bounded GPU sleep is queued first so the whole
@@ -260,6 +292,9 @@ def main():
         'tokens_per_s': round(B / (elapsed / args.steps), 1),
         'us_per_layer': round(ms_per_step * 1e3 / len(layers), 2),
         'roofline': roofline,
+        'replays': {'count': REPLAYS, 'median_ms': round(replay_ms, 4),
+                    'median_gbps': round(sweep_bytes / (replay_ms * 1e-3) / 1e9, 1)},
+        'clocks': gpu_clocks(),
     }
     if not args.no_cpu:
         rank32 = next((L for L in layers if L['rank'] == 32), layers[0])

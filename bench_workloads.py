@@ -43,6 +43,12 @@ def _time_steps(torch, step, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
+def _replays(torch, step, count=50):
+    """Median of `count` single steps bracketed by HIP events, and the clocks."""
+    from bench import gpu_clocks, replay_median_ms
+    return {'count': count, 'median_ms': round(replay_median_ms(torch, step, count), 4)}, gpu_clocks()
+
+
 def _result(metric, value, unit, args, seconds, dtype, config, **extra):
     out = {'metric': metric, 'value': round(value, 2), 'unit': unit, 'n_gpus': 1, 'steps': args.steps,
            'warmup': args.warmup, 'ms_per_step': round(seconds * 1e3, 4), 'higher_is_better': True,
@@ -106,6 +112,7 @@ def prefill(args):
             window(w)
 
     seconds = _time_steps(torch, step, args.steps, args.warmup)
+    replays, clocks = _replays(torch, step)
     pairs = [sum(min(keys(w), i + keys(w) - L + 1) for i in range(L)) for w in range(WINDOWS)]
     flops = [p * 4 * D * HQ * B for p in pairs]
     # attention kernel alone, events on the launch stream
@@ -127,7 +134,7 @@ def prefill(args):
                      roofline={'bound': 'mfma', 'achieved': round(achieved, 1), 'peak': MFMA_BF16_PEAK_TFLOPS,
                                'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                                'traffic': None, 'kernel': 'prefill_kernel', 'kernel_ms': round(kernel_s * 1e3, 3)},
-                     attention_tflop=round(sum(flops) / 1e12, 4))
+                     attention_tflop=round(sum(flops) / 1e12, 4), replays=replays, clocks=clocks)
     if not args.no_cpu:
         result['cpu_baseline'] = _prefill_cpu(torch, qs[1], work_k, work_v, keys(1), scale, pairs[1] * 4 * D * HQ * B)
     return result
@@ -186,6 +193,7 @@ def recon(args):
                                  sin=sin, out=L['out'])
 
     seconds = _time_steps(torch, step, args.steps, args.warmup)
+    replays, clocks = _replays(torch, step)
     # The beacon K is rebuilt and rotated tile by tile inside the attention
     # kernel and V is lifted after the weighted sum, so HBM sees the latents
     # once; the reference's materialised K/V (write + read of both) would add
@@ -200,7 +208,8 @@ def recon(args):
                             'batch': B, 'beacons': NB, 'raw_tokens': RAW},
                    hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), us_per_layer=round(seconds / LAYERS * 1e6, 2),
                    bytes_per_layer=per_layer, reconstruction_tflops=round(recon_tflops, 2),
-                   materialising_bytes_per_layer=per_layer + 4 * B * NB * HKV * D * 2)
+                   materialising_bytes_per_layer=per_layer + 4 * B * NB * HKV * D * 2, replays=replays,
+                   clocks=clocks)
 
 
 # ----------------------------------------------------------------------------- paged decode
@@ -278,6 +287,7 @@ def paged(args):
                                     raw_lengths=raw_len, out=out)
 
     seconds = _time_steps(torch, direct_step, args.steps, args.warmup)
+    replays, clocks = _replays(torch, direct_step)
     restore_s = _time_steps(torch, restore_step, args.steps, args.warmup)
     decode_s = _time_steps(torch, decode, args.steps, args.warmup)
     algo = sum(n * 2 * R * 2 + c * HKV * D * 2 * 2 for n, c in zip(nb, raw_count)) + NSEQ * 2 * HQ * D * 2 \
@@ -290,7 +300,7 @@ def paged(args):
                     'beacons_total': sum(nb)},
                    hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), bytes_per_step=algo,
                    restore_path_gbps=round(algo / restore_s / 1e9, 1), restore_path_ms=round(restore_s * 1e3, 4),
-                   dense_decode_only_gbps=round(algo / decode_s / 1e9, 1))
+                   dense_decode_only_gbps=round(algo / decode_s / 1e9, 1), replays=replays, clocks=clocks)
 
 
 def run_workload(args):
