@@ -60,6 +60,7 @@ def split_kernel_bytes(rk, rv):
 
 
 REPLAYS = 50
+PROFILE_REPLAYS = 20
 
 
 def replay_median_ms(torch, step, replays):
@@ -246,27 +247,47 @@ def main():
     print(f'bench: sweep {ms_per_step:.3f} ms, {gbps:.1f} GB/s', file=sys.stderr, flush=True)
     replay_ms = replay_median_ms(torch, step, REPLAYS)
 
-    # Split-K kernel alone: the library records HIP events immediately before and
-    # after each split launch.  A bounded GPU sleep is queued first so the whole
-    # sweep is enqueued before it starts: kernels and events then run back to
-    # back, as in the graph replay, instead of waiting on host launch latency.
+    # Split-K kernel alone.  With the library's split-only switch a decode call
+    # launches just its split kernel (reading the query operands the sweep left
+    # in the workspace; outputs not used).  The layers of one rank -- each with
+    # its own buffers, so the cache holds none of them -- are captured back to
+    # back in one graph and timed with HIP events over PROFILE_REPLAYS replays:
+    # the per-launch average includes the hand-off between launches, as the
+    # kernel trace does, and no per-launch event cost.
     lib = _lib.lib()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in layers]
-    for a, b in events:       # create the HIP events (torch creates them lazily)
-        a.record()
-        b.record()
+    sweep()
     torch.cuda.synchronize()
-    durations = {r: [] for r in set(ranks)}
-    for _ in range(max(3, min(args.steps, 10))):
-        torch.cuda._sleep(200_000_000)   # ~0.1 s of GPU clock cycles
-        rows = kernels.query_rope_rows(cos, sin, step_pos)
-        for L, (a, b) in zip(layers, events):
-            _lib.check(lib.slimkv_set_profile_events(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b.cuda_event)))
-            run_layer(kernels, L, rows, scale, workspace)
-        _lib.check(lib.slimkv_set_profile_events(None, None))
+    durations = {}
+    rows = kernels.query_rope_rows(cos, sin, step_pos)     # unused by split-only calls
+    for r in sorted(set(ranks)):
+        group = [L for L in layers if L['rank'] == r]
+
+        def split_sweep():
+            for L in group:
+                run_layer(kernels, L, rows, scale, workspace)
+        _lib.check(lib.slimkv_set_profile_split_only(1))
+        try:
+            split_sweep()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                split_sweep()
+            torch.cuda.current_stream().wait_stream(side)
+            split_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(split_graph):
+                split_sweep()
+        finally:
+            _lib.check(lib.slimkv_set_profile_split_only(0))
+        for _ in range(3):
+            split_graph.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        for L, (a, b) in zip(layers, events):
-            durations[L['rank']].append(a.elapsed_time(b) * 1e-3)
+        a.record()
+        for _ in range(PROFILE_REPLAYS):
+            split_graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        durations[r] = [a.elapsed_time(b) * 1e-3 / (PROFILE_REPLAYS * len(group))]
     dom = 32 if 32 in durations else max(durations, key=lambda r: len(durations[r]))
     dur = durations[dom]
     dur_avg = sum(dur) / len(dur)

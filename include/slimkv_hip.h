@@ -40,6 +40,14 @@ int slimkv_abi_version(void);
  * HIP events.  Pass NULL, NULL to clear. */
 int slimkv_set_profile_events(void* before, void* after);
 
+/* Measurement hook (no counterpart in the reference): while on (nonzero) on
+ * the calling thread, slimkv_latent_decode and slimkv_paged_latent_decode
+ * launch only their split-K attention kernel, reading the query operands an
+ * earlier call left in the same workspace, and skip the query prologue and
+ * the combine: their outputs are then not valid.  For timing that kernel
+ * alone over many layers back to back.  Pass 0 to restore normal calls. */
+int slimkv_set_profile_split_only(int on);
+
 /* ------------------------------------------------------------------------
  * Split-K decode attention with GQA, bottom-right causality and LSE.
  *

@@ -167,6 +167,7 @@ SIGNATURES = {
     'slimkv_last_error': (ctypes.c_char_p, []),
     'slimkv_abi_version': (ctypes.c_int, []),
     'slimkv_set_profile_events': (ctypes.c_int, [c_ptr, c_ptr]),
+    'slimkv_set_profile_split_only': (ctypes.c_int, [ctypes.c_int]),
     'slimkv_attention_workspace': (ctypes.c_size_t, [ctypes.POINTER(AttentionArgs)]),
     'slimkv_attention_forward': (ctypes.c_int, [ctypes.POINTER(AttentionArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(LatentDecodeArgs)]),

@@ -1317,6 +1317,7 @@ namespace {
 
 thread_local std::string g_error;
 thread_local hipEvent_t g_before = nullptr;
+thread_local int g_split_only = 0;          // latent decode: launch only the split kernel
 thread_local hipEvent_t g_after = nullptr;
 
 // Launch the split kernel bracketed by the caller's profiling events, if set.
@@ -1516,6 +1517,11 @@ extern "C" int slimkv_set_profile_events(void* before, void* after) {
     if ((before == nullptr) != (after == nullptr)) return fail(SLIMKV_EINVAL, "set both events or neither");
     g_before = static_cast<hipEvent_t>(before);
     g_after = static_cast<hipEvent_t>(after);
+    return SLIMKV_OK;
+}
+
+extern "C" int slimkv_set_profile_split_only(int on) {
+    g_split_only = on ? 1 : 0;
     return SLIMKV_OK;
 }
 
@@ -1756,7 +1762,9 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     const bool mfma_prologue = has_lat && bd && pp.ut && pp.wq % 16 == 0 && nct >= 1 && nct <= 3 &&
                                g * Lq <= 16 && ptr_aligned16(pp.ut) && ptr_aligned16(a->q) &&
                                (!a->up_k_bias || ptr_aligned16(a->up_k_bias));
-    if (mfma_prologue) {
+    if (g_split_only) {
+        // measurement: the query operands an earlier call left in the workspace
+    } else if (mfma_prologue) {
         if (nct == 1) hipLaunchKernelGGL(prologue_mfma_kernel<1>, dim3(B * Hkv), dim3(64), 0, st, pp);
         else if (nct == 2) hipLaunchKernelGGL(prologue_mfma_kernel<2>, dim3(B * Hkv), dim3(64), 0, st, pp);
         else hipLaunchKernelGGL(prologue_mfma_kernel<3>, dim3(B * Hkv), dim3(64), 0, st, pp);
@@ -1818,6 +1826,7 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
     rc = check_hip(timed_split(ka, kb, prm, grid, st, paged), "split kernel launch");
     if (rc != SLIMKV_OK) return rc;
+    if (g_split_only) return SLIMKV_OK;
 
     CombineParams cp{};
     cp.a_ml = r.part_ml; cp.a_acc = r.part_acc; cp.a_splits = r.splits; cp.a_w = D;

@@ -195,3 +195,28 @@ def test_rope_rows_without_positions_must_cover_every_query(device):
     with pytest.raises(ValueError, match='query positions'):
         kernels.latent_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
                               case.up_v, case.scale, block_diagonal=True, cos=case.cos[:2], sin=case.sin[:2])
+
+
+def test_split_only_measurement_switch(device):
+    """slimkv_set_profile_split_only: while on, a decode call launches only its
+    split kernel and leaves the output untouched; once off, calls are normal
+    again (bit-identical to a call made before)."""
+    from slimkv_amd import _lib, kernels
+    case = latent_case(batch=2, context=900, tail=40, seed=51, device=device)
+    _, k_rot = _rotated(case)
+    nbytes = kernels.latent_decode_workspace_bytes(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v,
+                                                   case.up_k, case.up_v, case.scale, block_diagonal=True,
+                                                   q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    want = _run(case, k_rot, True, workspace=ws)
+    out = torch.full_like(want[0], 7.0)
+    lib = _lib.lib()
+    _lib.check(lib.slimkv_set_profile_split_only(1))
+    try:
+        _run(case, k_rot, True, workspace=ws, out=out)
+    finally:
+        _lib.check(lib.slimkv_set_profile_split_only(0))
+    assert (out == 7.0).all()
+    got = _run(case, k_rot, True, workspace=ws)
+    assert torch.equal(got[0], want[0])
+    assert torch.equal(got[1], want[1])
