@@ -179,9 +179,10 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-graph', action='store_true', help='time eager launches instead of graph replay')
-    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged'),
+    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged', 'b1'),
                     help='latent: the headline decode sweep; prefill / recon / paged: the window prefill, '
-                         'reconstruction decode and paged-cache decode workloads')
+                         'reconstruction decode and paged-cache decode workloads; b1: batch-1 ms per token '
+                         'at the contexts the reference publishes')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: the decode path shards by sequence with no exchange, '

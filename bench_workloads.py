@@ -303,5 +303,79 @@ def paged(args):
                    dense_decode_only_gbps=round(algo / decode_s / 1e9, 1), replays=replays, clocks=clocks)
 
 
+# ----------------------------------------------------------------------------- batch 1
+
+# The reference's published attention GPU kernel time per token, 32 layers,
+# batch 1, SlimKV t4f4 latent decode on H20 (README.md:276-280), by context.
+REFERENCE_B1_MS = {32768: 4.81, 65536: 6.52, 98304: 8.10, 131072: 9.69, 262144: 16.03}
+
+
+def b1(args):
+    """Batch-1 latent decode attention, 32 layers per token, at the contexts the
+    reference publishes: ms per token (graph replay of the 32 layers' fused
+    decode, own buffers per layer, RoPE rows gathered once per token)."""
+    import torch
+    import bench
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
+    HQ, HKV, D, SINKS, TAIL, LAYERS = 32, 8, 128, 4, 128, 32
+    dev = torch.device('cuda:0')
+    ranks = bench.draw_ranks(LAYERS, args.seed)
+    scale = D ** -0.5
+    per_context = {}
+    for ctx in sorted(REFERENCE_B1_MS):
+        nb, raw = ctx // 4, SINKS + TAIL + 1
+        cos, sin = rope_tables(ctx + 1, D, 500000.0, dev)
+        layers = []
+        for i, r in enumerate(ranks):
+            gen = torch.Generator(device=dev).manual_seed(args.seed * 1000 + i)
+            cpu = torch.Generator().manual_seed(args.seed * 1000 + i + 1)
+            rnd = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(torch.bfloat16)
+            layers.append(dict(
+                q=rnd(1, 1, HQ, D), raw_k=rnd(1, raw, HKV, D), raw_v=rnd(1, raw, HKV, D),
+                lat_k=rnd(1, nb, HKV * r), lat_v=rnd(1, nb, HKV * r),
+                up_k=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+                up_v=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+                out=torch.empty(1, 1, HQ, D, dtype=torch.bfloat16, device=dev),
+                lse=torch.empty(1, HQ, 1, dtype=torch.float32, device=dev)))
+        pos = torch.full((1, 1), ctx, dtype=torch.int64, device=dev)
+        ws = torch.empty(max(kernels.latent_decode_workspace_bytes(
+            L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'], block_diagonal=True,
+            q_positions=pos, cos=cos, sin=sin) for L in layers), dtype=torch.uint8, device=dev)
+
+        def token():
+            rows = kernels.query_rope_rows(cos, sin, pos)
+            for L in layers:
+                kernels.latent_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'],
+                                      scale, block_diagonal=True, cos=rows[0], sin=rows[1], out=L['out'],
+                                      lse=L['lse'], workspace=ws)
+        token()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            token()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            token()
+        seconds = _time_steps(torch, graph.replay, args.steps, args.warmup)
+        replays, clocks = _replays(torch, graph.replay)
+        ms = seconds * 1e3
+        per_context[ctx] = {'ms_per_token': round(ms, 4), 'median_ms': replays['median_ms'],
+                            'reference_h20_ms': REFERENCE_B1_MS[ctx],
+                            'reference_over_ours': round(REFERENCE_B1_MS[ctx] / ms, 2)}
+        del layers, ws, graph
+        torch.cuda.empty_cache()
+    first = per_context[32768]
+    return _result('latent decode attention ms/token, 32 layers, B1, t4f4', first['ms_per_token'], 'ms', args,
+                   first['ms_per_token'] * 1e-3, 'bf16',
+                   {'workload': 'batch-1 latent beacon decode, 32 layers per token, Llama-3.1-8B layer shape, '
+                                'per-layer rank drawn from {16, 32, 48}', 'contexts': sorted(REFERENCE_B1_MS),
+                    'layer_ranks': ranks},
+                   higher_is_better=False, per_context={str(k): v for k, v in per_context.items()},
+                   reference_source='README.md:276-280 (H20, attention GPU kernel time per token)',
+                   clocks=clocks)
+
+
 def run_workload(args):
-    return {'prefill': prefill, 'recon': recon, 'paged': paged}[args.workload](args)
+    return {'prefill': prefill, 'recon': recon, 'paged': paged, 'b1': b1}[args.workload](args)

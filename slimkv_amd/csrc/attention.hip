@@ -840,6 +840,33 @@ constexpr int kMaxSplits = 256;
 constexpr int kMaxLatW = 1024;
 constexpr int kCombineThreads = 128;
 
+// Reductions over a block of T threads (T / 64 wavefronts); red holds T / 64 floats.
+template <int T>
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor_f(v, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+#pragma unroll
+    for (int w = 1; w < T / 64; ++w) v = fmaxf(v, red[w]);
+    __syncthreads();
+    return v;
+}
+
+template <int T>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_f(v, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+#pragma unroll
+    for (int w = 1; w < T / 64; ++w) v += red[w];
+    __syncthreads();
+    return v;
+}
+
 __device__ __forceinline__ float block_max128(float v, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor_f(v, o));
@@ -974,12 +1001,15 @@ constexpr int kFastRawSplits = 32;
 constexpr int kFastLatW = 64;
 constexpr int kFastLatPer = 32;     // latent partial values per thread
 
-__global__ void __launch_bounds__(kCombineThreads)
+// T = 128 or 256 threads: one split's (m, l) per thread, so a_splits +
+// b_splits <= T, and the latent partials in T / b_w groups of kFastLatPer.
+template <int T>
+__global__ void __launch_bounds__(T)
 combine_fast_kernel(CombineParams cp) {
     __shared__ float wts[2 * kMaxSplits];
-    __shared__ float part[kCombineThreads];
+    __shared__ float part[T];
     __shared__ float accb[kFastLatW];
-    __shared__ float red[2];
+    __shared__ float red[T / 64];
     const int t = threadIdx.x;
     const int HL = cp.Hq * cp.Lq;
     const int pr = blockIdx.x % HL;
@@ -1010,7 +1040,7 @@ combine_fast_kernel(CombineParams cp) {
     // latent: thread handles column k = t % b_w of splits s = t / b_w + i * (128 / b_w)
     float lb[kFastLatPer];
     const int kcol = cp.b_w ? t % cp.b_w : 0;
-    const int sstep = cp.b_w ? kCombineThreads / cp.b_w : 1;
+    const int sstep = cp.b_w ? T / cp.b_w : 1;
     const int s0 = cp.b_w ? t / cp.b_w : 0;
     const float* bacc = cp.b_splits ? cp.b_acc + row * cp.b_splits * cp.b_w : nullptr;
 #pragma unroll
@@ -1031,13 +1061,13 @@ combine_fast_kernel(CombineParams cp) {
 
     // -- split weights --
     if (t >= cp.a_splits && t < total && mv != kNegInf) mv += shift;
-    const float M = block_max128(mv, red);
+    const float M = block_max<T>(mv, red);
     const float Mref = M == kNegInf ? 0.f : M;
     const float wgt = (t < total && mv != kNegInf) ? fast_exp2(mv - Mref) : 0.f;
     if (t < total) wts[t] = wgt;
-    const float LA = block_sum128(t < cp.a_splits ? lv * wgt : 0.f, red);
-    const float LB = block_sum128(t >= cp.a_splits && t < total ? lv * wgt : 0.f, red);
-    const float L = LA + LB;    // block_sum128 synchronised, so wts[] is visible
+    const float LA = block_sum<T>(t < cp.a_splits ? lv * wgt : 0.f, red);
+    const float LB = block_sum<T>(t >= cp.a_splits && t < total ? lv * wgt : 0.f, red);
+    const float L = LA + LB;    // block_sum synchronised, so wts[] is visible
 
     // -- latent accumulator --
     if (cp.b_splits) {
@@ -1083,18 +1113,20 @@ combine_fast_kernel(CombineParams cp) {
         cp.lse[((int64_t)b * cp.Hq + j) * cp.Lq + lq] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
 }
 
-bool combine_fast_ok(const CombineParams& cp) {
+// Whether the fast combine with T threads takes these partials.  Latent widths
+// that do not divide the block (48) leave the threads past (T / b_w) * b_w
+// idle in the weighted sum.
+bool combine_fast_ok(const CombineParams& cp, int T) {
     if (cp.b_splits && !cp.up_v) return false;
-    // Latent widths that do not divide the block (48) leave the threads past
-    // (128 / b_w) * b_w idle in the weighted sum.
-    return cp.D <= kCombineThreads && cp.a_splits <= kFastRawSplits && cp.a_splits + cp.b_splits <= kCombineThreads &&
-           cp.b_w <= kFastLatW && (cp.b_splits == 0 ||
-           (cp.b_w % 8 == 0 && cp.b_splits <= kFastLatPer * (kCombineThreads / cp.b_w)));
+    return cp.D <= T && cp.a_splits <= kFastRawSplits && cp.a_splits + cp.b_splits <= T && cp.b_w <= kFastLatW &&
+           (cp.b_splits == 0 || (cp.b_w % 8 == 0 && cp.b_splits <= kFastLatPer * (T / cp.b_w)));
 }
 
 void launch_combine(const CombineParams& cp, int rows, hipStream_t st) {
-    if (combine_fast_ok(cp))
-        hipLaunchKernelGGL(combine_fast_kernel, dim3(rows), dim3(kCombineThreads), 0, st, cp);
+    if (combine_fast_ok(cp, 128))
+        hipLaunchKernelGGL(combine_fast_kernel<128>, dim3(rows), dim3(128), 0, st, cp);
+    else if (combine_fast_ok(cp, 256))
+        hipLaunchKernelGGL(combine_fast_kernel<256>, dim3(rows), dim3(256), 0, st, cp);
     else
         hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(kCombineThreads), 0, st, cp);
 }
@@ -1677,14 +1709,24 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     // resident slots so every workgroup starts in the first wave of residency.
     const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
     const int raw_wg = (int)B * ((int)(Hkv + kWaves - 1) / kWaves) * raw_req0;
-    const int lat_target = std::max(slots - raw_wg, slots / 2);
+    int lat_target = std::max(slots - raw_wg, slots / 2);
+    // Keep the latent split count within the fast combine's reach (one latent
+    // partial register pass, and one split per combine thread with the raw
+    // ones): at small batches the slots would otherwise fill with ever shorter
+    // splits whose partials the generic combine reads serially.
+    const int wown = bd ? rv : (int)Rv;
+    int fast_cap = kMaxSplits;
+    if (wown % 8 == 0 && wown <= kFastLatW)
+        fast_cap = std::max(1, std::min(kFastLatPer * (256 / wown), 256 - raw_req0));
+    const int lat_groups = (int)B * ((((P + cols - 1) / cols) + kWaves - 1) / kWaves);
+    if (a->lat_splits <= 0) lat_target = std::min<int64_t>(lat_target, (int64_t)lat_groups * fast_cap);
     p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, lat_target);
     if (pg && a->lat_splits <= 0) {
         // Compact schedule: size the splits from the total row count so the
         // non-empty splits of all sequences fill the resident slots once.
         const int64_t total = pg->rows_total > 0 ? pg->rows_total : B * nl;
         int64_t rps = (total + lat_target - 1) / lat_target;
-        rps = std::max<int64_t>(rps, (nl + kMaxSplits - 1) / kMaxSplits);
+        rps = std::max<int64_t>(rps, (nl + std::min(kMaxSplits, fast_cap) - 1) / std::min(kMaxSplits, fast_cap));
         rps = std::max<int64_t>(16, (rps + 15) / 16 * 16);
         const int groups = p->lat.nwg / p->lat.splits;
         p->lat.rows_per_split = (int)rps;

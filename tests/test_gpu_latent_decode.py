@@ -220,3 +220,17 @@ def test_split_only_measurement_switch(device):
     got = _run(case, k_rot, True, workspace=ws)
     assert torch.equal(got[0], want[0])
     assert torch.equal(got[1], want[1])
+
+
+@pytest.mark.parametrize('rank', [32, 48])
+def test_batch1_long_context_many_splits(device, rank):
+    """Batch 1 at 8192 beacons: the planner fills the GPU with over 128 latent
+    splits, which the 256-thread fast combine merges (the reference's B1
+    decode shape, fa2_decode.py:143-164)."""
+    case = latent_case(batch=1, context=8192 * 4 + 132, tail=128, rank_k=rank, rank_v=rank, seed=61 + rank,
+                       device=device)
+    q_rot, k_rot = _rotated(case)
+    out, lse = _run(case, k_rot, True)
+    eo, el = _oracle(case, q_rot, k_rot)
+    assert_close(to_np(out.transpose(1, 2)), eo)
+    assert_lse_close(to_np(lse), el)
