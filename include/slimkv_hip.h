@@ -310,7 +310,9 @@ int slimkv_merge(const slimkv_merge_args* a, void* stream);
  * q [B, Lq, Hq, 128]  k, v [B, Nk, Hk, 128]  out [B, Lq, Hq, 128] (BSHD);
  * lse [B, Hq, Lq] fp32 contiguous (may be NULL).  With `causal` query i sees
  * keys [0, n_b - Lq + i] where n_b = seqlens_k ? seqlens_k[b] : keys; a row
- * that sees no key gets output 0 and LSE -inf.
+ * that sees no key gets output 0 and LSE -inf.  Strides are multiples of 8
+ * elements, tensors 16-byte aligned, k_sn and v_sn in [128, 2^23) (SLIMKV_EUNSUP
+ * otherwise), scale > 0.
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_prefill_attention_args {
     const void* q; int64_t q_sb, q_sl, q_sh;
