@@ -222,15 +222,22 @@ def test_split_only_measurement_switch(device):
     assert torch.equal(got[1], want[1])
 
 
-@pytest.mark.parametrize('rank', [32, 48])
-def test_batch1_long_context_many_splits(device, rank):
+@pytest.mark.parametrize('rank,queries', [(32, 1), (48, 1), (32, 2)])
+def test_batch1_long_context_many_splits(device, rank, queries):
     """Batch 1 at 8192 beacons: the planner fills the GPU with over 128 latent
     splits, which the 256-thread fast combine merges (the reference's B1
-    decode shape, fa2_decode.py:143-164)."""
+    decode shape, fa2_decode.py:143-164), also for the two-query insertion
+    step with its causal latent branch."""
     case = latent_case(batch=1, context=8192 * 4 + 132, tail=128, rank_k=rank, rank_v=rank, seed=61 + rank,
                        device=device)
+    if queries == 2:
+        gen = torch.Generator(device=device).manual_seed(62)
+        case.q = torch.randn(1, 2, 32, 128, generator=gen, device=device).to(torch.bfloat16)
+        ctx = 8192 * 4 + 132
+        case.q_positions = torch.tensor([[ctx, ctx + 1]], device=device)
+        case.cos, case.sin = rope_tables(ctx + 2, 128, 500000.0, device)
     q_rot, k_rot = _rotated(case)
-    out, lse = _run(case, k_rot, True)
-    eo, el = _oracle(case, q_rot, k_rot)
+    out, lse = _run(case, k_rot, True, lat_causal=queries == 2)
+    eo, el = _oracle(case, q_rot, k_rot, lat_causal=queries == 2)
     assert_close(to_np(out.transpose(1, 2)), eo)
     assert_lse_close(to_np(lse), el)
