@@ -308,6 +308,8 @@ def paged(args):
 # The reference's published attention GPU kernel time per token, 32 layers,
 # batch 1, SlimKV t4f4 latent decode on H20 (README.md:276-280), by context.
 REFERENCE_B1_MS = {32768: 4.81, 65536: 6.52, 98304: 8.10, 131072: 9.69, 262144: 16.03}
+# ... and of its reconstruction decode (README.md:276-280, "Recon t4f4").
+REFERENCE_B1_RECON_MS = {32768: 10.40, 65536: 17.30, 98304: 24.14, 131072: 31.27, 262144: 57.99}
 
 
 def b1(args):
@@ -365,6 +367,43 @@ def b1(args):
                             'reference_h20_ms': REFERENCE_B1_MS[ctx],
                             'reference_over_ours': round(REFERENCE_B1_MS[ctx] / ms, 2)}
         del layers, ws, graph
+        torch.cuda.empty_cache()
+
+        # Reconstruction decode of the same token: beacon K rebuilt and rotated
+        # at the beacon slot positions inside the attention kernel, rank 32 in
+        # every layer (the fused route's V ranks are 32 and 64).
+        rec_layers = []
+        for i in range(LAYERS):
+            gen = torch.Generator(device=dev).manual_seed(args.seed * 1000 + 500 + i)
+            cpu = torch.Generator().manual_seed(args.seed * 1000 + 501 + i)
+            rnd = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(torch.bfloat16)
+            rec_layers.append(dict(
+                q=rnd(1, 1, HQ, D), raw_k=rnd(1, raw, HKV, D), raw_v=rnd(1, raw, HKV, D),
+                lat_k=rnd(1, nb, HKV * 32), lat_v=rnd(1, nb, HKV * 32),
+                up_k=block_diagonal([orthonormal_columns(D, 32, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+                up_v=block_diagonal([orthonormal_columns(D, 32, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+                out=torch.empty(1, 1, HQ, D, dtype=torch.bfloat16, device=dev)))
+        bpos = (SINKS + torch.arange(nb, device=dev))[None].contiguous()
+
+        def rec_token():
+            for L in rec_layers:
+                kernels.recon_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'],
+                                     scale, beacon_positions=bpos, block_diagonal=True, q_positions=pos, cos=cos,
+                                     sin=sin, out=L['out'])
+        rec_token()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            rec_token()
+        torch.cuda.current_stream().wait_stream(side)
+        rec_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(rec_graph):
+            rec_token()
+        rec_ms = _time_steps(torch, rec_graph.replay, args.steps, args.warmup) * 1e3
+        per_context[ctx].update(recon_ms_per_token=round(rec_ms, 4),
+                                reference_h20_recon_ms=REFERENCE_B1_RECON_MS[ctx],
+                                recon_reference_over_ours=round(REFERENCE_B1_RECON_MS[ctx] / rec_ms, 2))
+        del rec_layers, rec_graph
         torch.cuda.empty_cache()
     first = per_context[32768]
     return _result('latent decode attention ms/token, 32 layers, B1, t4f4', first['ms_per_token'], 'ms', args,

@@ -1991,8 +1991,12 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
         p->vl = (int)(a->rank_v / Hkv / 32);
         // The beacon splits are arithmetic-bound (rebuild + RoPE per tile), so
         // they take every resident slot; the short raw workgroups run ahead of them.
-        const int slots = cu * recon_occupancy(p->ksr, p->vl);
-        p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, 32 * p->vl, a->lat_splits, slots);
+        int slots = cu * recon_occupancy(p->ksr, p->vl);
+        // as for the latent decode: stay within the fast combine's split count
+        const int wv = 32 * p->vl;
+        const int fast_cap = std::max(1, std::min(kFastLatPer * (256 / wv), 256 - raw_req));
+        if (a->lat_splits <= 0) slots = std::min<int64_t>(slots, (int64_t)B * ((Hkv + kWaves - 1) / kWaves) * fast_cap);
+        p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, wv, a->lat_splits, slots);
     } else {
         p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, (int)D, a->lat_splits,
                               cu * split_occupancy(8, 8));
