@@ -411,7 +411,8 @@ def b1(args):
                    {'workload': 'batch-1 latent beacon decode, 32 layers per token, Llama-3.1-8B layer shape, '
                                 'per-layer rank drawn from {16, 32, 48}', 'contexts': sorted(REFERENCE_B1_MS),
                     'layer_ranks': ranks},
-                   higher_is_better=False, per_context={str(k): v for k, v in per_context.items()},
+                   higher_is_better=False, vs_baseline=round(first['ms_per_token'] / REFERENCE_B1_MS[32768], 4),
+                   per_context={str(k): v for k, v in per_context.items()},
                    reference_source='README.md:276-280 (H20, attention GPU kernel time per token)',
                    clocks=clocks)
 
