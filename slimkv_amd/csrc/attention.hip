@@ -101,11 +101,28 @@ __device__ __forceinline__ u32x4 zero_unless(bool ok, u32x4 v) {
     return u32x4{ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
 }
 
+// The RoPE table values one lane needs for a head_dim-128 query row held as
+// MFMA operand pieces (elements 32c + 8*grp + [0, 8), c = 0..3).
+struct RopeRow {
+    float4 c[4][2], s[4][2];
+};
+
+__device__ __forceinline__ void load_rope_row(RopeRow& t, const float* cs, const float* sn, int grp) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d0 = 32 * c + 8 * grp;
+        t.c[c][0] = *reinterpret_cast<const float4*>(cs + d0);
+        t.c[c][1] = *reinterpret_cast<const float4*>(cs + d0 + 4);
+        t.s[c][0] = *reinterpret_cast<const float4*>(sn + d0);
+        t.s[c][1] = *reinterpret_cast<const float4*>(sn + d0 + 4);
+    }
+}
+
 // Rotate one head_dim-128 query row held as MFMA operand pieces: x[c] holds
 // elements 32c + 8*grp + [0, 8); the rotate-half partner of piece c is c ^ 2.
 // out = bf16(bf16(x * bf16(cos)) + bf16(rotate_half(x) * bf16(sin))), the
 // reference's bf16 operation order (decode_kernels.py:7-51).
-__device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const float* cs, const float* sn, int grp) {
+__device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const RopeRow& t) {
     float v[4][8];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -116,9 +133,7 @@ __device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const float* cs, con
         }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        const int d0 = 32 * c + 8 * grp;
-        const float4 c0 = *reinterpret_cast<const float4*>(cs + d0), c1 = *reinterpret_cast<const float4*>(cs + d0 + 4);
-        const float4 s0 = *reinterpret_cast<const float4*>(sn + d0), s1 = *reinterpret_cast<const float4*>(sn + d0 + 4);
+        const float4 c0 = t.c[c][0], c1 = t.c[c][1], s0 = t.s[c][0], s1 = t.s[c][1];
         const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
         uint32_t w[4];
@@ -840,33 +855,6 @@ constexpr int kMaxSplits = 256;
 constexpr int kMaxLatW = 1024;
 constexpr int kCombineThreads = 128;
 
-// Reductions over a block of T threads (T / 64 wavefronts); red holds T / 64 floats.
-template <int T>
-__device__ __forceinline__ float block_max(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor_f(v, o));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    v = red[0];
-#pragma unroll
-    for (int w = 1; w < T / 64; ++w) v = fmaxf(v, red[w]);
-    __syncthreads();
-    return v;
-}
-
-template <int T>
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += shfl_xor_f(v, o);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    v = red[0];
-#pragma unroll
-    for (int w = 1; w < T / 64; ++w) v += red[w];
-    __syncthreads();
-    return v;
-}
-
 __device__ __forceinline__ float block_max128(float v, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, shfl_xor_f(v, o));
@@ -999,17 +987,22 @@ combine_kernel(CombineParams cp) {
 // reduction, so the whole combine costs one memory round trip.
 constexpr int kFastRawSplits = 32;
 constexpr int kFastLatW = 64;
-constexpr int kFastLatPer = 32;     // latent partial values per thread
+constexpr int kFastLatPer = 8;      // 16-byte latent partial loads (4 columns) per thread
+
+// Latent splits the fast combine with T threads takes at latent width b_w (a
+// multiple of 8): each thread loads kFastLatPer quads of one column group.
+constexpr int fast_lat_splits(int b_w, int T) { return kFastLatPer * (T / (b_w / 4)); }
 
 // T = 128 or 256 threads: one split's (m, l) per thread, so a_splits +
-// b_splits <= T, and the latent partials in T / b_w groups of kFastLatPer.
+// b_splits <= T, and the latent partials as 4-column quads: thread t takes
+// quad t % (b_w / 4) of splits t / (b_w / 4) + i * (T / (b_w / 4)).
 template <int T>
 __global__ void __launch_bounds__(T)
 combine_fast_kernel(CombineParams cp) {
     __shared__ float wts[2 * kMaxSplits];
-    __shared__ float part[T];
+    __shared__ float4 part[T];
     __shared__ float accb[kFastLatW];
-    __shared__ float red[T / 64];
+    __shared__ float red[3 * (T / 64)];      // per-wave maximum, then the two sums
     const int t = threadIdx.x;
     const int HL = cp.Hq * cp.Lq;
     const int pr = blockIdx.x % HL;
@@ -1037,16 +1030,17 @@ combine_fast_kernel(CombineParams cp) {
     const float* aacc = cp.a_acc + row * cp.a_splits * cp.a_w;
 #pragma unroll
     for (int s = 0; s < kFastRawSplits; ++s) ra[s] = (has_dd && s < cp.a_splits) ? aacc[(int64_t)s * cp.a_w + dd] : 0.f;
-    // latent: thread handles column k = t % b_w of splits s = t / b_w + i * (128 / b_w)
-    float lb[kFastLatPer];
-    const int kcol = cp.b_w ? t % cp.b_w : 0;
-    const int sstep = cp.b_w ? T / cp.b_w : 1;
-    const int s0 = cp.b_w ? t / cp.b_w : 0;
+    float4 lb[kFastLatPer];
+    const int quads = cp.b_w / 4;
+    const int kq = quads ? t % quads : 0;
+    const int sstep = quads ? T / quads : 1;
+    const int s0 = quads ? t / quads : 0;
     const float* bacc = cp.b_splits ? cp.b_acc + row * cp.b_splits * cp.b_w : nullptr;
 #pragma unroll
     for (int i = 0; i < kFastLatPer; ++i) {
         const int s = s0 + i * sstep;
-        lb[i] = (bacc && s < bsp && s0 < sstep) ? bacc[(int64_t)s * cp.b_w + kcol] : 0.f;
+        lb[i] = (bacc && s < bsp && s0 < sstep) ? *reinterpret_cast<const float4*>(bacc + (int64_t)s * cp.b_w + 4 * kq)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     u32x4 wv[kFastLatW / 8];
     const uint16_t* wr = nullptr;
@@ -1061,27 +1055,59 @@ combine_fast_kernel(CombineParams cp) {
 
     // -- split weights --
     if (t >= cp.a_splits && t < total && mv != kNegInf) mv += shift;
-    const float M = block_max<T>(mv, red);
+    // One barrier for the maximum, one for both sums (each reduction has its own
+    // slots in red[], so no barrier guards their reuse).
+    constexpr int NW = T / 64;
+    const int wave = t >> 6;
+    float M = mv;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, shfl_xor_f(M, o));
+    if ((t & 63) == 0) red[wave] = M;
+    __syncthreads();
+    M = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, red[w]);
     const float Mref = M == kNegInf ? 0.f : M;
     const float wgt = (t < total && mv != kNegInf) ? fast_exp2(mv - Mref) : 0.f;
     if (t < total) wts[t] = wgt;
-    const float LA = block_sum<T>(t < cp.a_splits ? lv * wgt : 0.f, red);
-    const float LB = block_sum<T>(t >= cp.a_splits && t < total ? lv * wgt : 0.f, red);
-    const float L = LA + LB;    // block_sum synchronised, so wts[] is visible
+    float LA = t < cp.a_splits ? lv * wgt : 0.f;
+    float LB = t >= cp.a_splits && t < total ? lv * wgt : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        LA += shfl_xor_f(LA, o);
+        LB += shfl_xor_f(LB, o);
+    }
+    if ((t & 63) == 0) {
+        red[NW + 2 * wave] = LA;
+        red[NW + 2 * wave + 1] = LB;
+    }
+    __syncthreads();            // also makes wts[] visible
+    LA = red[NW];
+    LB = red[NW + 1];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        LA += red[NW + 2 * w];
+        LB += red[NW + 2 * w + 1];
+    }
+    const float L = LA + LB;
 
     // -- latent accumulator --
     if (cp.b_splits) {
-        float sum = 0.f;
+        float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int i = 0; i < kFastLatPer; ++i) {
             const int s = s0 + i * sstep;
-            if (s < bsp && s0 < sstep) sum += lb[i] * wts[cp.a_splits + s];
+            if (s < bsp && s0 < sstep) {
+                const float w = wts[cp.a_splits + s];
+                sum.x += lb[i].x * w; sum.y += lb[i].y * w; sum.z += lb[i].z * w; sum.w += lb[i].w * w;
+            }
         }
         part[t] = sum;
         __syncthreads();
         if (t < cp.b_w) {
+            const float* pf = reinterpret_cast<const float*>(part);
             float acc = 0.f;
-            for (int g2 = 0; g2 < sstep; ++g2) acc += part[g2 * cp.b_w + t];
+            for (int g2 = 0; g2 < sstep; ++g2) acc += pf[4 * (g2 * quads + t / 4) + t % 4];
             accb[t] = acc;
         }
         __syncthreads();
@@ -1119,7 +1145,7 @@ combine_fast_kernel(CombineParams cp) {
 bool combine_fast_ok(const CombineParams& cp, int T) {
     if (cp.b_splits && !cp.up_v) return false;
     return cp.D <= T && cp.a_splits <= kFastRawSplits && cp.a_splits + cp.b_splits <= T && cp.b_w <= kFastLatW &&
-           (cp.b_splits == 0 || (cp.b_w % 8 == 0 && cp.b_splits <= kFastLatPer * (T / cp.b_w)));
+           (cp.b_splits == 0 || (cp.b_w % 8 == 0 && cp.b_splits <= fast_lat_splits(cp.b_w, T)));
 }
 
 void launch_combine(const CombineParams& cp, int rows, hipStream_t st) {
@@ -1277,8 +1303,8 @@ prologue_kernel(PrologueParams pp) {
 // g*Lq query rows of the head are the MFMA columns (lane col), rotated in
 // registers, and q_lat^T[c][p] = U_K^T[c][:] . q_rot[p][:] comes from NCT
 // 16-row tiles of the prepared per-head U_K^T.  Every load is issued before any
-// result is needed: one memory round trip for q, U_K^T and the position, one
-// more for the RoPE table rows.
+// result is needed: q, U_K^T and the RoPE table rows in one memory round trip
+// (given positions, the rows follow the position load they depend on).
 template <int NCT>
 __global__ void __launch_bounds__(64)
 prologue_mfma_kernel(PrologueParams pp) {
@@ -1301,14 +1327,23 @@ prologue_mfma_kernel(PrologueParams pp) {
     u32x4 qr[4];
     const uint16_t* qrow = pp.q + (int64_t)b * pp.q_sb + (int64_t)l * pp.q_sl + (int64_t)j * pp.q_sh + 8 * grp;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * c);
-        qr[c] = valid ? x : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int c = 0; c < 4; ++c) qr[c] = *reinterpret_cast<const u32x4*>(qrow + 32 * c);
+    // The table rows go out with the query and basis loads (with positions,
+    // after the position load they depend on).
+    RopeRow rr;
     if (pp.cos) {
         const int64_t pos = query_rope_row(pp, b, l);
-        rope_operand(qr, pp.cos + pos * D, pp.sin + pos * D, grp);
+        load_rope_row(rr, pp.cos + pos * D, pp.sin + pos * D, grp);
     }
+    u32x4 kb[4];
+    if (pp.shift) {
+        const uint16_t* bk = pp.up_k_bias + (int64_t)h * D + 8 * grp;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kb[c] = *reinterpret_cast<const u32x4*>(bk + 32 * c);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qr[c] = valid ? qr[c] : u32x4{0u, 0u, 0u, 0u};
+    if (pp.cos) rope_operand(qr, rr);
     const int64_t prow = ((int64_t)b * pp.Lq + l) * pp.Hq + j;
     if (valid) {
 #pragma unroll
@@ -1324,11 +1359,10 @@ prologue_mfma_kernel(PrologueParams pp) {
                 u32x2{f32_to_bf16(t4[0]) | (f32_to_bf16(t4[1]) << 16), f32_to_bf16(t4[2]) | (f32_to_bf16(t4[3]) << 16)};
     }
     if (pp.shift) {
-        const uint16_t* bk = pp.up_k_bias + (int64_t)h * D + 8 * grp;
         float dot = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const u32x4 bb = *reinterpret_cast<const u32x4*>(bk + 32 * c);
+            const u32x4 bb = kb[c];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 dot += bf16_to_f32(qr[c][e] & 0xffffu) * bf16_to_f32(bb[e] & 0xffffu);
@@ -1717,7 +1751,7 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     const int wown = bd ? rv : (int)Rv;
     int fast_cap = kMaxSplits;
     if (wown % 8 == 0 && wown <= kFastLatW)
-        fast_cap = std::max(1, std::min(kFastLatPer * (256 / wown), 256 - raw_req0));
+        fast_cap = std::max(1, std::min(fast_lat_splits(wown, 256), 256 - raw_req0));
     const int lat_groups = (int)B * ((((P + cols - 1) / cols) + kWaves - 1) / kWaves);
     if (a->lat_splits <= 0) lat_target = std::min<int64_t>(lat_target, (int64_t)lat_groups * fast_cap);
     p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, lat_target);
@@ -1994,7 +2028,7 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
         int slots = cu * recon_occupancy(p->ksr, p->vl);
         // as for the latent decode: stay within the fast combine's split count
         const int wv = 32 * p->vl;
-        const int fast_cap = std::max(1, std::min(kFastLatPer * (256 / wv), 256 - raw_req));
+        const int fast_cap = std::max(1, std::min(fast_lat_splits(wv, 256), 256 - raw_req));
         if (a->lat_splits <= 0) slots = std::min<int64_t>(slots, (int64_t)B * ((Hkv + kWaves - 1) / kWaves) * fast_cap);
         p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, wv, a->lat_splits, slots);
     } else {
