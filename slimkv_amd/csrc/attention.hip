@@ -28,6 +28,7 @@
 #include <cmath>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace slimkv {
@@ -222,6 +223,16 @@ struct TilePages {
     int32_t v[KS / 2];
 };
 
+// When a page holds at least 16 rows a 16-row tile touches at most two pages:
+// the wave reads their ids once per tile (p0 for the page of the tile's first
+// row, p1 for the next one), and each lane places its row from the first row's
+// slot with one compare instead of a division per row.  r0c is the tile's
+// first row clamped to the sequence's last row, as every row is.
+struct TilePair {
+    int32_t p0, p1;
+    int r0c, slot0;
+};
+
 // Paged variant of load_tile: the same lane/piece mapping, each row's base
 // taken from its page id.  Any page id is clamped into the pool, so every
 // address is inside it whatever the table holds.
@@ -259,11 +270,49 @@ __device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages
     }
 }
 
+// load_tile_paged with the tile's two pages: the same lane/piece mapping and
+// clamping (a lane's clamped row is at most 15 rows past r0c).
+template <int KS>
+__device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& tp, const Seg& sg,
+                                               const uint16_t* kpage, const uint16_t* vpage, int r0, int r_end,
+                                               int last_valid, int span_k, int span_v, int col, int grp, int lane,
+                                               bool act) {
+    constexpr int VT = KS;
+    auto row_base = [&](int row) -> int64_t {
+        int slot = tp.slot0 + (min(row, last_valid) - tp.r0c);
+        const bool next = slot >= sg.slots;
+        slot = next ? slot - sg.slots : slot;
+        return (int64_t)(next ? tp.p1 : tp.p0) * sg.page_stride + (int64_t)slot * sg.k_sn;
+    };
+    {
+        const int row = r0 + col;
+        const bool rv = act && row < r_end;
+        const uint16_t* src = kpage + row_base(row);
+#pragma unroll
+        for (int c = 0; c < KS / 2; ++c) {
+            const int kk = 32 * c + 8 * grp;
+            const bool ok = rv && kk + 8 <= span_k;
+            t.k[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src + (ok ? kk : 0)));
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < VT / 2; ++c) {
+        const int p = 64 * c + lane;
+        const int row = r0 + p / (2 * VT);
+        const int pc = p % (2 * VT);
+        const bool ok = act && row < r_end && 8 * pc + 8 <= span_v;
+        const uint16_t* src = vpage + row_base(row) + (ok ? 8 * pc : 0);
+        t.v[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src));
+    }
+}
+
 // A workgroup owns (batch b, group of 4 tile slots, key split s); a slot is a
 // (KV head, column tile) pair and each wave takes one slot.  The four waves
 // therefore stream the same keys' rows at the same time (whole DRAM pages),
 // never exchange data, and write their own partials.
-template <int KS, bool PIPE, bool PAGED = false>
+// PAGED: 0 dense rows, 1 rows through per-lane page ids, 2 rows through the
+// tile's two pages (pages of at least 16 rows).
+template <int KS, bool PIPE, int PAGED = 0>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int Hq,
                                               float scale_log2, char* lds) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
@@ -344,19 +393,37 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         const int r = min(row, last_valid);
         return tab[2 * (sg.slots_shift >= 0 ? (r >> sg.slots_shift) : r / sg.slots)];   // low word
     };
-    auto load_pages = [&](TilePages<KS>& pg, int it) {
+    const int last_page = PAGED == 2 ? last_valid / sg.slots : 0;
+    auto load_pages = [&](auto& pg, int it) {
         const int r0 = it < ntile ? r_begin + it * 16 : r_begin;
-        pg.k = page_of(r0 + col);
+        if constexpr (PAGED == 2) {
+            const int r0c = __builtin_amdgcn_readfirstlane(min(r0, last_valid));
+            const int pi = __builtin_amdgcn_readfirstlane(r0c / sg.slots);
+            const int32_t np = (int32_t)sg.num_pages;
+            const int32_t a = __builtin_amdgcn_readfirstlane(tab[2 * pi]);
+            const int32_t c = __builtin_amdgcn_readfirstlane(tab[2 * min(pi + 1, last_page)]);
+            pg.r0c = r0c;
+            pg.slot0 = r0c - pi * sg.slots;
+            pg.p0 = a < 0 ? 0 : (a >= np ? np - 1 : a);
+            pg.p1 = c < 0 ? 0 : (c >= np ? np - 1 : c);
+        } else {
+            pg.k = page_of(r0 + col);
 #pragma unroll
-        for (int c = 0; c < VT / 2; ++c) pg.v[c] = page_of(r0 + (64 * c + lane) / (2 * VT));
+            for (int c = 0; c < VT / 2; ++c) pg.v[c] = page_of(r0 + (64 * c + lane) / (2 * VT));
+        }
     };
-    auto fetch_paged = [&](TileRegs<KS>& tr, const TilePages<KS>& pg, int it) {
+    auto fetch_paged = [&](TileRegs<KS>& tr, const auto& pg, int it) {
         const bool act = it < ntile;
         const int r0 = act ? r_begin + it * 16 : r_begin;
-        load_tile_paged<KS>(tr, pg, sg, kbase, vbase, r0, act ? r_end : r_begin, last_valid, span_k, span_v, col,
-                            grp, lane, act);
+        if constexpr (PAGED == 2)
+            load_tile_pair<KS>(tr, pg, sg, kbase, vbase, r0, act ? r_end : r_begin, last_valid, span_k, span_v, col,
+                               grp, lane, act);
+        else
+            load_tile_paged<KS>(tr, pg, sg, kbase, vbase, r0, act ? r_end : r_begin, last_valid, span_k, span_v,
+                                col, grp, lane, act);
     };
-    TilePages<KS> pcur, poth;
+    using PageIds = std::conditional_t<PAGED == 2, TilePair, TilePages<KS>>;
+    PageIds pcur, poth;
     // First tile in flight before the query operand is fetched.
     TileRegs<KS> cur;
     if constexpr (PAGED) {
@@ -514,7 +581,7 @@ struct SplitWaves {
     static constexpr int value = KA <= 4 ? 4 : (KA <= 6 ? 3 : 1);
 };
 
-template <int KA, int KB, bool PAGED = false>
+template <int KA, int KB, int PAGED = 0>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SplitWaves<KA>::value)))
 split_kernel(SplitParams prm) {
     constexpr int LA = SplitLds<KA>::bytes;
@@ -1388,15 +1455,21 @@ thread_local hipEvent_t g_after = nullptr;
 
 // Launch the split kernel bracketed by the caller's profiling events, if set.
 hipError_t dispatch_split(int ka, int kb, const struct SplitParams& prm, int grid, hipStream_t st);
-hipError_t dispatch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
+template <int MODE>
+hipError_t launch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
     switch (ka) {
-        case 2: hipLaunchKernelGGL((split_kernel<2, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
-        case 4: hipLaunchKernelGGL((split_kernel<4, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
-        case 6: hipLaunchKernelGGL((split_kernel<6, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
-        case 8: hipLaunchKernelGGL((split_kernel<8, 8, true>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 2: hipLaunchKernelGGL((split_kernel<2, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 4: hipLaunchKernelGGL((split_kernel<4, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 6: hipLaunchKernelGGL((split_kernel<6, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 8: hipLaunchKernelGGL((split_kernel<8, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+// Pages of at least 16 rows take the two-pages-per-tile addressing.
+hipError_t dispatch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
+    return prm.seg[0].slots >= 16 ? launch_split_paged<2>(ka, prm, grid, st) : launch_split_paged<1>(ka, prm, grid, st);
 }
 
 hipError_t timed_split(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st, bool paged = false) {

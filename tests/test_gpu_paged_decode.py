@@ -5,7 +5,8 @@ table, instead of restore_memory's gather (slimkv/vllm_plugin/paged_model.py:
 
 Index handling is checked bit-exactly: with the same key splits the paged
 decode equals gather + dense decode bit for bit (same rows, same arithmetic),
-for power-of-two and other slot counts, ragged lengths including empty
+for power-of-two and other slot counts (pages of 2 to 60 rows, both
+addressing modes of the kernel), ragged lengths including empty
 sequences, and table entries past a sequence's pages that hold garbage.  The
 automatic compact schedule (splits sized from the total row count, only
 non-empty splits launched) is checked against the oracle's float64 attention
@@ -64,6 +65,10 @@ def _dense(c):
     ((16, 4, 256, 256, 1024), [333, 1024, 5, 0, 64, 900]),              # 4 slots per page (t4)
     ((12, 4, 256, 256, 1024), [301, 2, 299, 150]),                      # 3 slots: non-power-of-two
     ((16, 8, 128, 384, 1024), [513, 77, 1, 240]),                       # rank 16 K, rank 48 V
+    # pages of at least 16 rows: a tile reads its two pages' ids once
+    ((480, 8, 256, 256, 1024), [1000, 0, 37, 1, 777, 59, 60, 61, 1024]),  # 60 slots (the plugin's t8 pages)
+    ((256, 8, 256, 256, 1024), [513, 31, 32, 33, 0, 2000]),             # 32 slots: power of two
+    ((128, 8, 128, 384, 1024), [513, 77, 1, 240, 15, 16, 17]),          # 16 slots: tiles on page boundaries
 ])
 @pytest.mark.parametrize('splits', [3, 8])
 def test_paged_equals_gather_then_decode_bitwise(device, layout_args, lengths, splits):
@@ -84,14 +89,16 @@ def test_paged_equals_gather_then_decode_bitwise(device, layout_args, lengths, s
     assert torch.equal(got_lse, want_lse)
 
 
+@pytest.mark.parametrize('layout_args', [(16, 8, 256, 256, 1024), (480, 8, 256, 256, 1024)])
 @pytest.mark.parametrize('rows_total', ['exact', 0, 'low', 'high'])
-def test_compact_schedule_matches_oracle(device, rows_total):
+def test_compact_schedule_matches_oracle(device, rows_total, layout_args):
     """Automatic splits: rows_total only sizes them, so an exact, unknown,
-    too-low or too-high hint gives the same (correct) result."""
+    too-low or too-high hint gives the same (correct) result, with 2-row and
+    60-row pages."""
     from slimkv_amd import kernels
     lengths = [4100, 0, 1, 2047, 16, 3000, 255, 8191]
     raw_lengths = [1, 133, 64, 17, 4, 100, 2, 129]
-    c = _case(device, (16, 8, 256, 256, 1024), lengths, raw_lengths, seed=11)
+    c = _case(device, layout_args, lengths, raw_lengths, seed=11)
     hint = {'exact': sum(lengths), 0: 0, 'low': 100, 'high': 10 * sum(lengths)}[rows_total]
     scale = D ** -0.5
     got, lse = kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'], c['lengths'],
