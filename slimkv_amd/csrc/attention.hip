@@ -1053,6 +1053,7 @@ combine_kernel(CombineParams cp) {
 // splits, narrow latent slices): every global load is issued before the first
 // reduction, so the whole combine costs one memory round trip.
 constexpr int kFastRawSplits = 32;
+constexpr int kFastRawPer = 8;      // 16-byte raw partial loads (4 columns) per thread
 constexpr int kFastLatW = 64;
 constexpr int kFastLatPer = 8;      // 16-byte latent partial loads (4 columns) per thread
 
@@ -1061,13 +1062,15 @@ constexpr int kFastLatPer = 8;      // 16-byte latent partial loads (4 columns) 
 constexpr int fast_lat_splits(int b_w, int T) { return kFastLatPer * (T / (b_w / 4)); }
 
 // T = 128 or 256 threads: one split's (m, l) per thread, so a_splits +
-// b_splits <= T, and the latent partials as 4-column quads: thread t takes
-// quad t % (b_w / 4) of splits t / (b_w / 4) + i * (T / (b_w / 4)).
+// b_splits <= T, and the raw and latent partials as 4-column quads: thread t
+// takes quad t % (w / 4) of splits t / (w / 4) + i * (T / (w / 4)) of a
+// segment of width w; the groups of splits meet in LDS.
 template <int T>
 __global__ void __launch_bounds__(T)
 combine_fast_kernel(CombineParams cp) {
     __shared__ float wts[2 * kMaxSplits];
     __shared__ float4 part[T];
+    __shared__ float4 partr[T];
     __shared__ float accb[kFastLatW];
     __shared__ float red[3 * (T / 64)];      // per-wave maximum, then the two sums
     const int t = threadIdx.x;
@@ -1093,10 +1096,16 @@ combine_fast_kernel(CombineParams cp) {
     const float shift = (cp.b_splits && cp.b_shift) ? cp.b_shift[row] * kLog2e : 0.f;
     const int dd = t;
     const bool has_dd = dd < cp.D;
-    float ra[kFastRawSplits];
+    const int rq = cp.a_w / 4;
+    const int rkq = t % rq, r0 = t / rq, rstep = T / rq;
+    float4 ra[kFastRawPer];
     const float* aacc = cp.a_acc + row * cp.a_splits * cp.a_w;
 #pragma unroll
-    for (int s = 0; s < kFastRawSplits; ++s) ra[s] = (has_dd && s < cp.a_splits) ? aacc[(int64_t)s * cp.a_w + dd] : 0.f;
+    for (int i = 0; i < kFastRawPer; ++i) {
+        const int s = r0 + i * rstep;
+        ra[i] = (s < cp.a_splits && r0 < rstep) ? *reinterpret_cast<const float4*>(aacc + (int64_t)s * cp.a_w + 4 * rkq)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float4 lb[kFastLatPer];
     const int quads = cp.b_w / 4;
     const int kq = quads ? t % quads : 0;
@@ -1158,7 +1167,19 @@ combine_fast_kernel(CombineParams cp) {
     }
     const float L = LA + LB;
 
-    // -- latent accumulator --
+    // -- weighted partial sums of both segments, one barrier --
+    {
+        float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < kFastRawPer; ++i) {
+            const int s = r0 + i * rstep;
+            if (s < cp.a_splits && r0 < rstep) {
+                const float w = wts[s];
+                sum.x += ra[i].x * w; sum.y += ra[i].y * w; sum.z += ra[i].z * w; sum.w += ra[i].w * w;
+            }
+        }
+        partr[t] = sum;
+    }
     if (cp.b_splits) {
         float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -1170,7 +1191,10 @@ combine_fast_kernel(CombineParams cp) {
             }
         }
         part[t] = sum;
-        __syncthreads();
+    }
+    __syncthreads();
+    // -- latent accumulator --
+    if (cp.b_splits) {
         if (t < cp.b_w) {
             const float* pf = reinterpret_cast<const float*>(part);
             float acc = 0.f;
@@ -1181,10 +1205,9 @@ combine_fast_kernel(CombineParams cp) {
     }
     // -- output --
     if (has_dd) {
+        const float* pr4 = reinterpret_cast<const float*>(partr);
         float sum = 0.f;
-#pragma unroll
-        for (int s = 0; s < kFastRawSplits; ++s)
-            if (s < cp.a_splits) sum += ra[s] * wts[s];
+        for (int g2 = 0; g2 < rstep; ++g2) sum += pr4[4 * (g2 * rq + dd / 4) + dd % 4];
         if (cp.b_splits) {
             float lift = 0.f;
 #pragma unroll
@@ -1211,7 +1234,8 @@ combine_fast_kernel(CombineParams cp) {
 // idle in the weighted sum.
 bool combine_fast_ok(const CombineParams& cp, int T) {
     if (cp.b_splits && !cp.up_v) return false;
-    return cp.D <= T && cp.a_splits <= kFastRawSplits && cp.a_splits + cp.b_splits <= T && cp.b_w <= kFastLatW &&
+    return cp.D <= T && cp.a_w >= cp.D && cp.a_w % 4 == 0 && cp.a_w <= 4 * T && cp.a_splits <= kFastRawSplits &&
+           cp.a_splits <= kFastRawPer * (T / (cp.a_w / 4)) && cp.a_splits + cp.b_splits <= T && cp.b_w <= kFastLatW &&
            (cp.b_splits == 0 || (cp.b_w % 8 == 0 && cp.b_splits <= fast_lat_splits(cp.b_w, T)));
 }
 
