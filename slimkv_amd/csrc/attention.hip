@@ -1049,6 +1049,12 @@ combine_kernel(CombineParams cp) {
     }
 }
 
+// Raw buffer resource over `bytes` bytes at p (a null p with 0 bytes: every
+// load returns zeros).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // Fast path for the fused decode's shapes (D <= 128 output features, few raw
 // splits, narrow latent slices): every global load is issued before the first
 // reduction, so the whole combine costs one memory round trip.
@@ -1086,25 +1092,36 @@ combine_fast_kernel(CombineParams cp) {
     const float* aml = cp.a_ml + row * cp.a_splits * 2;
     const float* bml = cp.b_splits ? cp.b_ml + row * cp.b_splits * 2 : nullptr;
 
-    // -- issue every load --
-    float mv = kNegInf, lv = 0.f;
-    if (t < total) {
-        const float* src = t < cp.a_splits ? aml + 2 * t : bml + 2 * (t - cp.a_splits);
-        mv = src[0];
-        lv = src[1];
-    }
-    const float shift = (cp.b_splits && cp.b_shift) ? cp.b_shift[row] * kLog2e : 0.f;
+    // -- issue every load --  All through buffer resources: a lane with
+    // nothing to read uses an offset past the resource's range and receives
+    // zeros, and an absent optional operand is a resource of zero bytes, so the
+    // loads form one straight block with no branch around any of them and the
+    // split statistics, issued first, are waited on alone -- the weight
+    // reductions run while the partials are still arriving.
+    constexpr uint32_t kPast = 0x7ffffff0u;          // beyond every resource below
+    const bool live = t < total;
+    const bool in_a = t < cp.a_splits;
+    const auto r_aml = buffer_of(aml, (uint32_t)cp.a_splits * 8u);
+    const auto r_bml = buffer_of(bml, cp.b_splits ? (uint32_t)cp.b_splits * 8u : 0u);
+    const auto mla = __builtin_amdgcn_raw_buffer_load_b64(r_aml, in_a ? 8u * t : kPast, 0, 0);
+    const auto mlb = __builtin_amdgcn_raw_buffer_load_b64(r_bml, (!in_a && live) ? 8u * (t - cp.a_splits) : kPast, 0, 0);
+    float mv = live ? __uint_as_float(in_a ? mla[0] : mlb[0]) : kNegInf;
+    const float lv = __uint_as_float(in_a ? mla[1] : mlb[1]);     // zero past the live splits
+    const auto r_shift = buffer_of(cp.b_shift ? cp.b_shift + row : nullptr, (cp.b_splits && cp.b_shift) ? 4u : 0u);
+    const float shift = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_shift, 0u, 0, 0)) * kLog2e;
     const int dd = t;
     const bool has_dd = dd < cp.D;
     const int rq = cp.a_w / 4;
     const int rkq = t % rq, r0 = t / rq, rstep = T / rq;
     float4 ra[kFastRawPer];
     const float* aacc = cp.a_acc + row * cp.a_splits * cp.a_w;
+    const auto r_aacc = buffer_of(aacc, (uint32_t)(cp.a_splits * cp.a_w) * 4u);
 #pragma unroll
     for (int i = 0; i < kFastRawPer; ++i) {
         const int s = r0 + i * rstep;
-        ra[i] = (s < cp.a_splits && r0 < rstep) ? *reinterpret_cast<const float4*>(aacc + (int64_t)s * cp.a_w + 4 * rkq)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool ok = s < cp.a_splits && r0 < rstep;
+        ra[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                    r_aacc, ok ? (uint32_t)(s * cp.a_w + 4 * rkq) * 4u : kPast, 0, 0));
     }
     float4 lb[kFastLatPer];
     const int quads = cp.b_w / 4;
@@ -1112,22 +1129,27 @@ combine_fast_kernel(CombineParams cp) {
     const int sstep = quads ? T / quads : 1;
     const int s0 = quads ? t / quads : 0;
     const float* bacc = cp.b_splits ? cp.b_acc + row * cp.b_splits * cp.b_w : nullptr;
+    const auto r_bacc = buffer_of(bacc, (uint32_t)(cp.b_splits * cp.b_w) * 4u);
 #pragma unroll
     for (int i = 0; i < kFastLatPer; ++i) {
         const int s = s0 + i * sstep;
-        lb[i] = (bacc && s < bsp && s0 < sstep) ? *reinterpret_cast<const float4*>(bacc + (int64_t)s * cp.b_w + 4 * kq)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool ok = s < bsp && s0 < sstep;
+        lb[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                    r_bacc, ok ? (uint32_t)(s * cp.b_w + 4 * kq) * 4u : kPast, 0, 0));
     }
+    // V lift rows: W_V row h*D + dd, the head's b_w columns (own block when
+    // block-diagonal); rows past D read zeros.
+    const uint32_t w_bytes = cp.b_splits ? (uint32_t)((int64_t)cp.Hkv * cp.D * cp.up_v_ld * 2) : 0u;
+    const auto r_wv = buffer_of(cp.up_v, w_bytes);
+    const uint32_t w_off = (uint32_t)((((int64_t)h * cp.D + dd) * cp.up_v_ld + (cp.blockdiag ? h * cp.b_w : 0)) * 2);
     u32x4 wv[kFastLatW / 8];
-    const uint16_t* wr = nullptr;
-    if (cp.b_splits && has_dd) {
-        const int64_t wrow = (int64_t)h * cp.D + dd;
-        wr = cp.up_v + wrow * cp.up_v_ld + (cp.blockdiag ? h * cp.b_w : 0);
-    }
 #pragma unroll
     for (int c = 0; c < kFastLatW / 8; ++c)
-        wv[c] = (wr && 8 * c < cp.b_w) ? *reinterpret_cast<const u32x4*>(wr + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-    const float bias_v = (cp.b_splits && cp.up_v_bias && has_dd) ? bf16_to_f32(cp.up_v_bias[(int64_t)h * cp.D + dd]) : 0.f;
+        wv[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                    r_wv, (has_dd && 8 * c < cp.b_w) ? w_off + 16u * c : kPast, 0, 0));
+    const auto r_bias = buffer_of(cp.up_v_bias, (cp.b_splits && cp.up_v_bias) ? (uint32_t)(cp.Hkv * cp.D * 2) : 0u);
+    const float bias_v = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(
+        r_bias, has_dd ? (uint32_t)(((int64_t)h * cp.D + dd) * 2) : kPast, 0, 0));
 
     // -- split weights --
     if (t >= cp.a_splits && t < total && mv != kNegInf) mv += shift;
