@@ -122,7 +122,8 @@ __device__ __forceinline__ void load_rope_row(RopeRow& t, const float* cs, const
 // Rotate one head_dim-128 query row held as MFMA operand pieces: x[c] holds
 // elements 32c + 8*grp + [0, 8); the rotate-half partner of piece c is c ^ 2.
 // out = bf16(bf16(x * bf16(cos)) + bf16(rotate_half(x) * bf16(sin))), the
-// reference's bf16 operation order (decode_kernels.py:7-51).
+// reference's bf16 operation order (decode_kernels.py:7-51), each rounding one
+// packed conversion (round to nearest even).
 __device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const RopeRow& t) {
     float v[4][8];
 #pragma unroll
@@ -144,10 +145,10 @@ __device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const RopeRow& t) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float partner = c < 2 ? -v[c ^ 2][i + u] : v[c ^ 2][i + u];
-                o[u] = round_bf16(round_bf16(v[c][i + u] * round_bf16(cv[i + u])) +
-                                  round_bf16(partner * round_bf16(sv[i + u])));
+                o[u] = round_bf16_hw(v[c][i + u] * round_bf16_hw(cv[i + u])) +
+                       round_bf16_hw(partner * round_bf16_hw(sv[i + u]));
             }
-            w[i / 2] = f32_to_bf16(o[0]) | (f32_to_bf16(o[1]) << 16);
+            w[i / 2] = pack_bf16(o[0], o[1]);       // the sum's rounding
         }
         x[c] = u32x4{w[0], w[1], w[2], w[3]};
     }
