@@ -1341,10 +1341,11 @@ prologue_kernel(PrologueParams pp) {
             for (int i = 0; i < 8; ++i) {
                 float pt = bf16_to_f32(i & 1 ? (ps[i / 2] >> 16) : (ps[i / 2] & 0xffffu));
                 if (dd < half) pt = -pt;
-                x[i] = round_bf16(round_bf16(x[i] * round_bf16(cs[i])) + round_bf16(pt * round_bf16(ss[i])));
+                x[i] = round_bf16_hw(round_bf16_hw(x[i] * round_bf16_hw(cs[i])) +
+                                     round_bf16_hw(pt * round_bf16_hw(ss[i])));
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) xs[i] = f32_to_bf16(x[2 * i]) | (f32_to_bf16(x[2 * i + 1]) << 16);
+            for (int i = 0; i < 4; ++i) xs[i] = pack_bf16(x[2 * i], x[2 * i + 1]);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) qs[r * D + dd + i] = x[i];
