@@ -499,8 +499,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         m = mnew;
 #pragma unroll
         for (int i = 0; i < VT; ++i) acc[i] *= alpha;
-        const v4s pb = as_v4s(f32_to_bf16(p[0]) | (f32_to_bf16(p[1]) << 16),
-                              f32_to_bf16(p[2]) | (f32_to_bf16(p[3]) << 16));
+        const v4s pb = as_v4s(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]));
         wave_lds_fence();
 #pragma unroll
         for (int u = 0; u < VT / 2; ++u) {
