@@ -101,8 +101,8 @@ __global__ void __launch_bounds__(256) down_kernel(DownParams p) {
         if (p.splits == 1) {
             const int b = m / p.n, i = m % p.n;
             u32x2 w;
-            w.x = f32_to_bf16(acc[f][0]) | (f32_to_bf16(acc[f][1]) << 16);
-            w.y = f32_to_bf16(acc[f][2]) | (f32_to_bf16(acc[f][3]) << 16);
+            w.x = pack_bf16(acc[f][0], acc[f][1]);
+            w.y = pack_bf16(acc[f][2], acc[f][3]);
             uint16_t* dst = dst_row(p, b, i);
             if (dst) *reinterpret_cast<u32x2*>(dst + nn) = w;
         } else {
@@ -123,8 +123,8 @@ __global__ void __launch_bounds__(256) down_reduce_kernel(DownParams p) {
     for (int s = 1; s < p.splits; ++s) sum += *reinterpret_cast<const v4f*>(p.part + ((int64_t)s * M + m) * p.N + nn);
     const int b = (int)(m / p.n), i = (int)(m % p.n);
     u32x2 w;
-    w.x = f32_to_bf16(sum[0]) | (f32_to_bf16(sum[1]) << 16);
-    w.y = f32_to_bf16(sum[2]) | (f32_to_bf16(sum[3]) << 16);
+    w.x = pack_bf16(sum[0], sum[1]);
+    w.y = pack_bf16(sum[2], sum[3]);
     uint16_t* dst = dst_row(p, b, i);
     if (dst) *reinterpret_cast<u32x2*>(dst + nn) = w;
 }

@@ -69,7 +69,7 @@ recon_kernel(ReconParams p) {
             const int d = 16 * t + 4 * grp + i;
             float v = acc[t][i];
             if (p.bias) v += bf16_to_f32(p.bias[(int64_t)h * D + d]);
-            x[t][i] = round_bf16(v);
+            x[t][i] = round_bf16_hw(v);
         }
     if (p.positions) {
         const int64_t pos = clamp_i64(p.positions[(int64_t)b * p.pos_sb + row], 0, p.rope_rows - 1);
@@ -82,7 +82,7 @@ recon_kernel(ReconParams p) {
             for (int i = 0; i < 4; ++i) {
                 const int d = 16 * t + 4 * grp + i;
                 const float partner = t < 4 ? -x[t + 4][i] : x[t - 4][i];
-                y[t][i] = round_bf16(round_bf16(x[t][i] * round_bf16(cr[d])) + round_bf16(partner * round_bf16(sr[d])));
+                y[t][i] = round_bf16_hw(round_bf16_hw(x[t][i] * round_bf16_hw(cr[d])) + round_bf16_hw(partner * round_bf16_hw(sr[d])));
             }
 #pragma unroll
         for (int t = 0; t < 8; ++t)
@@ -93,8 +93,8 @@ recon_kernel(ReconParams p) {
     uint16_t* orow = p.out + (int64_t)b * p.o_sb + dst * p.o_sn + (int64_t)h * p.o_sh;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-        const uint32_t lo = f32_to_bf16(x[t][0]) | (f32_to_bf16(x[t][1]) << 16);
-        const uint32_t hi = f32_to_bf16(x[t][2]) | (f32_to_bf16(x[t][3]) << 16);
+        const uint32_t lo = pack_bf16(x[t][0], x[t][1]);
+        const uint32_t hi = pack_bf16(x[t][2], x[t][3]);
         *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * grp) = u32x2{lo, hi};
     }
 }
@@ -156,7 +156,7 @@ recon_stream_kernel(ReconParams p, int segs) {
 #pragma unroll
             for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[t][i] = round_bf16(p.bias ? acc[t][i] + bias[t][i] : acc[t][i]);
+                for (int i = 0; i < 4; ++i) x[t][i] = round_bf16_hw(p.bias ? acc[t][i] + bias[t][i] : acc[t][i]);
             if (p.positions) {
                 const int64_t pos = clamp_i64(p.positions[(int64_t)b * p.pos_sb + row], 0, p.rope_rows - 1);
                 const float* cr = p.cos + pos * D;
@@ -170,7 +170,7 @@ recon_stream_kernel(ReconParams p, int segs) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const float partner = t < 4 ? -x[t + 4][i] : x[t - 4][i];
-                        y[t][i] = round_bf16(round_bf16(x[t][i] * round_bf16(cv[i])) + round_bf16(partner * round_bf16(sv[i])));
+                        y[t][i] = round_bf16_hw(round_bf16_hw(x[t][i] * round_bf16_hw(cv[i])) + round_bf16_hw(partner * round_bf16_hw(sv[i])));
                     }
                 }
 #pragma unroll
@@ -182,8 +182,8 @@ recon_stream_kernel(ReconParams p, int segs) {
             uint16_t* orow = p.out + (int64_t)b * p.o_sb + dst * p.o_sn + (int64_t)h * p.o_sh;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const uint32_t lo = f32_to_bf16(x[t][0]) | (f32_to_bf16(x[t][1]) << 16);
-                const uint32_t hi = f32_to_bf16(x[t][2]) | (f32_to_bf16(x[t][3]) << 16);
+                const uint32_t lo = pack_bf16(x[t][0], x[t][1]);
+                const uint32_t hi = pack_bf16(x[t][2], x[t][3]);
                 *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * grp) = u32x2{lo, hi};
             }
         }

@@ -32,20 +32,18 @@ __device__ __forceinline__ void rope8(const uint16_t* src, uint16_t* dst, int dd
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        uint32_t pair = 0;
+        float sum[2];
 #pragma unroll
         for (int hbit = 0; hbit < 2; ++hbit) {
             const int idx = 2 * e + hbit;
             const float x = bf16_to_f32(hbit ? (xs[e] >> 16) : (xs[e] & 0xffffu));
             float pt = bf16_to_f32(hbit ? (ps[e] >> 16) : (ps[e] & 0xffffu));
             if (dd < half) pt = -pt;
-            const float c = round_bf16(cr[idx]);
-            const float s = round_bf16(sr[idx]);
-            const float first = round_bf16(x * c);
-            const float second = round_bf16(pt * s);
-            pair |= f32_to_bf16(first + second) << (16 * hbit);
+            const float c = round_bf16_hw(cr[idx]);
+            const float s = round_bf16_hw(sr[idx]);
+            sum[hbit] = round_bf16_hw(x * c) + round_bf16_hw(pt * s);
         }
-        o[e] = pair;
+        o[e] = pack_bf16(sum[0], sum[1]);
     }
     *reinterpret_cast<u32x4*>(dst + dd) = u32x4{o[0], o[1], o[2], o[3]};
 }
@@ -167,7 +165,7 @@ merge_kernel(slimkv_merge_args a) {
     for (int e = 0; e < 4; ++e) {
         const float r0 = bf16_to_f32(rs[e] & 0xffffu), r1 = bf16_to_f32(rs[e] >> 16);
         const float l0 = bf16_to_f32(ls[e] & 0xffffu), l1 = bf16_to_f32(ls[e] >> 16);
-        o[e] = f32_to_bf16(rw * r0 + lw * l0) | (f32_to_bf16(rw * r1 + lw * l1) << 16);
+        o[e] = pack_bf16(rw * r0 + lw * l0, rw * r1 + lw * l1);
     }
     *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + row * a.dim + dd) = u32x4{o[0], o[1], o[2], o[3]};
 }
