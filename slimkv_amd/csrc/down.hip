@@ -49,6 +49,10 @@ __device__ __forceinline__ uint16_t* dst_row(const DownParams& p, int b, int i) 
 
 constexpr int kMFrags = 4;       // 64 rows per wave
 
+__device__ __forceinline__ u32x4 zero_if_not(bool ok, u32x4 v) {
+    return u32x4{ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
+}
+
 __global__ void __launch_bounds__(256) down_kernel(DownParams p) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -86,10 +90,24 @@ __global__ void __launch_bounds__(256) down_kernel(DownParams p) {
     v4f acc[kMFrags];
 #pragma unroll
     for (int f = 0; f < kMFrags; ++f) acc[f] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int k = k_lo; k < k_hi; k += 32) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(wrow + k);
+    // Four 32-wide steps per pass: every operand load of the pass is issued
+    // before its first MFMA (steps past k_hi read column k_lo and are zeroed),
+    // so a pass costs one memory round trip; the accumulation order over k is
+    // unchanged.
+    for (int k0 = k_lo; k0 < k_hi; k0 += 128) {
+        u32x4 a[4], xv[4][kMFrags];
 #pragma unroll
-        for (int f = 0; f < kMFrags; ++f) acc[f] = mfma32(a, *reinterpret_cast<const u32x4*>(xrow[f] + k), acc[f]);
+        for (int u = 0; u < 4; ++u) {
+            const bool kin = k0 + 32 * u < k_hi;
+            const int kk = kin ? k0 + 32 * u : k_lo;
+            a[u] = zero_if_not(kin, *reinterpret_cast<const u32x4*>(wrow + kk));
+#pragma unroll
+            for (int f = 0; f < kMFrags; ++f) xv[u][f] = zero_if_not(kin, *reinterpret_cast<const u32x4*>(xrow[f] + kk));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int f = 0; f < kMFrags; ++f) acc[f] = mfma32(a[u], xv[u][f], acc[f]);
     }
     const int M_ = M;
 #pragma unroll
