@@ -837,8 +837,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         m = mnew;
 #pragma unroll
         for (int i = 0; i < 2 * VL; ++i) acc[i] *= alpha;
-        const v4s pb = as_v4s(f32_to_bf16(pr[0]) | (f32_to_bf16(pr[1]) << 16),
-                              f32_to_bf16(pr[2]) | (f32_to_bf16(pr[3]) << 16));
+        const v4s pb = as_v4s(pack_bf16(pr[0], pr[1]), pack_bf16(pr[2], pr[3]));
         wave_lds_fence();
 #pragma unroll
         for (int u = 0; u < VL; ++u) {
@@ -1042,7 +1041,7 @@ combine_kernel(CombineParams cp) {
             sum += lift;
             if (cp.up_v_bias) sum += bf16_to_f32(cp.up_v_bias[wrow]) * LB;
         }
-        orow[dd] = (uint16_t)f32_to_bf16(sum * inv);
+        orow[dd] = (uint16_t)pack_bf16(sum * inv, 0.f);
     }
     if (cp.lse && threadIdx.x == 0) {
         cp.lse[((int64_t)b * cp.Hq + j) * cp.Lq + lq] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
@@ -1245,7 +1244,7 @@ combine_fast_kernel(CombineParams cp) {
             sum += lift + bias_v * LB;
         }
         const float inv = L > 0.f ? 1.f / L : 0.f;
-        cp.out[(int64_t)b * cp.o_sb + (int64_t)lq * cp.o_sl + (int64_t)j * cp.o_sh + dd] = (uint16_t)f32_to_bf16(sum * inv);
+        cp.out[(int64_t)b * cp.o_sb + (int64_t)lq * cp.o_sl + (int64_t)j * cp.o_sh + dd] = (uint16_t)pack_bf16(sum * inv, 0.f);
     }
     if (cp.lse && t == 0)
         cp.lse[((int64_t)b * cp.Hq + j) * cp.Lq + lq] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
@@ -1405,7 +1404,7 @@ prologue_kernel(PrologueParams pp) {
             const int jj = r / pp.Lq, l = r % pp.Lq;
             uint32_t o4[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o4[e] = f32_to_bf16(sum[2 * e]) | (f32_to_bf16(sum[2 * e + 1]) << 16);
+            for (int e = 0; e < 4; ++e) o4[e] = pack_bf16(sum[2 * e], sum[2 * e + 1]);
             *reinterpret_cast<u32x4*>(pp.q_lat + (((int64_t)b * pp.Lq + l) * pp.Hq + h * g + jj) * pp.wq + 8 * k8) =
                 u32x4{o4[0], o4[1], o4[2], o4[3]};
         }
@@ -1470,7 +1469,7 @@ prologue_mfma_kernel(PrologueParams pp) {
         for (int c = 0; c < 4; ++c) t4 = mfma32(ua[ct][c], qr[c], t4);
         if (valid)
             *reinterpret_cast<u32x2*>(pp.q_lat + prow * pp.wq + 16 * ct + 4 * grp) =
-                u32x2{f32_to_bf16(t4[0]) | (f32_to_bf16(t4[1]) << 16), f32_to_bf16(t4[2]) | (f32_to_bf16(t4[3]) << 16)};
+                u32x2{pack_bf16(t4[0], t4[1]), pack_bf16(t4[2], t4[3])};
     }
     if (pp.shift) {
         float dot = 0.f;
@@ -2398,7 +2397,7 @@ __global__ void __launch_bounds__(256)
 prepare_pairs_kernel(const float* cos, const float* sin, int64_t total, uint32_t* out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    out[i] = f32_to_bf16(cos[i]) | (f32_to_bf16(sin[i]) << 16);
+    out[i] = pack_bf16(cos[i], sin[i]);
 }
 
 extern "C" int slimkv_prepare_rope_pairs(const float* cos, const float* sin, int64_t rows, int64_t dim, uint32_t* out,

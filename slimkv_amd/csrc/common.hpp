@@ -23,22 +23,9 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
     return __uint_as_float(bits << 16);
 }
 
-// Round-to-nearest-even to bf16; NaN maps to the canonical quiet NaN 0x7fc0,
-// as torch's float -> bfloat16 conversion does.
-__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
-
-__device__ __forceinline__ float round_bf16(float x) {
-    return bf16_to_f32(f32_to_bf16(x));
-}
-
-// bf16(a) | bf16(b) << 16 with the gfx950 packed conversion (round to nearest
-// even, identical to f32_to_bf16 for every non-NaN input; a NaN keeps its
-// payload, quieted, instead of becoming 0x7fc0).
+// bf16(a) | bf16(b) << 16 with the gfx950 packed conversion: round to nearest
+// even, as torch's float -> bfloat16 conversion, for every non-NaN input; a
+// NaN keeps its payload, quieted (torch writes the canonical 0x7fc0).
 typedef __bf16 bf16x2_hw __attribute__((ext_vector_type(2)));
 typedef float f32x2_hw __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
