@@ -76,19 +76,25 @@ def replay_median_ms(torch, step, replays):
 
 
 def gpu_clocks():
-    """Current shader and memory clocks as rocm-smi reports them (None if unavailable)."""
+    """Current shader and memory clocks of the first amdgpu card, read from the
+    driver's DPM tables in sysfs (the level marked '*'); None if unreadable.
+    Plain file reads: no process is started from a process that holds the GPU."""
+    import glob
     import re
-    import subprocess
-    try:
-        text = subprocess.run(['rocm-smi', '--showclocks'], capture_output=True, text=True, timeout=20).stdout
-    except (OSError, subprocess.SubprocessError):
-        return None
-    found = {}
-    for key in ('sclk', 'mclk', 'fclk', 'socclk'):
-        m = re.search(r'\b' + key + r' clock level: \d+: \(([^)]*)\)', text)
-        if m:
-            found[key] = m.group(1)
-    return found or None
+    for dev in sorted(glob.glob('/sys/class/drm/card*/device')):
+        found = {}
+        for key in ('sclk', 'mclk', 'fclk', 'socclk'):
+            try:
+                with open(os.path.join(dev, f'pp_dpm_{key}')) as f:
+                    text = f.read()
+            except OSError:
+                continue
+            m = re.search(r'^\s*\d+:\s*(\S+)\s*\*\s*$', text, re.M)
+            if m:
+                found[key] = m.group(1)
+        if found:
+            return found
+    return None
 
 
 def draw_ranks(layers, seed):

@@ -172,3 +172,66 @@ def test_down_project_matches_loops_and_selects_rows():
                 assert abs(got[b, i, n] - want) < 1e-12
     np.testing.assert_array_equal(oa.down_project(x, w, rows), round_bf16(got))
     np.testing.assert_array_equal(oa.down_project(x, w), oa.down_project(x, w, list(range(7))))
+
+
+def _recon_loops(q, k, v, scale, mask, bf16):
+    """LlamaAttention.forward's attention (modeling_llama.py:1450-1483) as
+    per-element loops: query head h reads KV head h // (H / Hkv) (repeat_kv),
+    bf16(q.k), bf16(* scale), + mask, fp32 softmax cast to bf16, bf16(p.v)."""
+    from oracle.bf16 import round_bf16
+
+    def rnd(x):
+        return float(round_bf16(np.float64(x))) if bf16 else x
+    B, H, L, D = q.shape
+    Hkv, N = k.shape[1], k.shape[2]
+    rep = H // Hkv
+    out = np.zeros((B, H, L, D))
+    lse = np.zeros((B, H, L))
+    for b in range(B):
+        for h in range(H):
+            kv = h // rep
+            for i in range(L):
+                s = []
+                for n in range(N):
+                    dot = rnd(sum(q[b, h, i, d] * k[b, kv, n, d] for d in range(D)))
+                    x = rnd(dot * scale)
+                    s.append(x + (mask[b, 0, i, n] if mask is not None else 0.0))
+                m = max(s)
+                z = sum(math.exp(x - m) for x in s)
+                lse[b, h, i] = m + math.log(z)
+                p = [rnd(math.exp(x - m) / z) for x in s]
+                for d in range(D):
+                    out[b, h, i, d] = rnd(sum(p[n] * v[b, kv, n, d] for n in range(N)))
+    return out, lse
+
+
+@pytest.mark.parametrize('bf16', [False, True])
+def test_eager_recon_layer_matches_per_element_loops(bf16):
+    """The reconstruction-route oracle against explicit loops on a tiny GQA
+    case (3 query heads per KV head, a causal additive mask with one fully
+    visible and one partly visible query)."""
+    from oracle.bf16 import round_bf16
+    B, H, Hkv, L, N, D = 2, 6, 2, 2, 5, 4
+    q, k, v = (np.asarray(round_bf16(rand(*s) * 2), np.float64) for s in ((B, H, L, D), (B, Hkv, N, D), (B, Hkv, N, D)))
+    mask = np.zeros((B, 1, L, N))
+    mask[:, :, 0, N - 1] = -1e30                      # bottom-right causal for L = 2
+    scale = 1 / math.sqrt(D)
+    got, lse = oa.eager_recon_layer(q, k, v, scale, mask, bf16_boundaries=bf16)
+    want, want_lse = _recon_loops(q, k, v, scale, mask, bf16)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(lse, want_lse, rtol=1e-12, atol=1e-12)
+
+
+def test_eager_recon_layer_without_rounding_equals_grouped_eager_forward():
+    """With the bf16 boundaries off the reconstruction route is plain GQA
+    attention: eager_forward over the same K/V (BSHD) to 1e-12, causal mask
+    included."""
+    B, H, Hkv, L, N, D = 2, 8, 2, 2, 9, 16
+    q, k, v = rand(B, H, L, D), rand(B, Hkv, N, D), rand(B, Hkv, N, D)
+    mask = np.zeros((B, 1, L, N))
+    mask[:, :, 0, N - 1] = -np.inf
+    got, lse = oa.eager_recon_layer(q, k, v, 0.37, mask, bf16_boundaries=False)
+    want, want_lse = oa.eager_forward(q.transpose(0, 2, 1, 3), k.transpose(0, 2, 1, 3), v.transpose(0, 2, 1, 3),
+                                      0.37, causal=True)
+    np.testing.assert_allclose(got, want.transpose(0, 2, 1, 3), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(lse, want_lse, rtol=1e-12, atol=1e-12)

@@ -86,6 +86,35 @@ def test_llama3_frequency_smoothing_regions():
     assert mid.any() and (scaled[mid] < base[mid]).all() and (scaled[mid] > base[mid] / 8.0).all()
 
 
+@pytest.mark.parametrize('base_theta,factor,orig,low_f,high_f', [
+    (500000.0, 8.0, 8192, 1.0, 4.0),      # Llama-3.1 rope_scaling
+    (10000.0, 4.0, 2048, 1.0, 8.0),       # a wider mid band at another base
+])
+def test_llama3_mid_band_matches_closed_form(base_theta, factor, orig, low_f, high_f):
+    """Every mid-band entry against the closed form in float64: with
+    s = (orig / wavelen - low) / (high - low), f' = f * ((1 - s) / factor + s).
+    The interpolation weight tends to 1 at the high-frequency edge (f' -> f)
+    and to 0 at the low-frequency edge (f' -> f / factor); a swapped s / 1 - s
+    or a wrong factor moves every mid-band value by far more than fp32 ulps."""
+    base = rope.inv_freq(128, base_theta).astype(np.float64)
+    scaled = rope.llama3_inv_freq(128, base_theta, factor, orig, low_f, high_f).astype(np.float64)
+    wavelen = 2 * math.pi / base
+    mid = (wavelen >= orig / high_f) & (wavelen <= orig / low_f)
+    assert mid.sum() >= 3
+    s = (orig / wavelen[mid] - low_f) / (high_f - low_f)
+    assert ((s >= 0) & (s <= 1)).all()
+    expected = base[mid] * ((1 - s) / factor + s)
+    np.testing.assert_allclose(scaled[mid], expected, rtol=1e-6, atol=0)
+    # monotone in the weight: the ratio f'/f falls from ~1 to ~1/factor across the band
+    ratio = scaled[mid] / base[mid]
+    assert (np.diff(ratio) <= 1e-7).all()
+    np.testing.assert_allclose(ratio, (1 - s) / factor + s, rtol=1e-6)
+    # the band edges of the piecewise rule continue the two outer regions
+    edge_hi = (orig / (orig / high_f) - low_f) / (high_f - low_f)
+    edge_lo = (orig / (orig / low_f) - low_f) / (high_f - low_f)
+    assert edge_hi == 1.0 and edge_lo == 0.0
+
+
 def test_decode_key_positions_rule():
     # slots: 2 sinks, 3 tail slots with window raw indices [0, 1, 3], current token
     pos = rope.decode_key_positions(6, 2, 10, [0, 1, 3], 99)
