@@ -133,12 +133,12 @@ def make_layer(torch, device, rank, seed, cos, sin):
                 lse=torch.empty(B, HQ, 1, dtype=torch.float32, device=device))
 
 
-def run_layer(kernels, L, rows, scale, workspace):
+def run_layer(kernels, L, rows, scale, workspace, stages=7):
     """One layer's fused decode; `rows` = the step's RoPE rows at the query
     positions (kernels.query_rope_rows), shared by every layer of the step."""
     kernels.latent_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'], scale,
                           block_diagonal=True, cos=rows[0], sin=rows[1],
-                          out=L['out'], lse=L['lse'], workspace=workspace)
+                          out=L['out'], lse=L['lse'], workspace=workspace, stages=stages)
 
 
 def cpu_baseline(torch, layer, cos, sin, scale, budget_s=(10.0, 30.0)):
@@ -254,37 +254,36 @@ def main():
     print(f'bench: sweep {ms_per_step:.3f} ms, {gbps:.1f} GB/s', file=sys.stderr, flush=True)
     replay_ms = replay_median_ms(torch, step, REPLAYS)
 
-    # Split-K kernel alone.  With the library's split-only switch a decode call
-    # launches just its split kernel (reading the query operands the sweep left
-    # in the workspace; outputs not used).  The layers of one rank -- each with
+    # Split-K kernel alone, through the library's staged entry point: every
+    # layer's prologue stage runs once into a workspace of its own, then the
+    # attend stages (the split kernel, full work over the layer's own latent and
+    # raw rows and its own query operands) of one rank's layers -- each with
     # its own buffers, so the cache holds none of them -- are captured back to
     # back in one graph and timed with HIP events over PROFILE_REPLAYS replays:
     # the per-launch average includes the hand-off between launches, as the
     # kernel trace does, and no per-launch event cost.
-    lib = _lib.lib()
-    sweep()
+    from slimkv_amd._lib import STAGE_ATTEND, STAGE_PROLOGUE
+    stage_ws = [torch.empty(ws_bytes, dtype=torch.uint8, device=device) for _ in layers]
+    rows = kernels.query_rope_rows(cos, sin, step_pos)
+    for L, w in zip(layers, stage_ws):
+        run_layer(kernels, L, rows, scale, w, stages=STAGE_PROLOGUE)
     torch.cuda.synchronize()
     durations = {}
-    rows = kernels.query_rope_rows(cos, sin, step_pos)     # unused by split-only calls
     for r in sorted(set(ranks)):
-        group = [L for L in layers if L['rank'] == r]
+        group = [(L, w) for L, w in zip(layers, stage_ws) if L['rank'] == r]
 
         def split_sweep():
-            for L in group:
-                run_layer(kernels, L, rows, scale, workspace)
-        _lib.check(lib.slimkv_set_profile_split_only(1))
-        try:
+            for L, w in group:
+                run_layer(kernels, L, rows, scale, w, stages=STAGE_ATTEND)
+        split_sweep()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
             split_sweep()
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                split_sweep()
-            torch.cuda.current_stream().wait_stream(side)
-            split_graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(split_graph):
-                split_sweep()
-        finally:
-            _lib.check(lib.slimkv_set_profile_split_only(0))
+        torch.cuda.current_stream().wait_stream(side)
+        split_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(split_graph):
+            split_sweep()
         for _ in range(3):
             split_graph.replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -295,6 +294,7 @@ def main():
         b.record()
         torch.cuda.synchronize()
         durations[r] = [a.elapsed_time(b) * 1e-3 / (PROFILE_REPLAYS * len(group))]
+    del stage_ws
     dom = 32 if 32 in durations else max(durations, key=lambda r: len(durations[r]))
     dur = durations[dom]
     dur_avg = sum(dur) / len(dur)

@@ -32,21 +32,22 @@ const char* slimkv_last_error(void);
 /* ABI version of this header (bumped on any struct change). */
 int slimkv_abi_version(void);
 
-/* Measurement hook (no counterpart in the reference, whose benchmark attributes
- * kernels with torch.profiler scopes, tools/benchmark/benchmark_context_decode.py:186-289).
- * While set on the calling thread, every entry point records `before` (a
- * hipEvent_t) on its stream immediately before its split-K attention kernel and
- * `after` immediately after it, so a caller can time that kernel alone with
- * HIP events.  Pass NULL, NULL to clear. */
-int slimkv_set_profile_events(void* before, void* after);
-
-/* Measurement hook (no counterpart in the reference): while on (nonzero) on
- * the calling thread, slimkv_latent_decode and slimkv_paged_latent_decode
- * launch only their split-K attention kernel, reading the query operands an
- * earlier call left in the same workspace, and skip the query prologue and
- * the combine: their outputs are then not valid.  For timing that kernel
- * alone over many layers back to back.  Pass 0 to restore normal calls. */
-int slimkv_set_profile_split_only(int on);
+/* Stages of a decode call, for the *_stages entry points (bit mask).  A
+ * decode runs three kernels that hand over through the caller's workspace:
+ *   SLIMKV_STAGE_PROLOGUE  query RoPE (and, for the latent decode, the query
+ *                          absorption into U_K and the K-bias LSE shift);
+ *   SLIMKV_STAGE_ATTEND    the split-K attention: per-split partials;
+ *   SLIMKV_STAGE_COMBINE   the LSE merge of the partials, the V lift, out/lse.
+ * A *_stages call runs the selected stages in that order.  Calls with the
+ * same arguments and workspace that together run every stage once, in order,
+ * write exactly what one full call writes.  No counterpart in the reference,
+ * whose decode runs as one sequence of launches (slimkv/llama3/fa2_decode.py:
+ * 143-164); callers use it to place the stages themselves, e.g. to time the
+ * attention kernel of many layers back to back. */
+#define SLIMKV_STAGE_PROLOGUE 1
+#define SLIMKV_STAGE_ATTEND 2
+#define SLIMKV_STAGE_COMBINE 4
+#define SLIMKV_STAGE_ALL 7
 
 /* ------------------------------------------------------------------------
  * Split-K decode attention with GQA, bottom-right causality and LSE.
@@ -137,6 +138,9 @@ typedef struct slimkv_latent_decode_args {
 size_t slimkv_latent_decode_workspace(const slimkv_latent_decode_args* a);
 int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
                          size_t workspace_bytes, void* stream);
+/* slimkv_latent_decode restricted to `stages` (SLIMKV_STAGE_*). */
+int slimkv_latent_decode_stages(const slimkv_latent_decode_args* a, int stages, void* workspace,
+                                size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Paged latent decode: slimkv_latent_decode with the beacon rows read straight
@@ -167,6 +171,9 @@ typedef struct slimkv_paged_latent_decode_args {
 size_t slimkv_paged_latent_decode_workspace(const slimkv_paged_latent_decode_args* a);
 int slimkv_paged_latent_decode(const slimkv_paged_latent_decode_args* a, void* workspace,
                                size_t workspace_bytes, void* stream);
+/* slimkv_paged_latent_decode restricted to `stages` (SLIMKV_STAGE_*). */
+int slimkv_paged_latent_decode_stages(const slimkv_paged_latent_decode_args* a, int stages, void* workspace,
+                                      size_t workspace_bytes, void* stream);
 
 /* One-time re-layout of block-diagonal K bases for slimkv_latent_decode (no
  * counterpart in the reference, whose project_query reads U_K as stored,
@@ -237,6 +244,11 @@ int slimkv_prepare_rope_pairs(const float* cos, const float* sin, int64_t rows, 
 
 size_t slimkv_recon_decode_workspace(const slimkv_recon_decode_args* a);
 int slimkv_recon_decode(const slimkv_recon_decode_args* a, void* workspace, size_t workspace_bytes, void* stream);
+/* slimkv_recon_decode restricted to `stages` (SLIMKV_STAGE_*): the prologue
+ * rotates the query; the attend stage rebuilds what the route rebuilds and
+ * runs the split kernel. */
+int slimkv_recon_decode_stages(const slimkv_recon_decode_args* a, int stages, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Decode RoPE of the query and the raw K cache, bf16-exact.

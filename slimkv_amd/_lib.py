@@ -166,20 +166,24 @@ RawPagesArgs = _struct('slimkv_raw_pages_args', [
 SIGNATURES = {
     'slimkv_last_error': (ctypes.c_char_p, []),
     'slimkv_abi_version': (ctypes.c_int, []),
-    'slimkv_set_profile_events': (ctypes.c_int, [c_ptr, c_ptr]),
-    'slimkv_set_profile_split_only': (ctypes.c_int, [ctypes.c_int]),
     'slimkv_attention_workspace': (ctypes.c_size_t, [ctypes.POINTER(AttentionArgs)]),
     'slimkv_attention_forward': (ctypes.c_int, [ctypes.POINTER(AttentionArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(LatentDecodeArgs)]),
     'slimkv_latent_decode': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_latent_decode_stages': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), ctypes.c_int, c_ptr,
+                                                   ctypes.c_size_t, c_ptr]),
     'slimkv_paged_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(PagedLatentDecodeArgs)]),
     'slimkv_paged_latent_decode': (ctypes.c_int, [ctypes.POINTER(PagedLatentDecodeArgs), c_ptr, ctypes.c_size_t,
                                                   c_ptr]),
+    'slimkv_paged_latent_decode_stages': (ctypes.c_int, [ctypes.POINTER(PagedLatentDecodeArgs), ctypes.c_int, c_ptr,
+                                                         ctypes.c_size_t, c_ptr]),
     'slimkv_prepare_latent_bases': (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
     'slimkv_prepare_rope_pairs': (ctypes.c_int, [c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr]),
     'slimkv_reconstruct': (ctypes.c_int, [ctypes.POINTER(ReconstructArgs), c_ptr]),
     'slimkv_recon_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(ReconDecodeArgs)]),
     'slimkv_recon_decode': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_recon_decode_stages': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), ctypes.c_int, c_ptr,
+                                                  ctypes.c_size_t, c_ptr]),
     'slimkv_rope_decode': (ctypes.c_int, [ctypes.POINTER(RopeDecodeArgs), c_ptr]),
     'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
     'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),
@@ -192,7 +196,9 @@ SIGNATURES = {
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
+
+STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 
 
 class SlimKVError(RuntimeError):

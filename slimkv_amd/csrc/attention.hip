@@ -102,6 +102,7 @@ __device__ __forceinline__ u32x4 zero_unless(bool ok, u32x4 v) {
     return u32x4{ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
 }
 
+
 // The RoPE table values one lane needs for a head_dim-128 query row held as
 // MFMA operand pieces (elements 32c + 8*grp + [0, 8), c = 0..3).
 struct RopeRow {
@@ -313,7 +314,7 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
 // never exchange data, and write their own partials.
 // PAGED: 0 dense rows, 1 rows through per-lane page ids, 2 rows through the
 // tile's two pages (pages of at least 16 rows).
-template <int KS, bool PIPE, int PAGED = 0>
+template <int KS, int DEPTH, int PAGED = 0>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int Hq,
                                               float scale_log2, char* lds) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
@@ -372,9 +373,18 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         Nb = sl < 0 ? 0 : (sl < sg.n ? sl : sg.n);
     }
     const int lim = !colv ? 0 : (sg.causal ? Nb - Lq + lq + 1 : Nb);
-    const int r_begin = s * sg.rows_per_split;
-    const int r_end = min(r_begin + sg.rows_per_split, Nb);
-    const int ntile = r_end > r_begin ? (r_end - r_begin + 15) / 16 : 0;
+    // Striped splits: the sequence's 16-row tiles are dealt round-robin over
+    // its ceil(Nb / rows_per_split) non-empty splits, so split s takes tiles
+    // s, s + S, s + 2S, ...  The workgroups resident at one time then read one
+    // contiguous window of each sequence's rows instead of a separate stream
+    // per split (far fewer DRAM rows open per channel); a split still owns a
+    // fixed tile set, so results do not depend on scheduling.
+    const int S = max(1, (Nb + sg.rows_per_split - 1) / sg.rows_per_split);
+    const int tiles_b = (Nb + 15) / 16;
+    const int ntile = s < S ? (tiles_b - s + S - 1) / S : 0;   // S <= tiles_b; splits past S are empty
+    const int r_begin = 16 * s;               // first row of the split's first tile
+    const int r_step = 16 * S;
+    const int r_end = Nb;
     const int vis = min(lim, r_end);
     const int last_row = sg.n - 1;
 
@@ -383,7 +393,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
 
     auto fetch = [&](TileRegs<KS>& tr, int it) {
         const bool act = it < ntile;
-        const int r0 = act ? r_begin + it * 16 : r_begin;
+        const int r0 = act ? r_begin + it * r_step : r_begin;
         load_tile<KS>(tr, kbase, vbase, sg.k_sn, sg.v_sn, r0, act ? r_end : r_begin, last_row, span_k, span_v,
                       col, grp, lane, act);
     };
@@ -396,7 +406,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
     };
     const int last_page = PAGED == 2 ? last_valid / sg.slots : 0;
     auto load_pages = [&](auto& pg, int it) {
-        const int r0 = it < ntile ? r_begin + it * 16 : r_begin;
+        const int r0 = it < ntile ? r_begin + it * r_step : r_begin;
         if constexpr (PAGED == 2) {
             const int r0c = __builtin_amdgcn_readfirstlane(min(r0, last_valid));
             const int pi = __builtin_amdgcn_readfirstlane(r0c / sg.slots);
@@ -415,7 +425,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
     };
     auto fetch_paged = [&](TileRegs<KS>& tr, const auto& pg, int it) {
         const bool act = it < ntile;
-        const int r0 = act ? r_begin + it * 16 : r_begin;
+        const int r0 = act ? r_begin + it * r_step : r_begin;
         if constexpr (PAGED == 2)
             load_tile_pair<KS>(tr, pg, sg, kbase, vbase, r0, act ? r_end : r_begin, last_valid, span_k, span_v, col,
                                grp, lane, act);
@@ -459,7 +469,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
 
     // One 16-key tile: V to LDS, scores, online softmax, P^T V^T.
     auto consume = [&](const TileRegs<KS>& tile, int it) {
-        const int r0 = r_begin + it * 16;
+        const int r0 = r_begin + it * r_step;
         uint16_t* vb = vbuf + (it & 1) * 16 * RS;
 #pragma unroll
         for (int c = 0; c < VT / 2; ++c) {
@@ -526,18 +536,23 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
             load_pages(pcur, it + 4);
             consume(other, it + 1);
         }
-    } else if constexpr (PIPE) {
-        // Ping-pong between two register sets so a tile's loads stay in flight
-        // while the previous tile is consumed (no register copy on the back
-        // edge).  Loads past the last tile are issued anyway (clamped, zeroed)
-        // to keep the outstanding-load count uniform.
-        TileRegs<KS> other;
-        for (int it = 0; it < ntile; it += 2) {
-            fetch(other, it + 1);
-            consume(cur, it);
-            if (it + 1 >= ntile) break;
-            fetch(cur, it + 2);
-            consume(other, it + 1);
+    } else if constexpr (DEPTH > 1) {
+        // A ring of DEPTH register tiles: the loads of the next DEPTH - 1
+        // tiles stay in flight while a tile is consumed (the ring index is
+        // static in the unrolled body, so no register copies).  Loads past the
+        // last tile are issued anyway (clamped, zeroed) to keep the
+        // outstanding-load count uniform.
+        TileRegs<KS> ring[DEPTH];
+        ring[0] = cur;
+#pragma unroll
+        for (int d = 1; d < DEPTH - 1; ++d) fetch(ring[d], d);
+        for (int it = 0; it < ntile; it += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                fetch(ring[(d + DEPTH - 1) % DEPTH], it + d + DEPTH - 1);
+                consume(ring[d], it + d);
+                if (it + d + 1 >= ntile) break;
+            }
         }
     } else {
         for (int it = 0; it < ntile; ++it) {
@@ -581,6 +596,12 @@ struct SplitWaves {
     static constexpr int value = KA <= 4 ? 4 : (KA <= 6 ? 3 : 1);
 };
 
+// Register tiles in flight per latent wave (2 = ping-pong).
+template <int KA>
+struct SplitDepth {
+    static constexpr int value = 2;
+};
+
 template <int KA, int KB, int PAGED = 0>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SplitWaves<KA>::value)))
 split_kernel(SplitParams prm) {
@@ -590,12 +611,12 @@ split_kernel(SplitParams prm) {
     int w = blockIdx.x;
     if constexpr (KB > 0) {
         if (w < prm.seg[1].nwg) {
-            split_segment<KB, false>(prm.seg[1], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+            split_segment<KB, 1>(prm.seg[1], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
             return;
         }
         w -= prm.seg[1].nwg;
     }
-    split_segment<KA, true, PAGED>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+    split_segment<KA, SplitDepth<KA>::value, PAGED>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -668,9 +689,18 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         Nb = sl < 0 ? 0 : (sl < sg.n ? sl : sg.n);
     }
     const int lim = !colv ? 0 : (sg.causal ? Nb - Lq + lq + 1 : Nb);
-    const int r_begin = s * sg.rows_per_split;
-    const int r_end = min(r_begin + sg.rows_per_split, Nb);
-    const int ntile = r_end > r_begin ? (r_end - r_begin + 15) / 16 : 0;
+    // Striped splits: the sequence's 16-row tiles are dealt round-robin over
+    // its ceil(Nb / rows_per_split) non-empty splits, so split s takes tiles
+    // s, s + S, s + 2S, ...  The workgroups resident at one time then read one
+    // contiguous window of each sequence's rows instead of a separate stream
+    // per split (far fewer DRAM rows open per channel); a split still owns a
+    // fixed tile set, so results do not depend on scheduling.
+    const int S = max(1, (Nb + sg.rows_per_split - 1) / sg.rows_per_split);
+    const int tiles_b = (Nb + 15) / 16;
+    const int ntile = s < S ? (tiles_b - s + S - 1) / S : 0;   // S <= tiles_b; splits past S are empty
+    const int r_begin = 16 * s;               // first row of the split's first tile
+    const int r_step = 16 * S;
+    const int r_end = Nb;
     const int vis = min(lim, r_end);
     const int last_row = sg.n - 1;
 
@@ -683,7 +713,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
     // split are masked in the scores and their V rows are zeroed on the way
     // to LDS, where the tile is used.
     auto fetch = [&](ReconTile<KSR, VL>& t, int it) {
-        const int r0 = it < ntile ? r_begin + it * 16 : r_begin;
+        const int r0 = it < ntile ? r_begin + it * r_step : r_begin;
         const uint16_t* src = kbase + (int64_t)min(r0 + col, last_row) * sg.lk_sn;
 #pragma unroll
         for (int ks = 0; ks < KSR; ++ks) t.k[ks] = *reinterpret_cast<const u32x2*>(src + 16 * ks);
@@ -747,7 +777,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
     uint16_t* vbuf = reinterpret_cast<uint16_t*>(lds) + wave * 2 * 16 * RSV;
 
     auto consume = [&](const ReconTile<KSR, VL>& t, const u32x4 (&cs)[4], int it) {
-        const int r0 = r_begin + it * 16;
+        const int r0 = r_begin + it * r_step;
         const int re = it < ntile ? r_end : r_begin;
         uint16_t* vb = vbuf + (it & 1) * 16 * RSV;
 #pragma unroll
@@ -1495,11 +1525,7 @@ prologue_mfma_kernel(PrologueParams pp) {
 namespace {
 
 thread_local std::string g_error;
-thread_local hipEvent_t g_before = nullptr;
-thread_local int g_split_only = 0;          // latent decode: launch only the split kernel
-thread_local hipEvent_t g_after = nullptr;
 
-// Launch the split kernel bracketed by the caller's profiling events, if set.
 hipError_t dispatch_split(int ka, int kb, const struct SplitParams& prm, int grid, hipStream_t st);
 template <int MODE>
 hipError_t launch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
@@ -1518,14 +1544,8 @@ hipError_t dispatch_split_paged(int ka, const SplitParams& prm, int grid, hipStr
     return prm.seg[0].slots >= 16 ? launch_split_paged<2>(ka, prm, grid, st) : launch_split_paged<1>(ka, prm, grid, st);
 }
 
-hipError_t timed_split(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st, bool paged = false) {
-    if (g_before) {
-        hipError_t e = hipEventRecord(g_before, st);
-        if (e != hipSuccess) return e;
-    }
-    hipError_t e = paged ? dispatch_split_paged(ka, prm, grid, st) : dispatch_split(ka, kb, prm, grid, st);
-    if (e == hipSuccess && g_after) e = hipEventRecord(g_after, st);
-    return e;
+hipError_t launch_split_any(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st, bool paged = false) {
+    return paged ? dispatch_split_paged(ka, prm, grid, st) : dispatch_split(ka, kb, prm, grid, st);
 }
 
 int round_even_tile(int width) {
@@ -1696,19 +1716,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 5; }
-
-extern "C" int slimkv_set_profile_events(void* before, void* after) {
-    if ((before == nullptr) != (after == nullptr)) return fail(SLIMKV_EINVAL, "set both events or neither");
-    g_before = static_cast<hipEvent_t>(before);
-    g_after = static_cast<hipEvent_t>(after);
-    return SLIMKV_OK;
-}
-
-extern "C" int slimkv_set_profile_split_only(int on) {
-    g_split_only = on ? 1 : 0;
-    return SLIMKV_OK;
-}
+extern "C" int slimkv_abi_version(void) { return 6; }
 
 extern "C" size_t slimkv_attention_workspace(const slimkv_attention_args* a) {
     AttnPlan plan{};
@@ -1750,7 +1758,7 @@ extern "C" int slimkv_attention_forward(const slimkv_attention_args* a, void* wo
     sg.wown = (int)a->width_v;
     sg.nwg = plan.sp.nwg;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    rc = check_hip(timed_split(plan.sp.ks, 0, prm, sg.nwg, st), "split kernel launch");
+    rc = check_hip(launch_split_any(plan.sp.ks, 0, prm, sg.nwg, st), "split kernel launch");
     if (rc != SLIMKV_OK) return rc;
     CombineParams cp{};
     cp.a_ml = sg.part_ml; cp.a_acc = sg.part_acc; cp.a_splits = sg.splits; cp.a_w = sg.wown;
@@ -1921,10 +1929,20 @@ extern "C" size_t slimkv_latent_decode_workspace(const slimkv_latent_decode_args
 
 namespace {
 
+int check_stages(int stages) {
+    if (stages <= 0 || stages > SLIMKV_STAGE_ALL) return fail(SLIMKV_EINVAL, "stages must be a nonempty mask of SLIMKV_STAGE_*");
+    return SLIMKV_OK;
+}
+
+// Prologue (query RoPE + absorption into the workspace), split-K attention
+// (partials into the workspace), combine (merge + V lift into the output):
+// the stages in `stages` run in that order and hand over through the workspace.
 int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, void* workspace,
-                      size_t workspace_bytes, void* stream) {
+                      size_t workspace_bytes, void* stream, int stages = SLIMKV_STAGE_ALL) {
+    int rc = check_stages(stages);
+    if (rc != SLIMKV_OK) return rc;
     LatentPlan p{};
-    int rc = plan_latent(a, &p, pg);
+    rc = plan_latent(a, &p, pg);
     if (rc != SLIMKV_OK) return rc;
     if (!workspace || workspace_bytes < p.total) return fail(SLIMKV_EWORKSPACE, "workspace too small");
     char* ws = static_cast<char*>(workspace);
@@ -1957,8 +1975,8 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     const bool mfma_prologue = has_lat && bd && pp.ut && pp.wq % 16 == 0 && nct >= 1 && nct <= 3 &&
                                g * Lq <= 16 && ptr_aligned16(pp.ut) && ptr_aligned16(a->q) &&
                                (!a->up_k_bias || ptr_aligned16(a->up_k_bias));
-    if (g_split_only) {
-        // measurement: the query operands an earlier call left in the workspace
+    if (!(stages & SLIMKV_STAGE_PROLOGUE)) {
+        // the query operands of an earlier prologue stage are in the workspace
     } else if (mfma_prologue) {
         if (nct == 1) hipLaunchKernelGGL(prologue_mfma_kernel<1>, dim3(B * Hkv), dim3(64), 0, st, pp);
         else if (nct == 2) hipLaunchKernelGGL(prologue_mfma_kernel<2>, dim3(B * Hkv), dim3(64), 0, st, pp);
@@ -2019,9 +2037,11 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     const bool paged = pg && has_lat;
     if (paged && ka > 8) return fail(SLIMKV_EUNSUP, "paged decode handles latent tiles up to 128 wide");
     const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
-    rc = check_hip(timed_split(ka, kb, prm, grid, st, paged), "split kernel launch");
-    if (rc != SLIMKV_OK) return rc;
-    if (g_split_only) return SLIMKV_OK;
+    if (stages & SLIMKV_STAGE_ATTEND) {
+        rc = check_hip(launch_split_any(ka, kb, prm, grid, st, paged), "split kernel launch");
+        if (rc != SLIMKV_OK) return rc;
+    }
+    if (!(stages & SLIMKV_STAGE_COMBINE)) return SLIMKV_OK;
 
     CombineParams cp{};
     cp.a_ml = r.part_ml; cp.a_acc = r.part_acc; cp.a_splits = r.splits; cp.a_w = D;
@@ -2055,6 +2075,12 @@ extern "C" int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* wo
     return latent_decode_run(a, nullptr, workspace, workspace_bytes, stream);
 }
 
+extern "C" int slimkv_latent_decode_stages(const slimkv_latent_decode_args* a, int stages, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+    return latent_decode_run(a, nullptr, workspace, workspace_bytes, stream, stages);
+}
+
+
 extern "C" size_t slimkv_paged_latent_decode_workspace(const slimkv_paged_latent_decode_args* a) {
     if (!a) return 0;
     const PagedRows pg = paged_rows(a);
@@ -2068,6 +2094,13 @@ extern "C" int slimkv_paged_latent_decode(const slimkv_paged_latent_decode_args*
     if (!a) return fail(SLIMKV_EINVAL, "null arguments");
     const PagedRows pg = paged_rows(a);
     return latent_decode_run(&a->base, &pg, workspace, workspace_bytes, stream);
+}
+
+extern "C" int slimkv_paged_latent_decode_stages(const slimkv_paged_latent_decode_args* a, int stages,
+                                                 void* workspace, size_t workspace_bytes, void* stream) {
+    if (!a) return fail(SLIMKV_EINVAL, "null arguments");
+    const PagedRows pg = paged_rows(a);
+    return latent_decode_run(&a->base, &pg, workspace, workspace_bytes, stream, stages);
 }
 
 // ---------------------------------------------------------------------------
@@ -2192,7 +2225,8 @@ int recon_occupancy(int ksr, int vl) {
 
 // Raw rows and rebuilt-per-tile beacon rows in one launch, then the combine
 // with the latent V lift.  q_rot already holds the rotated queries.
-int recon_fused_run(const slimkv_recon_decode_args* r, const ReconPlan& p, char* ws, uint16_t* q_rot, hipStream_t st) {
+int recon_fused_run(const slimkv_recon_decode_args* r, const ReconPlan& p, char* ws, uint16_t* q_rot, hipStream_t st,
+                    int stages) {
     const slimkv_latent_decode_args* a = &r->base;
     const int B = (int)a->batch, Lq = (int)a->queries, Hq = (int)a->heads, Hkv = (int)a->kv_heads, D = (int)a->head_dim;
     const int g = Hq / Hkv;
@@ -2225,23 +2259,19 @@ int recon_fused_run(const slimkv_recon_decode_args* r, const ReconPlan& p, char*
     bs.part_ml = reinterpret_cast<float*>(ws + p.bml_off); bs.part_acc = reinterpret_cast<float*>(ws + p.bacc_off);
 
     const int grid = rs.nwg + bs.nwg;
-    if (g_before) {
-        const hipError_t e = hipEventRecord(g_before, st);
-        if (e != hipSuccess) return check_hip(e, "profile event");
-    }
+    int rc = SLIMKV_OK;
+    if (stages & SLIMKV_STAGE_ATTEND) {
 #define SLIMKV_LAUNCH(K, V)                                                                                       \
     if (p.ksr == K && p.vl == V) {                                                                                \
         if (bs.pairs) hipLaunchKernelGGL((recon_split_kernel<K, V, true>), dim3(grid), dim3(kThreads), 0, st, prm, bs); \
         else hipLaunchKernelGGL((recon_split_kernel<K, V, false>), dim3(grid), dim3(kThreads), 0, st, prm, bs);       \
     }
-    SLIMKV_LAUNCH(1, 1) SLIMKV_LAUNCH(2, 1) SLIMKV_LAUNCH(3, 1) SLIMKV_LAUNCH(1, 2) SLIMKV_LAUNCH(2, 2)
+        SLIMKV_LAUNCH(1, 1) SLIMKV_LAUNCH(2, 1) SLIMKV_LAUNCH(3, 1) SLIMKV_LAUNCH(1, 2) SLIMKV_LAUNCH(2, 2)
 #undef SLIMKV_LAUNCH
-    int rc = check_hip(hipGetLastError(), "reconstruction split kernel launch");
-    if (rc != SLIMKV_OK) return rc;
-    if (g_after) {
-        rc = check_hip(hipEventRecord(g_after, st), "profile event");
+        rc = check_hip(hipGetLastError(), "reconstruction split kernel launch");
         if (rc != SLIMKV_OK) return rc;
     }
+    if (!(stages & SLIMKV_STAGE_COMBINE)) return SLIMKV_OK;
 
     CombineParams cp{};
     cp.a_ml = rs.part_ml; cp.a_acc = rs.part_acc; cp.a_splits = rs.splits; cp.a_w = D;
@@ -2264,11 +2294,15 @@ extern "C" size_t slimkv_recon_decode_workspace(const slimkv_recon_decode_args* 
     return p.total;
 }
 
-extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+namespace {
+
+int recon_decode_run(const slimkv_recon_decode_args* r, void* workspace, size_t workspace_bytes, void* stream,
+                     int stages) {
     if (!r) return fail(SLIMKV_EINVAL, "null arguments");
+    int rc = check_stages(stages);
+    if (rc != SLIMKV_OK) return rc;
     ReconPlan p{};
-    int rc = plan_recon(r, &p);
+    rc = plan_recon(r, &p);
     if (rc != SLIMKV_OK) return rc;
     if (!workspace || workspace_bytes < p.total) return fail(SLIMKV_EWORKSPACE, "workspace too small");
     const slimkv_latent_decode_args* a = &r->base;
@@ -2290,14 +2324,16 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
     pp.wq = 0;
     pp.B = B; pp.Lq = Lq; pp.Hq = Hq; pp.Hkv = Hkv; pp.D = D; pp.Rk = (int)a->rank_k; pp.parts = 1;
     pp.scale = (float)a->scale;
-    hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
-    rc = check_hip(hipGetLastError(), "prologue kernel launch");
-    if (rc != SLIMKV_OK) return rc;
+    if (stages & SLIMKV_STAGE_PROLOGUE) {
+        hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
+        rc = check_hip(hipGetLastError(), "prologue kernel launch");
+        if (rc != SLIMKV_OK) return rc;
+    }
 
-    if (p.fused) return recon_fused_run(r, p, ws, q_rot, st);
+    if (p.fused) return recon_fused_run(r, p, ws, q_rot, st, stages);
 
     // 2. rebuild beacon K (optionally RoPE'd) and, unless it stays latent, V: [B, Nl, Hkv, D]
-    if (has_lat) {
+    if (has_lat && (stages & SLIMKV_STAGE_ATTEND)) {
         for (int kind = 0; kind < (p.v_latent ? 1 : 2); ++kind) {
             slimkv_reconstruct_args ra{};
             ra.latent = kind ? a->lat_v : a->lat_k;
@@ -2349,8 +2385,11 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
         bs.nwg = p.rec.nwg;
     }
     const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
-    rc = check_hip(timed_split(8, has_lat ? 8 : 0, prm, grid, st), "split kernel launch");
-    if (rc != SLIMKV_OK) return rc;
+    if (stages & SLIMKV_STAGE_ATTEND) {
+        rc = check_hip(launch_split_any(8, has_lat ? 8 : 0, prm, grid, st), "split kernel launch");
+        if (rc != SLIMKV_OK) return rc;
+    }
+    if (!(stages & SLIMKV_STAGE_COMBINE)) return SLIMKV_OK;
 
     // 4. merge the two segments
     CombineParams cp{};
@@ -2371,6 +2410,18 @@ extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* work
     cp.lse = a->lse;
     launch_combine(cp, B * Hq * Lq, st);
     return check_hip(hipGetLastError(), "combine kernel launch");
+}
+
+}  // namespace
+
+extern "C" int slimkv_recon_decode(const slimkv_recon_decode_args* r, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    return recon_decode_run(r, workspace, workspace_bytes, stream, SLIMKV_STAGE_ALL);
+}
+
+extern "C" int slimkv_recon_decode_stages(const slimkv_recon_decode_args* r, int stages, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    return recon_decode_run(r, workspace, workspace_bytes, stream, stages);
 }
 
 // ---------------------------------------------------------------------------

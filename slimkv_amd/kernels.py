@@ -267,7 +267,7 @@ def query_rope_rows(cos, sin, q_positions):
 def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias=None, up_v_bias=None,
                   block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
                   raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None,
-                  workspace=None, prepared_bases=True):
+                  workspace=None, prepared_bases=True, stages=_lib.STAGE_ALL):
     """Fused latent beacon decode for one layer.
 
     q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given;
@@ -278,7 +278,9 @@ def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias
     A caller-provided `workspace` (uint8, at least latent_decode_workspace_bytes)
     makes the call allocation-free, e.g. under HIP graph capture.  With
     block-diagonal bases the query absorption runs on MFMA from per-head bases
-    prepared once per weight (`prepared_bases`, the default).
+    prepared once per weight (`prepared_bases`, the default).  `stages`
+    (a mask of _lib.STAGE_*) runs part of the call; the stages of one decode
+    hand over through `workspace`, which is then required.
     """
     a, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
                                      block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
@@ -286,17 +288,28 @@ def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias
     nbytes = lib().slimkv_latent_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
-    if workspace is None or workspace.numel() < nbytes:
-        workspace = _workspace(nbytes, q.device)
-    check(lib().slimkv_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    workspace = _stage_workspace(workspace, nbytes, stages, q.device)
+    if stages == _lib.STAGE_ALL:
+        check(lib().slimkv_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    else:
+        check(lib().slimkv_latent_decode_stages(ctypes.byref(a), int(stages), _ptr(workspace), nbytes,
+                                                _lib.stream_handle(q.device)))
     del keep
     return out, lse
+
+
+def _stage_workspace(workspace, nbytes, stages, device):
+    if workspace is not None and workspace.numel() >= nbytes:
+        return workspace
+    if stages != _lib.STAGE_ALL:
+        raise ValueError('a partial-stage call needs the workspace its other stages use')
+    return _workspace(nbytes, device)
 
 
 def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, layout, up_k, up_v, scale, *,
                         rows_total=0, up_k_bias=None, up_v_bias=None, block_diagonal=False, lat_causal=False,
                         q_positions=None, cos=None, sin=None, raw_lengths=None, raw_splits=0, lat_splits=0,
-                        out=None, lse=None, workspace=None):
+                        out=None, lse=None, workspace=None, stages=_lib.STAGE_ALL):
     """latent_decode with the beacon rows read straight out of beacon pages.
 
     pages [num_pages, layout.page_elements] bf16 in BeaconPageLayout format;
@@ -323,9 +336,13 @@ def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, la
     nbytes = lib().slimkv_paged_latent_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
-    if workspace is None or workspace.numel() < nbytes:
-        workspace = _workspace(nbytes, q.device)
-    check(lib().slimkv_paged_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    workspace = _stage_workspace(workspace, nbytes, stages, q.device)
+    if stages == _lib.STAGE_ALL:
+        check(lib().slimkv_paged_latent_decode(ctypes.byref(a), _ptr(workspace), nbytes,
+                                               _lib.stream_handle(q.device)))
+    else:
+        check(lib().slimkv_paged_latent_decode_stages(ctypes.byref(a), int(stages), _ptr(workspace), nbytes,
+                                                      _lib.stream_handle(q.device)))
     del keep
     return out, lse
 
@@ -377,9 +394,11 @@ def reconstruct(latent, weight, bias=None, *, kv_heads, out=None, dst_rows=None,
 
 def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_positions=None, up_k_bias=None,
                  up_v_bias=None, block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
-                 raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None, workspace=None):
+                 raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None, workspace=None,
+                 stages=_lib.STAGE_ALL):
     """Reconstruction decode: rebuild beacon K (RoPE'd at beacon_positions
-    [B, Nl] when given) and V, then attend over [beacons ; raw rows]."""
+    [B, Nl] when given) and V, then attend over [beacons ; raw rows].
+    `stages` as latent_decode."""
     base, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
                                         block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
                                         lat_lengths, raw_splits, lat_splits, out, lse, prepared_bases=False)
@@ -396,9 +415,12 @@ def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_pos
     nbytes = lib().slimkv_recon_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
-    if workspace is None or workspace.numel() < nbytes:
-        workspace = _workspace(nbytes, q.device)
-    check(lib().slimkv_recon_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    workspace = _stage_workspace(workspace, nbytes, stages, q.device)
+    if stages == _lib.STAGE_ALL:
+        check(lib().slimkv_recon_decode(ctypes.byref(a), _ptr(workspace), nbytes, _lib.stream_handle(q.device)))
+    else:
+        check(lib().slimkv_recon_decode_stages(ctypes.byref(a), int(stages), _ptr(workspace), nbytes,
+                                               _lib.stream_handle(q.device)))
     del keep
     return out, lse
 

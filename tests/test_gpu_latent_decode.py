@@ -197,29 +197,35 @@ def test_rope_rows_without_positions_must_cover_every_query(device):
                               case.up_v, case.scale, block_diagonal=True, cos=case.cos[:2], sin=case.sin[:2])
 
 
-def test_split_only_measurement_switch(device):
-    """slimkv_set_profile_split_only: while on, a decode call launches only its
-    split kernel and leaves the output untouched; once off, calls are normal
-    again (bit-identical to a call made before)."""
+@pytest.mark.parametrize('block_diagonal', [True, False])
+def test_stages_in_separate_calls_equal_one_call(device, block_diagonal):
+    """slimkv_latent_decode_stages: the prologue, attend and combine stages run
+    as three calls over one workspace write exactly what one full call writes;
+    a call without the combine stage leaves the output untouched."""
     from slimkv_amd import _lib, kernels
     case = latent_case(batch=2, context=900, tail=40, seed=51, device=device)
     _, k_rot = _rotated(case)
     nbytes = kernels.latent_decode_workspace_bytes(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v,
-                                                   case.up_k, case.up_v, case.scale, block_diagonal=True,
+                                                   case.up_k, case.up_v, case.scale, block_diagonal=block_diagonal,
                                                    q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    want = _run(case, k_rot, block_diagonal)
     ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-    want = _run(case, k_rot, True, workspace=ws)
     out = torch.full_like(want[0], 7.0)
-    lib = _lib.lib()
-    _lib.check(lib.slimkv_set_profile_split_only(1))
-    try:
-        _run(case, k_rot, True, workspace=ws, out=out)
-    finally:
-        _lib.check(lib.slimkv_set_profile_split_only(0))
-    assert (out == 7.0).all()
-    got = _run(case, k_rot, True, workspace=ws)
-    assert torch.equal(got[0], want[0])
-    assert torch.equal(got[1], want[1])
+    lse = torch.full_like(want[1], 7.0)
+    _run(case, k_rot, block_diagonal, workspace=ws, out=out, lse=lse,
+         stages=_lib.STAGE_PROLOGUE | _lib.STAGE_ATTEND)
+    torch.cuda.synchronize()
+    assert (out == 7.0).all() and (lse == 7.0).all()
+    _run(case, k_rot, block_diagonal, workspace=ws, out=out, lse=lse, stages=_lib.STAGE_COMBINE)
+    assert torch.equal(out, want[0]) and torch.equal(lse, want[1])
+    ws.zero_()
+    for stage in (_lib.STAGE_PROLOGUE, _lib.STAGE_ATTEND, _lib.STAGE_COMBINE):
+        _run(case, k_rot, block_diagonal, workspace=ws, out=out, lse=lse, stages=stage)
+    assert torch.equal(out, want[0]) and torch.equal(lse, want[1])
+    with pytest.raises(ValueError, match='stages'):
+        _run(case, k_rot, block_diagonal, workspace=ws, stages=0)
+    with pytest.raises(ValueError, match='workspace'):
+        _run(case, k_rot, block_diagonal, stages=_lib.STAGE_ATTEND)
 
 
 @pytest.mark.parametrize('rank,queries', [(32, 1), (48, 1), (32, 2)])
