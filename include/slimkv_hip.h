@@ -142,6 +142,20 @@ int slimkv_latent_decode(const slimkv_latent_decode_args* a, void* workspace,
 int slimkv_latent_decode_stages(const slimkv_latent_decode_args* a, int stages, void* workspace,
                                 size_t workspace_bytes, void* stream);
 
+/* Allocation-free slimkv_latent_decode (no counterpart in the reference): for
+ * callers that cannot allocate -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  The workspace is a device array of
+ * SLIMKV_NOALLOC_SCRATCH_BYTES inside the library (one per GPU, held until the
+ * process ends), so the call allocates nothing; a call whose workspace
+ * (slimkv_latent_decode_workspace) would exceed it fails with
+ * SLIMKV_EWORKSPACE before launching anything.  The stream must belong to the
+ * current device.  Every call on one GPU uses that GPU's one array: calls that
+ * overlap on a GPU (other streams, other threads) race and must be ordered by
+ * the caller.  The array needs no clearing between calls.  Results equal
+ * slimkv_latent_decode's. */
+#define SLIMKV_NOALLOC_SCRATCH_BYTES (32u << 20)
+int slimkv_latent_decode_noalloc(const slimkv_latent_decode_args* a, void* stream);
+
 /* ------------------------------------------------------------------------
  * Paged latent decode: slimkv_latent_decode with the beacon rows read straight
  * out of beacon pages, no restore/gather step.  Replaces the page gather of

@@ -172,6 +172,7 @@ SIGNATURES = {
     'slimkv_latent_decode': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_latent_decode_stages': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), ctypes.c_int, c_ptr,
                                                    ctypes.c_size_t, c_ptr]),
+    'slimkv_latent_decode_noalloc': (ctypes.c_int, [ctypes.POINTER(LatentDecodeArgs), c_ptr]),
     'slimkv_paged_latent_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(PagedLatentDecodeArgs)]),
     'slimkv_paged_latent_decode': (ctypes.c_int, [ctypes.POINTER(PagedLatentDecodeArgs), c_ptr, ctypes.c_size_t,
                                                   c_ptr]),
@@ -199,6 +200,7 @@ SIGNATURES = {
 ABI_VERSION = 6
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
 class SlimKVError(RuntimeError):

@@ -2080,6 +2080,55 @@ extern "C" int slimkv_latent_decode_stages(const slimkv_latent_decode_args* a, i
     return latent_decode_run(a, nullptr, workspace, workspace_bytes, stream, stages);
 }
 
+// ---------------------------------------------------------------------------
+// allocation-free latent decode: the workspace is a file-scope device array
+// ---------------------------------------------------------------------------
+
+// One copy per GPU, allocated when the library's code object is loaded on that
+// GPU and held until the process ends.  In host code `scratch` names a
+// host-side stand-in: its device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) unsigned char scratch[SLIMKV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;   // device address of `scratch`, per device ordinal
+
+// The address of the current device's `scratch`, looked up once per device
+// with that device current.
+int scratch_address(void** out) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc != SLIMKV_OK) return rc;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (rc != SLIMKV_OK) return rc;
+        if (!p) return fail(SLIMKV_EHIP, "hipGetSymbolAddress(scratch) returned a null address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return SLIMKV_OK;
+}
+
+}  // namespace
+
+extern "C" int slimkv_latent_decode_noalloc(const slimkv_latent_decode_args* a, void* stream) {
+    LatentPlan p{};
+    int rc = plan_latent(a, &p);
+    if (rc != SLIMKV_OK) return rc;
+    if (p.total > (size_t)SLIMKV_NOALLOC_SCRATCH_BYTES)
+        return fail(SLIMKV_EWORKSPACE, "slimkv_latent_decode_noalloc: this call needs " + std::to_string(p.total) +
+                                           " bytes of workspace, more than the " +
+                                           std::to_string((size_t)SLIMKV_NOALLOC_SCRATCH_BYTES) +
+                                           "-byte device scratch; use slimkv_latent_decode with a caller workspace");
+    void* ws = nullptr;
+    rc = scratch_address(&ws);
+    if (rc != SLIMKV_OK) return rc;
+    return latent_decode_run(a, nullptr, ws, (size_t)SLIMKV_NOALLOC_SCRATCH_BYTES, stream);
+}
 
 extern "C" size_t slimkv_paged_latent_decode_workspace(const slimkv_paged_latent_decode_args* a) {
     if (!a) return 0;
