@@ -163,27 +163,47 @@ def _prefill_cpu(torch, q, k, v, n, scale, flops):
 
 # ----------------------------------------------------------------------------- reconstruction decode
 
+RECON_SHAPE = dict(B=8, HQ=40, HKV=8, D=128, NB=8192, S=4, T=128, r=32, CTX=32768)
+
+
+def recon_layer(torch, dev, seed):
+    """One reconstruction-decode layer at the Qwen2.5-14B shape (B8, 40/8
+    heads, 8192 beacons of rank 32 per head, 4 sinks + 128 tail + current
+    token); raw K stands in as already rotated."""
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+    c = RECON_SHAPE
+    B, HQ, HKV, D, NB, r = c['B'], c['HQ'], c['HKV'], c['D'], c['NB'], c['r']
+    RAW = c['S'] + c['T'] + 1
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    rnd = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(torch.bfloat16)
+    cpu = torch.Generator().manual_seed(seed + 50)
+    return dict(
+        q=rnd(B, 1, HQ, D), raw_k=rnd(B, RAW, HKV, D), raw_v=rnd(B, RAW, HKV, D),
+        lat_k=rnd(B, NB, HKV * r), lat_v=rnd(B, NB, HKV * r),
+        up_k=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+        up_v=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
+        out=torch.empty(B, 1, HQ, D, dtype=torch.bfloat16, device=dev))
+
+
+def recon_positions(torch, dev):
+    """(query positions [B, 1], beacon slot positions [B, NB]) of the workload."""
+    c = RECON_SHAPE
+    qpos = torch.full((c['B'], 1), c['CTX'], dtype=torch.long, device=dev)
+    bpos = (c['S'] + torch.arange(c['NB'], device=dev))[None].expand(c['B'], -1).contiguous()
+    return qpos, bpos
+
+
 def recon(args):
     import torch
     from slimkv_amd import kernels
-    from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
-    B, HQ, HKV, D, NB, S, T, r, LAYERS = 8, 40, 8, 128, 8192, 4, 128, 32, 8
-    R, RAW, CTX = HKV * r, S + T + 1, 32768
+    from slimkv_amd.workloads import rope_tables
+    c = RECON_SHAPE
+    B, HQ, HKV, D, NB, S, T, r, LAYERS = c['B'], c['HQ'], c['HKV'], c['D'], c['NB'], c['S'], c['T'], c['r'], 8
+    R, RAW, CTX = HKV * r, S + T + 1, c['CTX']
     dev = torch.device('cuda:0')
     cos, sin = rope_tables(CTX + 1, D, 500000.0, dev)
-    layers = []
-    for i in range(LAYERS):
-        gen = torch.Generator(device=dev).manual_seed(args.seed * 100 + i)
-        rnd = lambda *sh: torch.randn(*sh, generator=gen, device=dev).to(torch.bfloat16)
-        cpu = torch.Generator().manual_seed(args.seed * 100 + i + 50)
-        layers.append(dict(
-            q=rnd(B, 1, HQ, D), raw_k=rnd(B, RAW, HKV, D), raw_v=rnd(B, RAW, HKV, D),
-            lat_k=rnd(B, NB, R), lat_v=rnd(B, NB, R),
-            up_k=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
-            up_v=block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16),
-            out=torch.empty(B, 1, HQ, D, dtype=torch.bfloat16, device=dev)))
-    qpos = torch.full((B, 1), CTX, dtype=torch.long, device=dev)
-    bpos = (S + torch.arange(NB, device=dev))[None].expand(B, -1).contiguous()   # beacon slot positions
+    layers = [recon_layer(torch, dev, args.seed * 100 + i) for i in range(LAYERS)]
+    qpos, bpos = recon_positions(torch, dev)
     scale = D ** -0.5
 
     def step():
@@ -214,46 +234,65 @@ def recon(args):
 
 # ----------------------------------------------------------------------------- paged decode
 
-def paged(args):
+PAGED_SHAPE = dict(NSEQ=64, HQ=32, HKV=8, D=128, RATIO=8, S=4, r=32, POOL=400_000)
+
+
+def paged_case(torch, dev, seed):
+    """The paged workload's seeded draw: 64 sequences with contexts in
+    [1024, 131072] and tails in [0, 255], t8 beacon pages
+    BeaconPageLayout(16, 8, 256, 256, 1024) at a seeded random permutation of a
+    400K-page pool, raw pages of 16 tokens for sinks + tail + current token."""
     import random
-    import torch
-    from slimkv_amd import _lib, kernels
-    from slimkv_amd.paged_cache import BeaconPageLayout, BeaconPages, RawPages
-    from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
-    NSEQ, HQ, HKV, D, RATIO, S, r, POOL = 64, 32, 8, 128, 8, 4, 32, 400_000
+    from slimkv_amd.paged_cache import BeaconPageLayout
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+    c = PAGED_SHAPE
+    NSEQ, HQ, HKV, D, RATIO, S, r, POOL = (c[k] for k in ('NSEQ', 'HQ', 'HKV', 'D', 'RATIO', 'S', 'r', 'POOL'))
     R = HKV * r
-    rng = random.Random(args.seed)
+    rng = random.Random(seed)
     ctx = [rng.randint(1024, 131072) for _ in range(NSEQ)]
     tails = [rng.randint(0, 255) for _ in range(NSEQ)]
-    nb = [c // RATIO for c in ctx]
+    nb = [x // RATIO for x in ctx]
     layout = BeaconPageLayout(16, RATIO, R, R, HKV * D)
-    dev = torch.device('cuda:0')
     pool = torch.empty(POOL, layout.page_elements, dtype=torch.bfloat16, device=dev)
-    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    gen = torch.Generator(device=dev).manual_seed(seed)
     for i in range(0, POOL, 50_000):
         pool[i:i + 50_000].normal_(generator=gen)
     pages_needed = [(n + layout.slots - 1) // layout.slots for n in nb]
-    perm = torch.randperm(POOL, generator=torch.Generator().manual_seed(args.seed))
+    perm = torch.randperm(POOL, generator=torch.Generator().manual_seed(seed))
     width = max(pages_needed)
     tables = torch.full((NSEQ, width), 0, dtype=torch.long)
     off = 0
     for sidx, n in enumerate(pages_needed):
         tables[sidx, :n] = perm[off:off + n]
         off += n
-    tables = tables.to(dev)
     raw_count = [S + t + 1 for t in tails]                       # sinks + tail + current token
     raw_blocks = (max(raw_count) + 15) // 16
     raw_pool = torch.randn(NSEQ * raw_blocks, 16, 2, HKV, D, generator=gen, device=dev).to(torch.bfloat16)
-    raw_tables = torch.randperm(NSEQ * raw_blocks, generator=torch.Generator().manual_seed(args.seed + 1))
-    raw_tables = raw_tables.view(NSEQ, raw_blocks).to(dev)
-    beacons = BeaconPages(pool, layout)
-    raw = RawPages(raw_pool)
-    lat_len = torch.tensor(nb, dtype=torch.int32, device=dev)
-    raw_len = torch.tensor(raw_count, dtype=torch.int32, device=dev)
-    cpu = torch.Generator().manual_seed(args.seed + 2)
+    raw_tables = torch.randperm(NSEQ * raw_blocks, generator=torch.Generator().manual_seed(seed + 1))
+    cpu = torch.Generator().manual_seed(seed + 2)
     up_k = block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16)
     up_v = block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16)
     q = torch.randn(NSEQ, 1, HQ, D, generator=gen, device=dev).to(torch.bfloat16)
+    return dict(ctx=ctx, nb=nb, raw_count=raw_count, layout=layout, pool=pool, tables_cpu=tables,
+                tables=tables.to(dev), raw_pool=raw_pool, raw_tables=raw_tables.view(NSEQ, raw_blocks).to(dev),
+                lat_len=torch.tensor(nb, dtype=torch.int32, device=dev),
+                raw_len=torch.tensor(raw_count, dtype=torch.int32, device=dev), up_k=up_k, up_v=up_v, q=q)
+
+
+def paged(args):
+    import torch
+    from slimkv_amd import kernels
+    from slimkv_amd.paged_cache import BeaconPages, RawPages
+    c = PAGED_SHAPE
+    NSEQ, HQ, HKV, D, RATIO, S, r, POOL = (c[k] for k in ('NSEQ', 'HQ', 'HKV', 'D', 'RATIO', 'S', 'r', 'POOL'))
+    R = HKV * r
+    dev = torch.device('cuda:0')
+    pc = paged_case(torch, dev, args.seed)
+    nb, raw_count, layout, pool, tables = pc['nb'], pc['raw_count'], pc['layout'], pc['pool'], pc['tables']
+    raw_pool, raw_tables, lat_len, raw_len = pc['raw_pool'], pc['raw_tables'], pc['lat_len'], pc['raw_len']
+    up_k, up_v, q = pc['up_k'], pc['up_v'], pc['q']
+    beacons = BeaconPages(pool, layout)
+    raw = RawPages(raw_pool)
     out = torch.empty(NSEQ, 1, HQ, D, dtype=torch.bfloat16, device=dev)
     scale = D ** -0.5
     max_nb, max_raw = max(nb), max(raw_count)
@@ -261,13 +300,14 @@ def paged(args):
     lat_v = torch.zeros_like(lat_k)
     raw_k = torch.zeros(NSEQ, HKV, max_raw, D, dtype=torch.bfloat16, device=dev)
     raw_v = torch.zeros_like(raw_k)
-    lib = _lib.lib()
-    split_ev = _events(torch)
+    # block-table index errors land here and are checked once after the timed
+    # steps (the default per-call check would synchronise every step)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def gather():
-        beacons._move(tables, 0, lat_k, lat_v, False, lat_len)
+        beacons._move(tables, 0, lat_k, lat_v, False, lat_len, status)
         kernels.raw_pages(raw.pages, raw_tables, raw_k, raw_v, start=0, count=max_raw, to_pages=False,
-                          lengths=raw_len)
+                          lengths=raw_len, status=status)
 
     def decode():
         kernels.latent_decode(q, raw_k.transpose(1, 2), raw_v.transpose(1, 2), lat_k, lat_v, up_k, up_v, scale,
@@ -281,15 +321,16 @@ def paged(args):
         # raw rows (sinks + tail) still come out of their pages into a small dense
         # buffer; the beacon rows are read by the decode straight from the pages
         kernels.raw_pages(raw.pages, raw_tables, raw_k, raw_v, start=0, count=max_raw, to_pages=False,
-                          lengths=raw_len)
+                          lengths=raw_len, status=status)
         kernels.paged_latent_decode(q, raw_k.transpose(1, 2), raw_v.transpose(1, 2), pool, tables, lat_len, max_nb,
                                     layout, up_k, up_v, scale, rows_total=sum(nb), block_diagonal=True,
-                                    raw_lengths=raw_len, out=out)
+                                    raw_lengths=raw_len, out=out, status=status)
 
     seconds = _time_steps(torch, direct_step, args.steps, args.warmup)
     replays, clocks = _replays(torch, direct_step)
     restore_s = _time_steps(torch, restore_step, args.steps, args.warmup)
     decode_s = _time_steps(torch, decode, args.steps, args.warmup)
+    kernels.check_status(status)
     algo = sum(n * 2 * R * 2 + c * HKV * D * 2 * 2 for n, c in zip(nb, raw_count)) + NSEQ * 2 * HQ * D * 2 \
         + 2 * HKV * D * R * 2
     gbps = algo / seconds / 1e9

@@ -26,6 +26,16 @@ extern "C" {
 #define SLIMKV_EWORKSPACE (-3) /* workspace too small */
 #define SLIMKV_EHIP (-4)     /* HIP runtime error */
 
+/* Block tables follow torch's indexing rules, like the reference's page I/O
+ * (slimkv/vllm_plugin/paged_cache.py:60-67, :111-127): an entry in
+ * [-num_pages, 0) counts from the end of the pool; a row whose table column
+ * lies past the table or whose entry lies outside [-num_pages, num_pages) is an
+ * index error (the reference raises IndexError).  Kernels reading such a row
+ * use no data from it, kernels writing it write nothing, and when the
+ * argument struct's `status` (device int32, optional) is set they store
+ * SLIMKV_STATUS_BAD_PAGE there with an ordinary store; nothing clears it. */
+#define SLIMKV_STATUS_BAD_PAGE 1
+
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* slimkv_last_error(void);
 
@@ -166,8 +176,10 @@ int slimkv_latent_decode_noalloc(const slimkv_latent_decode_args* a, void* strea
  * | slots x (rank_k + rank_v)] bf16; beacon i of sequence b sits in page
  * table[b * t_sb + i / slots] (t_cols entries per row, at least
  * ceil(lat_keys / slots), like the reference's IndexError) at column sink_elements + (i % slots) *
- * (rank_k + rank_v), K first, then V.  Page ids are clamped into
- * [0, num_pages).  base.lat_k / lat_v and their strides are ignored;
+ * (rank_k + rank_v), K first, then V.  Page ids follow the block-table rules
+ * above (an out-of-pool id is reported through `status`; the row then reads
+ * page 0 so every access stays inside the pool, and the output is not
+ * meaningful).  base.lat_k / lat_v and their strides are ignored;
  * base.lat_lengths (beacons per sequence) is required and base.lat_keys is
  * the largest count.  rows_total: the sum of lat_lengths when the host knows
  * it (sizes the key splits; 0 = unknown), never needed for correctness.
@@ -180,6 +192,7 @@ typedef struct slimkv_paged_latent_decode_args {
     const int64_t* table; int64_t t_sb, t_cols;
     int64_t slots, sink_elements;
     int64_t rows_total;
+    int32_t* status;   /* optional: SLIMKV_STATUS_BAD_PAGE on an index error */
 } slimkv_paged_latent_decode_args;
 
 size_t slimkv_paged_latent_decode_workspace(const slimkv_paged_latent_decode_args* a);
@@ -387,14 +400,16 @@ int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size
  * Row i of request b is beacon start + i: page table[b*t_sb + (start+i)/slots]
  * (t_cols entries per row), columns sink_elements + ((start+i) % slots) *
  * slot_width + column + [0, out_features); column is 0 for the K latent and
- * key_rank for the V latent (BeaconPageLayout, paged_cache.py:27-44).  Rows
- * whose table index or page id falls outside the table or pool are skipped.
+ * key_rank for the V latent (BeaconPageLayout, paged_cache.py:27-44).  Table
+ * entries follow the block-table rules above: a row with an index error is
+ * not written and is reported through dst->status.
  * a->out / o_sb / o_sn are ignored; workspace as slimkv_down_project. */
 typedef struct slimkv_page_rows {
     void* pages; int64_t num_pages, page_stride;
     const int64_t* table; int64_t t_sb, t_cols;
     int64_t slots, sink_elements, slot_width, column;
     int64_t start;
+    int32_t* status;   /* optional: SLIMKV_STATUS_BAD_PAGE on an index error */
 } slimkv_page_rows;
 
 int slimkv_down_project_to_pages(const slimkv_down_project_args* a, const slimkv_page_rows* dst, void* workspace,
@@ -414,18 +429,20 @@ int slimkv_down_project_to_pages(const slimkv_down_project_args* a, const slimkv
  *   K at dense_k[b*dk_sb + (i-start)*dk_sn + c], V likewise.
  * lengths: optional device int32 [batch]; request b moves only beacons
  * i < lengths[b] (the rest of its dense rows and pages are untouched).
- * A table entry outside [0, num_pages) moves nothing for its rows.
+ * Each table row holds t_cols entries; entries follow the block-table rules
+ * above (a row with an index error moves nothing and sets `status`).
  * to_pages = 1 appends (dense -> pages), 0 reads (pages -> dense).
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_beacon_pages_args {
     void* pages; int64_t num_pages, page_stride;
-    const int64_t* table; int64_t t_sb;
+    const int64_t* table; int64_t t_sb, t_cols;
     void* dense_k; int64_t dk_sb, dk_sn;
     void* dense_v; int64_t dv_sb, dv_sn;
     const int32_t* lengths;
     int64_t batch, start, count;
     int64_t slots, key_rank, value_rank, sink_elements;
     int32_t to_pages;
+    int32_t* status;   /* optional: SLIMKV_STATUS_BAD_PAGE on an index error */
 } slimkv_beacon_pages_args;
 
 int slimkv_beacon_pages(const slimkv_beacon_pages_args* a, void* stream);
@@ -439,17 +456,19 @@ int slimkv_beacon_pages(const slimkv_beacon_pages_args* a, void* stream);
  * start .. start+count-1 map to dense row t - start:
  *   K at dense_k[b*dk_sb + h*dk_sh + (t-start)*dk_sn + d], V likewise.
  * lengths: optional device int32 [batch] token counts (positions >= lengths[b]
- * are skipped).  A table entry outside [0, num_blocks) moves nothing.
+ * are skipped).  Each table row holds t_cols entries; entries follow the
+ * block-table rules above with num_blocks as the pool size.
  * to_pages = 1 writes, 0 reads.
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_raw_pages_args {
     void* pages; int64_t num_blocks, p_sblk, p_stok, p_skind, p_sh;
-    const int64_t* table; int64_t t_sb;
+    const int64_t* table; int64_t t_sb, t_cols;
     void* dense_k; int64_t dk_sb, dk_sh, dk_sn;
     void* dense_v; int64_t dv_sb, dv_sh, dv_sn;
     const int32_t* lengths;
     int64_t batch, start, count, block_size, kv_heads, head_dim;
     int32_t to_pages;
+    int32_t* status;   /* optional: SLIMKV_STATUS_BAD_PAGE on an index error */
 } slimkv_raw_pages_args;
 
 int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream);

@@ -83,6 +83,7 @@ PagedLatentDecodeArgs = _struct('slimkv_paged_latent_decode_args', [
     ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
     ('table', c_ptr), *_i64s('t_sb', 't_cols'),
     *_i64s('slots', 'sink_elements', 'rows_total'),
+    ('status', c_ptr),
 ])
 
 RopeDecodeArgs = _struct('slimkv_rope_decode_args', [
@@ -140,26 +141,29 @@ PageRows = _struct('slimkv_page_rows', [
     ('table', c_ptr), *_i64s('t_sb', 't_cols'),
     *_i64s('slots', 'sink_elements', 'slot_width', 'column'),
     ('start', c_i64),
+    ('status', c_ptr),
 ])
 
 BeaconPagesArgs = _struct('slimkv_beacon_pages_args', [
     ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
-    ('table', c_ptr), ('t_sb', c_i64),
+    ('table', c_ptr), *_i64s('t_sb', 't_cols'),
     ('dense_k', c_ptr), *_i64s('dk_sb', 'dk_sn'),
     ('dense_v', c_ptr), *_i64s('dv_sb', 'dv_sn'),
     ('lengths', c_ptr),
     *_i64s('batch', 'start', 'count', 'slots', 'key_rank', 'value_rank', 'sink_elements'),
     ('to_pages', c_i32),
+    ('status', c_ptr),
 ])
 
 RawPagesArgs = _struct('slimkv_raw_pages_args', [
     ('pages', c_ptr), *_i64s('num_blocks', 'p_sblk', 'p_stok', 'p_skind', 'p_sh'),
-    ('table', c_ptr), ('t_sb', c_i64),
+    ('table', c_ptr), *_i64s('t_sb', 't_cols'),
     ('dense_k', c_ptr), *_i64s('dk_sb', 'dk_sh', 'dk_sn'),
     ('dense_v', c_ptr), *_i64s('dv_sb', 'dv_sh', 'dv_sn'),
     ('lengths', c_ptr),
     *_i64s('batch', 'start', 'count', 'block_size', 'kv_heads', 'head_dim'),
     ('to_pages', c_i32),
+    ('status', c_ptr),
 ])
 
 # name -> (restype, argtypes)
@@ -197,10 +201,11 @@ SIGNATURES = {
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20
+STATUS_BAD_PAGE = 1
 
 
 class SlimKVError(RuntimeError):

@@ -55,9 +55,12 @@ struct Seg {
     int wown;
     int nwg;
     // Paged rows (PAGED instances): row i of batch b starts at
-    // k / v + clamp(table[b][i / slots]) * page_stride + (i % slots) * k_sn.
+    // k / v + page(table[b][i / slots]) * page_stride + (i % slots) * k_sn,
+    // page() with torch's indexing rules; an entry outside the pool is
+    // reported in *status (the row then reads page 0, inside the pool).
     const int64_t* table; int64_t t_sb, page_stride, num_pages;
     int slots, slots_shift;                          // slots_shift = log2(slots) or -1
+    int32_t* status;
     // Compact schedule: workgroup items enumerate only the non-empty splits of
     // each batch entry (needs seqlens); items past the last one exit at once.
     int compact, batch;
@@ -216,9 +219,8 @@ __device__ __forceinline__ bool locate_split(int item, const int32_t* lens, int 
     return false;
 }
 
-// Page ids of one tile's rows for the lanes' K row and V pieces (PAGED): the
-// low words of the int64 table entries (the host limits pools to 2^31 pages;
-// any other value is clamped into the pool like an out-of-range id).
+// Page ids of one tile's rows for the lanes' K row and V pieces (PAGED),
+// already resolved into [0, num_pages) (the host limits pools to 2^31 pages).
 template <int KS>
 struct TilePages {
     int32_t k;
@@ -236,8 +238,8 @@ struct TilePair {
 };
 
 // Paged variant of load_tile: the same lane/piece mapping, each row's base
-// taken from its page id.  Any page id is clamped into the pool, so every
-// address is inside it whatever the table holds.
+// taken from its resolved page id, so every address is inside the pool
+// whatever the table holds.
 template <int KS>
 __device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages<KS>& pg, const Seg& sg,
                                                 const uint16_t* kpage, const uint16_t* vpage, int r0, int r_end,
@@ -245,7 +247,6 @@ __device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages
                                                 bool act) {
     constexpr int VT = KS;
     auto row_base = [&](int32_t pid, int row) -> int64_t {
-        pid = pid < 0 ? 0 : (pid >= sg.num_pages ? (int32_t)sg.num_pages - 1 : pid);
         const int r = min(row, last_valid);
         const int slot = sg.slots_shift >= 0 ? (r & (sg.slots - 1)) : r % sg.slots;
         return pid * sg.page_stride + (int64_t)slot * sg.k_sn;
@@ -397,30 +398,41 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         load_tile<KS>(tr, kbase, vbase, sg.k_sn, sg.v_sn, r0, act ? r_end : r_begin, last_row, span_k, span_v,
                       col, grp, lane, act);
     };
-    // Paged rows: the page ids of a tile are loaded two tiles ahead of its data.
-    const int32_t* tab = PAGED ? reinterpret_cast<const int32_t*>(sg.table + (int64_t)b * sg.t_sb) : nullptr;
+    // Paged rows: the page ids of a tile are loaded two tiles ahead of its
+    // data.  An entry outside the pool that a row of the sequence needs sets
+    // `bad` (reported once the split is done) and is read as page 0.
+    const int64_t* tab = PAGED ? sg.table + (int64_t)b * sg.t_sb : nullptr;
     const int last_valid = Nb > 0 ? Nb - 1 : 0;
-    auto page_of = [&](int row) -> int32_t {
+    bool bad = false;
+    auto page_of = [&](int row, bool used) -> int32_t {
         const int r = min(row, last_valid);
-        return tab[2 * (sg.slots_shift >= 0 ? (r >> sg.slots_shift) : r / sg.slots)];   // low word
+        const int64_t p = table_page(tab[sg.slots_shift >= 0 ? (r >> sg.slots_shift) : r / sg.slots], sg.num_pages);
+        bad |= used && p < 0;
+        return p < 0 ? 0 : (int32_t)p;
     };
     const int last_page = PAGED == 2 ? last_valid / sg.slots : 0;
     auto load_pages = [&](auto& pg, int it) {
-        const int r0 = it < ntile ? r_begin + it * r_step : r_begin;
+        const bool act = it < ntile;
+        const int r0 = act ? r_begin + it * r_step : r_begin;
         if constexpr (PAGED == 2) {
             const int r0c = __builtin_amdgcn_readfirstlane(min(r0, last_valid));
             const int pi = __builtin_amdgcn_readfirstlane(r0c / sg.slots);
-            const int32_t np = (int32_t)sg.num_pages;
-            const int32_t a = __builtin_amdgcn_readfirstlane(tab[2 * pi]);
-            const int32_t c = __builtin_amdgcn_readfirstlane(tab[2 * min(pi + 1, last_page)]);
+            const int64_t a = table_page(tab[pi], sg.num_pages);
+            const int64_t c = table_page(tab[min(pi + 1, last_page)], sg.num_pages);
             pg.r0c = r0c;
             pg.slot0 = r0c - pi * sg.slots;
-            pg.p0 = a < 0 ? 0 : (a >= np ? np - 1 : a);
-            pg.p1 = c < 0 ? 0 : (c >= np ? np - 1 : c);
+            // the tile's valid rows reach the next page when its last one does
+            const bool crosses = min(r0 + 15, last_valid) - r0c + pg.slot0 >= sg.slots;
+            bad |= act && (a < 0 || (crosses && c < 0));
+            pg.p0 = a < 0 ? 0 : (int32_t)a;
+            pg.p1 = c < 0 ? 0 : (int32_t)c;
         } else {
-            pg.k = page_of(r0 + col);
+            pg.k = page_of(r0 + col, act && r0 + col < r_end);
 #pragma unroll
-            for (int c = 0; c < VT / 2; ++c) pg.v[c] = page_of(r0 + (64 * c + lane) / (2 * VT));
+            for (int c = 0; c < VT / 2; ++c) {
+                const int row = r0 + (64 * c + lane) / (2 * VT);
+                pg.v[c] = page_of(row, act && row < r_end);
+            }
         }
     };
     auto fetch_paged = [&](TileRegs<KS>& tr, const auto& pg, int it) {
@@ -561,6 +573,9 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         }
     }
 
+    if constexpr (PAGED) {
+        if (bad) report_bad_page(sg.status);
+    }
     // Column sums: every lane group holds a quarter of the keys.
     lsum += shfl_xor_f(lsum, 16);
     lsum += shfl_xor_f(lsum, 32);
@@ -1716,7 +1731,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 6; }
+extern "C" int slimkv_abi_version(void) { return 7; }
 
 extern "C" size_t slimkv_attention_workspace(const slimkv_attention_args* a) {
     AttnPlan plan{};
@@ -1789,6 +1804,7 @@ struct PagedRows {
     const uint16_t* pages; int64_t num_pages, page_stride;
     const int64_t* table; int64_t t_sb, t_cols;
     int64_t slots, sink, rows_total;
+    int32_t* status;
 };
 
 int check_paged(const slimkv_latent_decode_args* a, const PagedRows* pg) {
@@ -2029,6 +2045,7 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
             l.table = pg->table; l.t_sb = pg->t_sb; l.page_stride = pg->page_stride; l.num_pages = pg->num_pages;
             l.slots = (int)pg->slots;
             l.slots_shift = (pg->slots & (pg->slots - 1)) == 0 ? __builtin_ctzll((unsigned long long)pg->slots) : -1;
+            l.status = pg->status;
             l.compact = 1; l.batch = B;
         }
         ka = p.lat.ks;
@@ -2065,7 +2082,7 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
 
 PagedRows paged_rows(const slimkv_paged_latent_decode_args* a) {
     return PagedRows{static_cast<const uint16_t*>(a->pages), a->num_pages, a->page_stride, a->table, a->t_sb,
-                     a->t_cols, a->slots, a->sink_elements, a->rows_total};
+                     a->t_cols, a->slots, a->sink_elements, a->rows_total, a->status};
 }
 
 }  // namespace

@@ -70,6 +70,19 @@ __device__ __forceinline__ int64_t clamp_i64(int64_t x, int64_t lo, int64_t hi) 
     return x < lo ? lo : (x > hi ? hi : x);
 }
 
+// Block-table entry -> page index with torch's indexing rules: [-n, 0) counts
+// from the end of the pool; -1 marks an entry outside [-n, n) (an index error).
+__device__ __forceinline__ int64_t table_page(int64_t id, int64_t n) {
+    const int64_t p = id < 0 ? id + n : id;
+    return (p >= 0 && p < n) ? p : -1;
+}
+
+// Index-error report: an ordinary store of the status code (any number of
+// lanes may store the same value).
+__device__ __forceinline__ void report_bad_page(int32_t* status) {
+    if (status) *status = SLIMKV_STATUS_BAD_PAGE;
+}
+
 // Thread-local message behind slimkv_last_error().
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);

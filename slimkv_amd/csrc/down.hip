@@ -32,18 +32,22 @@ struct DownParams {
     int B, n, N, K, blocks, splits, kchunk;
     // Page destination (table != null): row i of request b is beacon start + i,
     // written at out + page * page_stride + ((start + i) % slots) * slot_width
-    // with page = table[b * t_sb + (start + i) / slots]; rows whose table
-    // entry lies outside [0, t_cols) or whose page lies outside the pool are skipped.
+    // with page = table[b * t_sb + (start + i) / slots] under torch's indexing
+    // rules; a row whose table column lies past t_cols or whose entry lies
+    // outside [-num_pages, num_pages) is not written and is reported in status.
     const int64_t* table; int64_t t_sb, t_cols, slots, page_stride, num_pages, slot_width, start;
+    int32_t* status;
 };
 
 __device__ __forceinline__ uint16_t* dst_row(const DownParams& p, int b, int i) {
     if (!p.table) return p.out + (int64_t)b * p.o_sb + (int64_t)i * p.o_sn;
     const int64_t beacon = p.start + i;
     const int64_t idx = beacon / p.slots;
-    if (idx >= p.t_cols) return nullptr;
-    const int64_t page = p.table[(int64_t)b * p.t_sb + idx];
-    if (page < 0 || page >= p.num_pages) return nullptr;
+    const int64_t page = idx < p.t_cols ? table_page(p.table[(int64_t)b * p.t_sb + idx], p.num_pages) : -1;
+    if (page < 0) {
+        report_bad_page(p.status);
+        return nullptr;
+    }
     return p.out + page * p.page_stride + (beacon % p.slots) * p.slot_width;
 }
 
@@ -216,6 +220,7 @@ int down_run(const slimkv_down_project_args* a, const slimkv_page_rows* pg, void
         p.table = pg->table; p.t_sb = pg->t_sb; p.t_cols = pg->t_cols; p.slots = pg->slots;
         p.page_stride = pg->page_stride; p.num_pages = pg->num_pages; p.slot_width = pg->slot_width;
         p.start = pg->start;
+        p.status = pg->status;
     }
     const int64_t grid = (p.N + 63) / 64 * ((M + 63) / 64) * p.splits;
     hipStream_t st = static_cast<hipStream_t>(stream);

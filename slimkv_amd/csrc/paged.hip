@@ -5,7 +5,8 @@
 // table[i / slots] at columns sink_elements + (i % slots) * width + [0, width),
 // K latent (key_rank) first, then V latent (value_rank).
 // Raw pages (paged_cache.py:102-127): [blocks, block_size, 2, Hkv, D]; token t
-// lives in block table[t / block_size] at row t % block_size.
+// lives in block table[t / block_size] at row t % block_size.  Table entries
+// follow torch's indexing rules; an index error moves nothing and is reported.
 //
 // These copies are HBM-bound byte moves: one thread moves one 16-byte piece
 // (VEC = 8 bf16) whenever every row start and width allows it, else one
@@ -37,8 +38,12 @@ beacon_pages_kernel(slimkv_beacon_pages_args a) {
     const int64_t c = (gid % per_row) * VEC;           // column inside [K | V]
     const int64_t logical = a.start + r;
     if (a.lengths && logical >= a.lengths[b]) return;
-    const int64_t page = a.table[b * a.t_sb + logical / a.slots];
-    if (page < 0 || page >= a.num_pages) return;
+    const int64_t col = logical / a.slots;
+    const int64_t page = col < a.t_cols ? table_page(a.table[b * a.t_sb + col], a.num_pages) : -1;
+    if (page < 0) {
+        report_bad_page(a.status);
+        return;
+    }
     uint16_t* pg = static_cast<uint16_t*>(a.pages) + page * a.page_stride + a.sink_elements +
                    (logical % a.slots) * width + c;
     const bool is_k = c < a.key_rank;
@@ -57,8 +62,12 @@ raw_pages_kernel(slimkv_raw_pages_args a) {
     const int64_t r = blockIdx.x;
     const int64_t t = a.start + r;
     if (a.lengths && t >= a.lengths[b]) return;
-    const int64_t block = a.table[b * a.t_sb + t / a.block_size];
-    if (block < 0 || block >= a.num_blocks) return;
+    const int64_t col = t / a.block_size;
+    const int64_t block = col < a.t_cols ? table_page(a.table[b * a.t_sb + col], a.num_blocks) : -1;
+    if (block < 0) {
+        if (threadIdx.x == 0) report_bad_page(a.status);
+        return;
+    }
     const int dv = (int)a.head_dim / VEC, hd = (int)a.kv_heads * dv;
     uint16_t* pg = static_cast<uint16_t*>(a.pages) + block * a.p_sblk + (t % a.block_size) * a.p_stok;
     for (int i = threadIdx.x; i < 2 * hd; i += blockDim.x) {
@@ -94,7 +103,7 @@ extern "C" int slimkv_beacon_pages(const slimkv_beacon_pages_args* a, void* stre
     if (!a || !a->pages || !a->table || (a->count > 0 && (!a->dense_k || !a->dense_v)))
         return fail(SLIMKV_EINVAL, "null pointer");
     if (a->slots <= 0 || a->key_rank <= 0 || a->value_rank <= 0 || a->sink_elements < 0 || a->start < 0 ||
-        a->count < 0 || a->batch < 0 || a->num_pages < 0 || a->batch > 65535 ||
+        a->count < 0 || a->batch < 0 || a->num_pages < 0 || a->batch > 65535 || a->t_cols <= 0 || a->t_sb < a->t_cols ||
         a->page_stride < a->sink_elements + a->slots * (a->key_rank + a->value_rank))
         return fail(SLIMKV_EINVAL, "invalid beacon page layout");
     if (a->count == 0 || a->batch == 0) return SLIMKV_OK;
@@ -112,7 +121,7 @@ extern "C" int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream) {
     if (!a || !a->pages || !a->table || (a->count > 0 && (!a->dense_k || !a->dense_v)))
         return fail(SLIMKV_EINVAL, "null pointer");
     if (a->block_size <= 0 || a->kv_heads <= 0 || a->head_dim <= 0 || a->start < 0 || a->count < 0 ||
-        a->batch < 0 || a->batch > 65535 || a->num_blocks < 0)
+        a->batch < 0 || a->batch > 65535 || a->num_blocks < 0 || a->t_cols <= 0 || a->t_sb < a->t_cols)
         return fail(SLIMKV_EINVAL, "invalid raw page layout");
     if (a->count == 0 || a->batch == 0) return SLIMKV_OK;
     if (a->count > ((int64_t)1 << 31) - 1 || a->kv_heads * a->head_dim > (1 << 20))

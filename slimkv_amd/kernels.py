@@ -136,13 +136,14 @@ def down_project(x, weight, rows=None, *, blocks=1, out=None):
     return out
 
 
-def down_project_to_pages(x, weight, pages, table, layout, start, kind, rows=None, *, blocks=1):
+def down_project_to_pages(x, weight, pages, table, layout, start, kind, rows=None, *, blocks=1, status=None):
     """down_project with the latents written straight into beacon pages:
     row i of request b becomes beacon `start + i` of that request (its K
     latent when kind == 'k', V latent when 'v'), at the BeaconPageLayout
     position table[b, (start + i) // slots].  pages [num_pages, >= page
-    elements] bf16, table [B, T] int64.  Rows mapping outside the table or
-    pool are skipped."""
+    elements] bf16, table [B, T] int64 under torch's indexing rules.  A row
+    mapping outside the table or pool is not written; `status` as
+    beacon_pages."""
     _need_device(x, weight, rows, pages, table)
     _need_bf16(x, weight, pages)
     if kind not in ('k', 'v'):
@@ -165,15 +166,18 @@ def down_project_to_pages(x, weight, pages, table, layout, start, kind, rows=Non
     n = L if rows is None else rows.numel()
     a = _lib.DownProjectArgs(_ptr(x), x.stride(0), x.stride(1), _ptr(rows), n, L, _ptr(weight),
                              _ptr(pages), 0, 0, B, K, N, int(blocks))
+    status, owned = _status_word(status, pages.device)
     dst = _lib.PageRows(_ptr(pages), pages.shape[0], pages.stride(0), _ptr(table), table.stride(0), table.shape[1],
                         layout.slots, layout.sink_elements, layout.width, 0 if kind == 'k' else layout.key_rank,
-                        int(start))
+                        int(start), _ptr(status))
     nbytes = lib().slimkv_down_project_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
     ws = _workspace(nbytes, x.device)
     check(lib().slimkv_down_project_to_pages(ctypes.byref(a), ctypes.byref(dst), _ptr(ws), nbytes,
                                              _lib.stream_handle(x.device)))
+    if owned:
+        check_status(status)
     return pages
 
 
@@ -309,14 +313,18 @@ def _stage_workspace(workspace, nbytes, stages, device):
 def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, layout, up_k, up_v, scale, *,
                         rows_total=0, up_k_bias=None, up_v_bias=None, block_diagonal=False, lat_causal=False,
                         q_positions=None, cos=None, sin=None, raw_lengths=None, raw_splits=0, lat_splits=0,
-                        out=None, lse=None, workspace=None, stages=_lib.STAGE_ALL):
+                        out=None, lse=None, workspace=None, stages=_lib.STAGE_ALL, status=None):
     """latent_decode with the beacon rows read straight out of beacon pages.
 
     pages [num_pages, layout.page_elements] bf16 in BeaconPageLayout format;
     table [B, >= ceil(lat_keys / slots)] int64 page ids; lat_lengths [B] int32
     beacons per sequence (<= lat_keys).  rows_total = sum of lat_lengths when
     known on the host (sizes the key splits only).  Same result as gathering
-    the rows (BeaconPages.read_batch) and calling latent_decode.
+    the rows (BeaconPages.read_batch) and calling latent_decode.  Table
+    entries follow torch's indexing rules; an entry outside the pool that a
+    beacon needs raises IndexError after the call (one host synchronisation)
+    unless the caller passes its own device int32 `status` word (graph
+    capture, serving loops) and checks it with check_status.
     """
     _need_device(pages, table, lat_lengths)
     _need_bf16(pages)
@@ -331,8 +339,9 @@ def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, la
     base, out, lse, keep = _latent_args(q, raw_k, raw_v, None, None, up_k, up_v, scale, up_k_bias, up_v_bias,
                                         block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
                                         lat_lengths, raw_splits, lat_splits, out, lse, True, lat_rows=lat_keys)
+    status, owned = _status_word(status, pages.device)
     a = _lib.PagedLatentDecodeArgs(base, _ptr(pages), pages.shape[0], pages.stride(0), _ptr(table), table.stride(0),
-                                   table.shape[1], layout.slots, layout.sink_elements, int(rows_total))
+                                   table.shape[1], layout.slots, layout.sink_elements, int(rows_total), _ptr(status))
     nbytes = lib().slimkv_paged_latent_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
@@ -343,6 +352,8 @@ def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, la
     else:
         check(lib().slimkv_paged_latent_decode_stages(ctypes.byref(a), int(stages), _ptr(workspace), nbytes,
                                                       _lib.stream_handle(q.device)))
+    if owned and stages & _lib.STAGE_ATTEND:
+        check_status(status)
     del keep
     return out, lse
 
@@ -506,6 +517,24 @@ def default_scale(head_dim):
     return 1.0 / math.sqrt(head_dim)
 
 
+def _status_word(status, device):
+    """(status, owned): the caller's device int32 status word, or a fresh zeroed
+    one that the call checks itself (one host synchronisation) when owned."""
+    if status is not None:
+        if status.dtype != torch.int32 or status.device != device or status.numel() < 1:
+            raise ValueError('status must be a device int32 tensor on the pages\' device')
+        return status, False
+    return torch.zeros(1, dtype=torch.int32, device=device), True
+
+
+def check_status(status):
+    """Raise IndexError when a kernel reported a block-table index error in
+    `status` (the reference's torch indexing raises IndexError for an entry
+    outside the pool, paged_cache.py:60-67).  Synchronises the host."""
+    if int(status.reshape(-1)[0].item()) != 0:
+        raise IndexError('block table refers to a page outside the allocation')
+
+
 def _table(table, device):
     """Block table as device int64 [B, T] (a 1-D table is one request)."""
     table = table.to(device=device, dtype=torch.long)
@@ -526,10 +555,13 @@ def _lengths(lengths, batch, device):
 
 
 def beacon_pages(pages, table, dense_k, dense_v, *, slots, key_rank, value_rank, sink_elements, start, count,
-                 to_pages, lengths=None):
+                 to_pages, lengths=None, status=None):
     """Copy beacon latents between pages [num_pages, >=page_elements] and dense
     rows dense_k [B, count, key_rank], dense_v [B, count, value_rank]
-    (slimkv/vllm_plugin/paged_cache.py:60-87).  table: [B, T] or [T] int64."""
+    (slimkv/vllm_plugin/paged_cache.py:60-87).  table: [B, T] or [T] int64,
+    entries under torch's indexing rules.  A row whose entry lies outside the
+    pool moves nothing; without a caller `status` word that raises IndexError
+    here (one host synchronisation), with one it is left in `status`."""
     _need_device(pages, dense_k, dense_v)
     _need_bf16(pages, dense_k, dense_v)
     if pages.dim() != 2 or pages.stride(1) != 1:
@@ -539,22 +571,24 @@ def beacon_pages(pages, table, dense_k, dense_v, *, slots, key_rank, value_rank,
     for t, w in ((dense_k, key_rank), (dense_v, value_rank)):
         if t.dim() != 3 or t.shape != (B, count, w) or t.stride(2) != 1:
             raise ValueError(f'dense latents must be [{B}, {count}, {w}] with contiguous rows')
-    if table.shape[1] * slots < start + count:
-        raise ValueError('block table does not cover the requested beacons')
     lengths = _lengths(lengths, B, pages.device)
+    status, owned = _status_word(status, pages.device)
     a = _lib.BeaconPagesArgs(
         pages=_ptr(pages), num_pages=pages.shape[0], page_stride=pages.stride(0),
-        table=_ptr(table), t_sb=table.stride(0),
+        table=_ptr(table), t_sb=table.stride(0), t_cols=table.shape[1],
         dense_k=_ptr(dense_k), dk_sb=dense_k.stride(0), dk_sn=dense_k.stride(1),
         dense_v=_ptr(dense_v), dv_sb=dense_v.stride(0), dv_sn=dense_v.stride(1),
         lengths=_ptr(lengths), batch=B, start=start, count=count, slots=slots, key_rank=key_rank,
-        value_rank=value_rank, sink_elements=sink_elements, to_pages=int(bool(to_pages)))
+        value_rank=value_rank, sink_elements=sink_elements, to_pages=int(bool(to_pages)), status=_ptr(status))
     check(lib().slimkv_beacon_pages(ctypes.byref(a), _lib.stream_handle(pages.device)))
+    if owned:
+        check_status(status)
 
 
-def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths=None):
+def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths=None, status=None):
     """Copy raw K/V between pages [blocks, block_size, 2, Hkv, D] and dense
-    dense_k/dense_v [B, Hkv, count, D] (slimkv/vllm_plugin/paged_cache.py:102-127)."""
+    dense_k/dense_v [B, Hkv, count, D] (slimkv/vllm_plugin/paged_cache.py:102-127).
+    Table entries and `status` as beacon_pages."""
     _need_device(pages, dense_k, dense_v)
     _need_bf16(pages, dense_k, dense_v)
     if pages.dim() != 5 or pages.shape[2] != 2 or pages.stride(4) != 1:
@@ -565,15 +599,16 @@ def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths
     for t in (dense_k, dense_v):
         if t.dim() != 4 or t.shape != (B, H, count, D) or t.stride(3) != 1:
             raise ValueError(f'dense K/V must be [{B}, {H}, {count}, {D}] with contiguous rows')
-    if table.shape[1] * block_size < start + count:
-        raise ValueError('block table does not cover the requested tokens')
     lengths = _lengths(lengths, B, pages.device)
+    status, owned = _status_word(status, pages.device)
     a = _lib.RawPagesArgs(
         pages=_ptr(pages), num_blocks=pages.shape[0], p_sblk=pages.stride(0), p_stok=pages.stride(1),
         p_skind=pages.stride(2), p_sh=pages.stride(3),
-        table=_ptr(table), t_sb=table.stride(0),
+        table=_ptr(table), t_sb=table.stride(0), t_cols=table.shape[1],
         dense_k=_ptr(dense_k), dk_sb=dense_k.stride(0), dk_sh=dense_k.stride(1), dk_sn=dense_k.stride(2),
         dense_v=_ptr(dense_v), dv_sb=dense_v.stride(0), dv_sh=dense_v.stride(1), dv_sn=dense_v.stride(2),
         lengths=_ptr(lengths), batch=B, start=start, count=count, block_size=block_size, kv_heads=H,
-        head_dim=D, to_pages=int(bool(to_pages)))
+        head_dim=D, to_pages=int(bool(to_pages)), status=_ptr(status))
     check(lib().slimkv_raw_pages(ctypes.byref(a), _lib.stream_handle(pages.device)))
+    if owned:
+        check_status(status)

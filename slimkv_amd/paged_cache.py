@@ -52,13 +52,6 @@ class BeaconPageLayout:
         return (self.page_elements + self.width - 1) // self.width
 
 
-def _check_table_values(table, limit):
-    """Host tables are range-checked before upload (torch indexing would raise
-    IndexError); device tables are bounded inside the kernel."""
-    if table.device.type == 'cpu' and table.numel() and (int(table.min()) < 0 or int(table.max()) >= limit):
-        raise IndexError('block table refers to a page outside the allocation')
-
-
 class BeaconPages:
     """Read and append compact rows without owning or allocating KV pages
     (paged_cache.py:47-99)."""
@@ -73,12 +66,14 @@ class BeaconPages:
             raise ValueError('Physical page is too small for the declared ranks.')
         self.layout = layout
 
-    def _move(self, table, start, key, value, to_pages, lengths=None):
+    def _move(self, table, start, key, value, to_pages, lengths=None, status=None):
+        """Block-table entries follow torch's indexing rules; an entry outside
+        the pool that a row needs raises IndexError (as the reference's indexing
+        does, paged_cache.py:60-67), or with a caller `status` word is left there."""
         L = self.layout
-        _check_table_values(table, self.pages.shape[0])
         kernels.beacon_pages(self.pages, table, key, value, slots=L.slots, key_rank=L.key_rank,
                              value_rank=L.value_rank, sink_elements=L.sink_elements, start=start,
-                             count=key.shape[1], to_pages=to_pages, lengths=lengths)
+                             count=key.shape[1], to_pages=to_pages, lengths=lengths, status=status)
 
     def read(self, block_table, count):
         """(k [1,1,count,key_rank], v [1,1,count,value_rank]) of beacons 0..count-1."""
@@ -103,24 +98,27 @@ class BeaconPages:
             return
         self._move(block_table, start, key[0], value[0], True)
 
-    def read_batch(self, tables, lengths, count=None):
+    def read_batch(self, tables, lengths, count=None, status=None):
         """Dense latents of many requests: tables [B, T] (one block-table row per
         request), lengths [B] beacon counts.  Returns k [B, count, key_rank] and
-        v [B, count, value_rank]; rows at or past a request's length are zero."""
+        v [B, count, value_rank]; rows at or past a request's length are zero.
+        `status`: an optional device int32 word that receives index errors
+        instead of an IndexError (then rows with an index error stay zero)."""
         L = self.layout
         count = int(lengths.max()) if count is None else count
         B = tables.shape[0]
         k = torch.zeros(B, count, L.key_rank, dtype=self.pages.dtype, device=self.pages.device)
         v = torch.zeros(B, count, L.value_rank, dtype=self.pages.dtype, device=self.pages.device)
         if count:
-            self._move(tables, 0, k, v, False, lengths)
+            self._move(tables, 0, k, v, False, lengths, status)
         return k, v
 
-    def append_batch(self, tables, start, key, value, lengths=None):
+    def append_batch(self, tables, start, key, value, lengths=None, status=None):
         """Store key [B, n, key_rank] / value [B, n, value_rank] of many requests
-        as their beacons start..start+n-1 (rows past lengths[b] are skipped)."""
+        as their beacons start..start+n-1 (rows past lengths[b] are skipped;
+        `status` as read_batch)."""
         if key.shape[1]:
-            self._move(tables, start, key, value, True, lengths)
+            self._move(tables, start, key, value, True, lengths, status)
 
     def write_sink(self, root_block, key, value):
         rows = torch.cat([key.flatten(), value.flatten()])
@@ -149,7 +147,6 @@ class RawPages:
         """(K, V) as [1, Hkv, count, D] of raw positions start..start+count-1."""
         if count == 0:
             return None, None
-        _check_table_values(block_table, self.pages.shape[0])
         _, _, _, H, D = self.pages.shape
         k = torch.empty(1, H, count, D, dtype=self.pages.dtype, device=self.pages.device)
         v = torch.empty_like(k)
@@ -166,7 +163,6 @@ class RawPages:
             raise ValueError('Raw cache dimensions differ from the engine allocation.')
         if key.shape[2] == 0:
             return
-        _check_table_values(block_table, self.pages.shape[0])
         kernels.raw_pages(self.pages, block_table, key.contiguous(), value.contiguous(), start=start,
                           count=key.shape[2], to_pages=True)
 

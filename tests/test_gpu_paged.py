@@ -107,7 +107,10 @@ def test_serving_layout_read_append_bit_exact(device, start, count):
     np.testing.assert_array_equal(bits(rv[0, 0]), gathered[:, 256:])
 
 
-def test_batched_read_with_lengths_and_out_of_range_entries(device):
+def test_batched_read_with_lengths_and_negative_entries(device):
+    """Batched reads past each request's length stay zero; a negative entry in
+    [-n, 0) counts from the end of the pool (torch indexing, as the
+    reference's pages[page, column] does)."""
     from slimkv_amd.paged_cache import BeaconPageLayout, BeaconPages
     layout = BeaconPageLayout(16, 8, 256, 256, 1024)
     olayout = opaged.Layout(16, 8, 256, 256, 1024)
@@ -116,8 +119,9 @@ def test_batched_read_with_lengths_and_out_of_range_entries(device):
     perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(2))[:B * T].reshape(B, T)
     lengths = torch.tensor([0, 1, 2, 3, 77, 128, 239, 240, 17], dtype=torch.int32)
     tables = perm.clone()
-    tables[4, 10] = -1                                         # beacons 20, 21 of request 4: no page
-    tables[5, 3] = n_pages                                     # beacons 6, 7 of request 5: past the pool
+    tables[4, 10] = -1                                         # beacons 20, 21 of request 4: the last page
+    tables[5, 3] = -n_pages                                    # beacons 6, 7 of request 5: page 0
+    tables[2, 5:] = n_pages + 99                               # past request 2's length: never read
     pages = BeaconPages(pool, layout)
     k, v = pages.read_batch(tables.to(device), lengths.to(device))
     assert k.shape == (B, 240, 256) and v.shape == (B, 240, 256)
@@ -127,19 +131,50 @@ def test_batched_read_with_lengths_and_out_of_range_entries(device):
         n = int(lengths[b])
         page, first = opaged.beacon_indices(olayout, tables[b].numpy(), 0, n)
         for i in range(240):
-            if i >= n or page[i] < 0 or page[i] >= n_pages:
+            if i >= n:
                 assert not kb[b, i].any() and not vb[b, i].any(), (b, i)
-            else:
+            else:   # numpy indexing wraps negative page ids the way torch's does
                 np.testing.assert_array_equal(kb[b, i], host[page[i], first[i]:first[i] + 256])
                 np.testing.assert_array_equal(vb[b, i], host[page[i], first[i] + 256:first[i] + 512])
     # a batched append of the same rows back into fresh pages round-trips
     fresh = torch.zeros_like(pool)
     again = BeaconPages(fresh, layout)
-    again.append_batch(perm.to(device), 0, k, v, lengths.to(device))
-    k2, v2 = again.read_batch(perm.to(device), lengths.to(device), count=240)
-    ok = (tables >= 0) & (tables < n_pages)
-    mask = np.repeat(ok.numpy(), 2, axis=1)[:, :240]
-    assert (bits(k2)[mask] == kb[mask]).all() and (bits(v2)[mask] == vb[mask]).all()
+    again.append_batch(tables.to(device), 0, k, v, lengths.to(device))
+    k2, v2 = again.read_batch(tables.to(device), lengths.to(device), count=240)
+    assert torch.equal(k2, k) and torch.equal(v2, v)
+
+
+def test_index_errors_raise_or_report_and_move_nothing(device):
+    """An entry outside [-n, n) that a row needs is an index error: the
+    reference's indexing raises IndexError; here the copy of that row does not
+    happen and the call raises IndexError, or, given a status word, leaves
+    SLIMKV_STATUS_BAD_PAGE in it.  A table too short for the rows is the same
+    error."""
+    from slimkv_amd import _lib
+    from slimkv_amd.paged_cache import BeaconPageLayout, BeaconPages, RawPages
+    layout = BeaconPageLayout(16, 8, 256, 256, 1024)
+    n_pages = 50
+    pool = _serving_pool(device, n_pages, layout, 6)
+    pages = BeaconPages(pool, layout)
+    table = torch.arange(10, dtype=torch.long)[None].repeat(2, 1)
+    table[1, 3] = n_pages                                      # beacons 6, 7 of request 1
+    lengths = torch.tensor([20, 20], dtype=torch.int32, device=device)
+    with pytest.raises(IndexError):
+        pages.read_batch(table.to(device), lengths)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    k, v = pages.read_batch(table.to(device), lengths, status=status)
+    assert int(status.item()) == _lib.STATUS_BAD_PAGE
+    assert not k[1, 6:8].any() and not v[1, 6:8].any() and k[1, 5].any() and k[1, 8].any()
+    with pytest.raises(IndexError):                            # single-request read past the table
+        pages.read(torch.arange(3), 7)
+    before = pool.clone()
+    with pytest.raises(IndexError):                            # append: nothing written for the bad rows
+        pages.append(torch.tensor([1, -51]), 0, k[:1, None, :4], v[:1, None, :4])
+    assert torch.equal(pool[2:], before[2:]) and torch.equal(pool[0], before[0])
+    raw = RawPages(torch.zeros(6, 4, 2, 2, 8, dtype=torch.bfloat16, device=device))
+    with pytest.raises(IndexError):
+        raw.read(torch.tensor([0, 6]), 0, 8)
+    assert raw.read(torch.tensor([0, -6]), 0, 8)[0].shape == (1, 2, 8, 8)
 
 
 def test_raw_pages_serving_shape_batched(device):

@@ -158,3 +158,43 @@ def test_down_projection_into_pages_equals_project_then_append(device, layout_ar
     kernels.down_project_to_pages(x, wv, got, table, layout, start, 'v', rows, blocks=blocks)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize('layout_args', [(16, 8, 256, 256, 1024), (480, 8, 256, 256, 1024)])
+def test_negative_entries_wrap_and_index_errors_are_reported(device, layout_args):
+    """Table entries follow torch's indexing rules (the reference reads the
+    pages with pages[page, column], paged_cache.py:60-73): an entry in
+    [-n, 0) is page entry + n -- bit-identical output to the positive ids --
+    and an entry outside [-n, n) that a beacon needs raises IndexError, or,
+    given a status word, is reported there (garbage past the beacons a
+    sequence has is never read, as every other test here checks)."""
+    from slimkv_amd import _lib, kernels
+    lengths = [700, 37, 0, 121]
+    c = _case(device, layout_args, lengths, [9, 17, 3, 40], seed=91)
+    scale = D ** -0.5
+    args = (c['q'], c['raw_k'], c['raw_v'], c['pages'])
+    kw = dict(block_diagonal=True, raw_lengths=c['raw_lengths'], lat_splits=4)
+
+    def run(table, **extra):
+        return kernels.paged_latent_decode(*args, table, c['lengths'], c['lat_keys'], c['layout'], c['up_k'],
+                                           c['up_v'], scale, **kw, **extra)
+    want = run(c['tables'])
+    pool = c['pages'].shape[0]
+    slots = c['layout'].slots
+    neg = c['tables'].clone()
+    for b, n in enumerate(lengths):
+        used = (n + slots - 1) // slots
+        neg[b, :used:2] -= pool                                # every other page by its negative id
+    got = run(neg)
+    torch.cuda.synchronize()
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    bad = c['tables'].clone()
+    bad[3, (120 // slots)] = pool                              # the page of beacon 120 of sequence 3
+    with pytest.raises(IndexError):
+        run(bad)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    run(bad, status=status)
+    assert int(status.item()) == _lib.STATUS_BAD_PAGE
+    status.zero_()
+    run(neg, status=status)
+    assert int(status.item()) == 0
