@@ -141,11 +141,11 @@ def run_layer(kernels, L, rows, scale, workspace, stages=7):
                           out=L['out'], lse=L['lse'], workspace=workspace, stages=stages)
 
 
-def cpu_baseline(torch, layer, cos, sin, scale, budget_s=(10.0, 30.0)):
-    """Time the torch fp32 eager restatement of the reference path on the host."""
+def cpu_baseline(torch, layer, cos, sin, scale):
+    """The torch fp32 eager restatement of the reference decode path on the
+    host: one full-shape layer, at every host thread and at one thread."""
+    from bench_workloads import cpu_baseline as timed
     from oracle import eager_torch
-    threads = int(os.environ.get('OMP_NUM_THREADS', '0')) or len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
     from slimkv_amd import kernels
     q_rot, _ = kernels.rope_decode(layer['q'].transpose(1, 2), layer['raw_k'].transpose(1, 2)[:, :, :1].contiguous(),
                                    cos, sin, layer['q_pos'], None, 0, 0)
@@ -156,24 +156,10 @@ def cpu_baseline(torch, layer, cos, sin, scale, budget_s=(10.0, 30.0)):
     def once():
         return eager_torch.latent_layer(q_cpu, cpu['raw_k'], cpu['raw_v'], lat_k, lat_v, cpu['up_k'], cpu['up_v'],
                                         scale, HKV)
-
-    once()
-    times = []
-    start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        once()
-        times.append(time.perf_counter() - t0)
-        elapsed = time.perf_counter() - start
-        if (elapsed >= budget_s[0] and len(times) >= 5) or elapsed >= budget_s[1]:
-            break
-    times.sort()
-    median = times[len(times) // 2]
     rk = layer['rank']
-    return {'value': round(layer_bytes(rk, rk) / median / 1e9, 3), 'unit': 'GB/s', 'cores': threads,
-            'kind': 'port', 'ms_per_layer': round(median * 1e3, 2),
-            'sample': f'one full-shape rank-{rk} layer (B16, 8192 beacons, 133 raw), torch fp32 eager '
-                      f'restatement, {len(times)} runs in {elapsed:.1f}s, median'}
+    return timed(torch, once, layer_bytes(rk, rk), 'GB/s', 1e9,
+                 f'one full-shape rank-{rk} layer (B16, 8192 beacons, 133 raw), torch fp32 eager restatement of the '
+                 f'reference decode')
 
 
 def main():
@@ -185,10 +171,11 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-graph', action='store_true', help='time eager launches instead of graph replay')
-    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged', 'b1'),
+    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged', 'b1', 'ceiling'),
                     help='latent: the headline decode sweep; prefill / recon / paged: the window prefill, '
                          'reconstruction decode and paged-cache decode workloads; b1: batch-1 ms per token '
-                         'at the contexts the reference publishes')
+                         'at the contexts the reference publishes; ceiling: the HBM read rate a plain '
+                         'stream reaches on this GPU')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) > 1:
         print('bench.py measures one GPU: the decode path shards by sequence with no exchange, '
@@ -295,6 +282,11 @@ def main():
         torch.cuda.synchronize()
         durations[r] = [a.elapsed_time(b) * 1e-3 / (PROFILE_REPLAYS * len(group))]
     del stage_ws
+    # The read rate a plain grid-stride stream reaches on this GPU (the
+    # slimkv_probe_stream_read ceiling probe), to read the split kernel's rate
+    # against beside the 8 TB/s peak.
+    from bench_workloads import ceiling_probe
+    _, ceiling = ceiling_probe(torch, device)
     dom = 32 if 32 in durations else max(durations, key=lambda r: len(durations[r]))
     dur = durations[dom]
     dur_avg = sum(dur) / len(dur)
@@ -306,6 +298,9 @@ def main():
                 'kernel': f'split_kernel (rank-{dom} layers)',
                 'avg_us': round(dur_avg * 1e6, 2),
                 'split_kernel_sweep_frac': round(all_split / (elapsed / args.steps), 3),
+                'ceiling': {'plain_gbps': ceiling['plain'], 'nt_gbps': ceiling['nt'],
+                            'frac_of_plain': round(achieved / ceiling['plain'], 4),
+                            'source': 'slimkv_probe_stream_read over 4 GiB, best configuration, same run'},
                 'avg_us_by_rank': {str(r): round(sum(v) / len(v) * 1e6, 2) for r, v in sorted(durations.items())}}
 
     result = {

@@ -26,6 +26,7 @@ import time
 
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+_STAGE_PROLOGUE, _STAGE_ATTEND, _STAGE_ALL = 1, 2, 7      # SLIMKV_STAGE_* of include/slimkv_hip.h
 
 
 def _events(torch):
@@ -47,6 +48,87 @@ def _replays(torch, step, count=50):
     """Median of `count` single steps bracketed by HIP events, and the clocks."""
     from bench import gpu_clocks, replay_median_ms
     return {'count': count, 'median_ms': round(replay_median_ms(torch, step, count), 4)}, gpu_clocks()
+
+
+def cpu_info():
+    """Host CPU model and the threads this process may use."""
+    model = None
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {'model': model, 'threads_available': len(os.sched_getaffinity(0))}
+
+
+def _time_cpu(torch, fn, threads, budget_s):
+    """Median seconds of `fn` at `threads` host threads: one warm-up, then at
+    least 5 runs or until budget_s[0] seconds, at most budget_s[1]."""
+    torch.set_num_threads(threads)
+    fn()
+    times = []
+    start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        elapsed = time.perf_counter() - start
+        if (elapsed >= budget_s[0] and len(times) >= 5) or elapsed >= budget_s[1]:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times), elapsed
+
+
+def cpu_baseline(torch, fn, work, unit, scale, sample, budget_s=(8.0, 20.0)):
+    """The reference's path restated on the host (the oracle's torch fp32
+    port), timed at every available thread and at one thread (the reference
+    CI's setting): value = work / median seconds / scale in `unit`."""
+    threads = int(os.environ.get('OMP_NUM_THREADS', '0')) or len(os.sched_getaffinity(0))
+    med, runs, elapsed = _time_cpu(torch, fn, threads, budget_s)
+    med1, runs1, elapsed1 = _time_cpu(torch, fn, 1, (budget_s[0] / 2, budget_s[1] / 2))
+    torch.set_num_threads(threads)
+    return {'value': round(work / med / scale, 4), 'unit': unit, 'cores': threads, 'kind': 'port',
+            'sample': f'{sample}; median of {runs} runs in {elapsed:.1f}s',
+            'ms_per_run': round(med * 1e3, 2),
+            'one_thread': {'value': round(work / med1 / scale, 4), 'cores': 1, 'ms_per_run': round(med1 * 1e3, 2),
+                           'runs': runs1},
+            'cpu': cpu_info()}
+
+
+def staged_attend_seconds(torch, calls, stage_prologue, stage_attend, replays=20):
+    """Per-launch seconds of the attend stage (the split-K kernel): every call's
+    prologue stage runs once, then the attend stages of all calls -- each on
+    its own buffers and workspace -- are captured back to back in one graph
+    and timed with HIP events over `replays` replays."""
+    for call in calls:
+        call(stage_prologue)
+    torch.cuda.synchronize()
+
+    def sweep():
+        for call in calls:
+            call(stage_attend)
+    sweep()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sweep()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sweep()
+    for _ in range(3):
+        graph.replay()
+    a, b = _events(torch)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(replays):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3 / (replays * len(calls))
 
 
 def _result(metric, value, unit, args, seconds, dtype, config, **extra):
@@ -142,9 +224,8 @@ def prefill(args):
 
 def _prefill_cpu(torch, q, k, v, n, scale, flops):
     """Reference eager semantics in fp32 on the host for window 1 (torch
-    restatement of the causal attention)."""
-    threads = int(os.environ.get('OMP_NUM_THREADS', '0')) or len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
+    restatement of the causal attention: 1280 queries over 1540 keys, b4,
+    32/8 heads)."""
     qc = q.float().cpu().transpose(1, 2)                       # [B, H, L, D]
     kc = k[:, :n].float().cpu().transpose(1, 2)
     vc = v[:, :n].float().cpu().transpose(1, 2)
@@ -152,13 +233,14 @@ def _prefill_cpu(torch, q, k, v, n, scale, flops):
     kc, vc = kc.repeat_interleave(g, 1), vc.repeat_interleave(g, 1)
     L = qc.shape[2]
     mask = torch.arange(n)[None, :] > (torch.arange(L)[:, None] + n - L)
-    t0 = time.perf_counter()
-    s = (qc @ kc.transpose(-1, -2)) * scale
-    s.masked_fill_(mask, float('-inf'))
-    torch.softmax(s, -1) @ vc
-    dt = time.perf_counter() - t0
-    return {'value': round(flops / dt / 1e12, 4), 'unit': 'TFLOP/s', 'cores': threads, 'kind': 'port',
-            'sample': f'window 1 (1280 queries x {n} keys, b4, 32 heads), torch fp32 eager, one run {dt:.1f}s'}
+
+    def run():
+        s = (qc @ kc.transpose(-1, -2)) * scale
+        s.masked_fill_(mask, float('-inf'))
+        return torch.softmax(s, -1) @ vc
+    return cpu_baseline(torch, run, flops, 'TFLOP/s', 1e12,
+                        f'window 1 (1280 queries x {n} keys, b4, 32 heads), torch fp32 eager causal attention',
+                        budget_s=(5.0, 15.0))
 
 
 # ----------------------------------------------------------------------------- reconstruction decode
@@ -206,11 +288,14 @@ def recon(args):
     qpos, bpos = recon_positions(torch, dev)
     scale = D ** -0.5
 
+    def call(L, stages=_STAGE_ALL, workspace=None):
+        kernels.recon_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'],
+                             scale, beacon_positions=bpos, block_diagonal=True, q_positions=qpos, cos=cos,
+                             sin=sin, out=L['out'], stages=stages, workspace=workspace)
+
     def step():
         for L in layers:
-            kernels.recon_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'],
-                                 scale, beacon_positions=bpos, block_diagonal=True, q_positions=qpos, cos=cos,
-                                 sin=sin, out=L['out'])
+            call(L)
 
     seconds = _time_steps(torch, step, args.steps, args.warmup)
     replays, clocks = _replays(torch, step)
@@ -220,16 +305,57 @@ def recon(args):
     # 4 * B * NB * HKV * D * 2 bytes per layer.
     per_layer = B * (NB * 2 * R * 2 + RAW * HKV * D * 2 * 2 + 2 * HQ * D * 2) + 2 * HKV * D * R * 2
     gbps = per_layer * LAYERS / seconds / 1e9
-    # up-projection MFMA work done inside the kernel: 2 * 128 * r flops per beacon per KV head
-    recon_tflops = B * NB * HKV * 2 * D * r * LAYERS / seconds / 1e12
-    return _result('reconstruction decode GB/s, Qwen2.5-14B layer shape b8 ctx32K t4', gbps, 'GB/s', args, seconds,
-                   'bf16', {'workload': 'reconstruction decode, 8-layer sweep, 40/8 heads, rank 32, beacon K-RoPE, '
-                                        'K rebuilt per tile in the attention kernel',
-                            'batch': B, 'beacons': NB, 'raw_tokens': RAW},
-                   hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), us_per_layer=round(seconds / LAYERS * 1e6, 2),
-                   bytes_per_layer=per_layer, reconstruction_tflops=round(recon_tflops, 2),
-                   materialising_bytes_per_layer=per_layer + 4 * B * NB * HKV * D * 2, replays=replays,
-                   clocks=clocks)
+    # MFMA work of the split kernel per layer: the K rebuild (2 * 128 * r flops
+    # per beacon per KV head), the scores (2 * 128 per beacon per query head)
+    # and the latent P.V (2 * r per beacon per query head)
+    rebuild_flop = B * NB * HKV * 2 * D * r
+    attend_flop = B * NB * HQ * 2 * (D + r) + B * RAW * HQ * 4 * D
+    # the split kernel reads the latents, the raw rows, q and U_K once
+    split_bytes = B * (NB * 2 * R * 2 + RAW * HKV * D * 2 * 2 + HQ * D * 2) + HKV * D * R * 2
+    ws = [torch.empty(64 << 20, dtype=torch.uint8, device=dev) for _ in layers]
+    attend_s = staged_attend_seconds(torch, [lambda st, L=L, w=w: call(L, st, w) for L, w in zip(layers, ws)],
+                                     _STAGE_PROLOGUE, _STAGE_ATTEND)
+    del ws
+    achieved = split_bytes / attend_s / 1e9
+    mfma_tflops = (rebuild_flop + attend_flop) / attend_s / 1e12
+    result = _result('reconstruction decode GB/s, Qwen2.5-14B layer shape b8 ctx32K t4', gbps, 'GB/s', args, seconds,
+                     'bf16', {'workload': 'reconstruction decode, 8-layer sweep, 40/8 heads, rank 32, beacon K-RoPE, '
+                                          'K rebuilt per tile in the attention kernel',
+                              'batch': B, 'beacons': NB, 'raw_tokens': RAW},
+                     hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), us_per_layer=round(seconds / LAYERS * 1e6, 2),
+                     bytes_per_layer=per_layer,
+                     roofline={'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+                               'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
+                               'kernel': 'recon_split_kernel (attend stage)', 'avg_us': round(attend_s * 1e6, 2),
+                               'bytes_per_launch': split_bytes,
+                               'mfma': {'achieved': round(mfma_tflops, 2), 'peak': MFMA_BF16_PEAK_TFLOPS,
+                                        'unit': 'TFLOP/s', 'frac': round(mfma_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                                        'flop_per_launch': rebuild_flop + attend_flop}},
+                     materialising_bytes_per_layer=per_layer + 4 * B * NB * HKV * D * 2, replays=replays,
+                     clocks=clocks)
+    if not args.no_cpu:
+        result['cpu_baseline'] = _recon_cpu(torch, layers[0], cos, sin, qpos, bpos, scale, per_layer)
+    return result
+
+
+def _recon_cpu(torch, L, cos, sin, qpos, bpos, scale, per_layer):
+    """The reference's reconstruction route (materialise K/V from the latents,
+    RoPE the rebuilt K at its slot positions, fp32 softmax attention) in torch
+    fp32 on the host, one full-shape layer (B8, 8192 beacons, 40/8 heads)."""
+    from oracle import eager_torch
+    c = RECON_SHAPE
+    f = lambda x: x.float().cpu()
+    p = int(qpos[0, 0])
+    q = f(L['q']).transpose(1, 2)
+    cq, sq = f(cos[p]), f(sin[p])
+    q_rot = eager_torch.rotate(q, cq, sq)
+    bp = bpos[0].cpu()
+    cos_rows, sin_rows = f(cos[bp]), f(sin[bp])
+    args = (q_rot, f(L['raw_k']), f(L['raw_v']), f(L['lat_k']), f(L['lat_v']), f(L['up_k']), f(L['up_v']), scale,
+            c['HKV'], cos_rows, sin_rows)
+    return cpu_baseline(torch, lambda: eager_torch.recon_layer(*args), per_layer, 'GB/s', 1e9,
+                        'one full-shape layer (B8, 8192 beacons, 133 raw, 40/8 heads), torch fp32 reconstruction '
+                        'route (rebuild, beacon K-RoPE, attention)')
 
 
 # ----------------------------------------------------------------------------- paged decode
@@ -317,31 +443,149 @@ def paged(args):
         gather()
         decode()
 
+    def paged_call(stages=_STAGE_ALL, workspace=None):
+        kernels.paged_latent_decode(q, raw_k.transpose(1, 2), raw_v.transpose(1, 2), pool, tables, lat_len, max_nb,
+                                    layout, up_k, up_v, scale, rows_total=sum(nb), block_diagonal=True,
+                                    raw_lengths=raw_len, out=out, status=status, stages=stages, workspace=workspace)
+
     def direct_step():
         # raw rows (sinks + tail) still come out of their pages into a small dense
         # buffer; the beacon rows are read by the decode straight from the pages
         kernels.raw_pages(raw.pages, raw_tables, raw_k, raw_v, start=0, count=max_raw, to_pages=False,
                           lengths=raw_len, status=status)
-        kernels.paged_latent_decode(q, raw_k.transpose(1, 2), raw_v.transpose(1, 2), pool, tables, lat_len, max_nb,
-                                    layout, up_k, up_v, scale, rows_total=sum(nb), block_diagonal=True,
-                                    raw_lengths=raw_len, out=out, status=status)
+        paged_call()
 
     seconds = _time_steps(torch, direct_step, args.steps, args.warmup)
     replays, clocks = _replays(torch, direct_step)
     restore_s = _time_steps(torch, restore_step, args.steps, args.warmup)
     decode_s = _time_steps(torch, decode, args.steps, args.warmup)
+    # the split kernel alone (attend stage): the pool (2.4 GB) is far larger
+    # than the MALL, so back-to-back launches over it read HBM
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    attend_s = staged_attend_seconds(torch, [lambda st: paged_call(st, ws)] * 4, _STAGE_PROLOGUE, _STAGE_ATTEND)
+    del ws
     kernels.check_status(status)
     algo = sum(n * 2 * R * 2 + c * HKV * D * 2 * 2 for n, c in zip(nb, raw_count)) + NSEQ * 2 * HQ * D * 2 \
         + 2 * HKV * D * R * 2
+    split_bytes = sum(n * 2 * R * 2 + c * HKV * D * 2 * 2 for n, c in zip(nb, raw_count)) + NSEQ * HQ * D * 2 \
+        + HKV * D * R * 2
     gbps = algo / seconds / 1e9
-    return _result('paged latent decode GB/s, 64 seqs ctx U[1K,128K] t8', gbps, 'GB/s', args, seconds, 'bf16',
-                   {'workload': 'paged decode: beacon rows read from the pages by the fused latent decode, '
-                                'raw rows gathered, t8, rank 32',
-                    'sequences': NSEQ, 'page_layout': [16, RATIO, R, R, HKV * D], 'pool_pages': POOL,
-                    'beacons_total': sum(nb)},
-                   hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), bytes_per_step=algo,
-                   restore_path_gbps=round(algo / restore_s / 1e9, 1), restore_path_ms=round(restore_s * 1e3, 4),
-                   dense_decode_only_gbps=round(algo / decode_s / 1e9, 1), replays=replays, clocks=clocks)
+    achieved = split_bytes / attend_s / 1e9
+    result = _result('paged latent decode GB/s, 64 seqs ctx U[1K,128K] t8', gbps, 'GB/s', args, seconds, 'bf16',
+                     {'workload': 'paged decode: beacon rows read from the pages by the fused latent decode, '
+                                  'raw rows gathered, t8, rank 32',
+                      'sequences': NSEQ, 'page_layout': [16, RATIO, R, R, HKV * D], 'pool_pages': POOL,
+                      'beacons_total': sum(nb)},
+                     hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), bytes_per_step=algo,
+                     roofline={'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+                               'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
+                               'kernel': 'split_kernel<KA,8,paged> (attend stage)', 'avg_us': round(attend_s * 1e6, 2),
+                               'bytes_per_launch': split_bytes},
+                     restore_path_gbps=round(algo / restore_s / 1e9, 1), restore_path_ms=round(restore_s * 1e3, 4),
+                     dense_decode_only_gbps=round(algo / decode_s / 1e9, 1), replays=replays, clocks=clocks)
+    if not args.no_cpu:
+        result['cpu_baseline'] = _paged_cpu(torch, pc, raw_k, raw_v, scale)
+    return result
+
+
+def _paged_cpu(torch, pc, raw_k, raw_v, scale, sample=4):
+    """restore_memory's gather (BeaconPages._indices + advanced indexing,
+    paged_cache.py:60-73) and the eager latent decode (fa2_decode.py:143-164 in
+    fp32) on the host, for the `sample` sequences of median length; their
+    pages are copied to a host pool first (table entries renumbered)."""
+    import numpy as np
+    from oracle import eager_torch
+    from oracle import paged as opaged
+    c = PAGED_SHAPE
+    layout = pc['layout']
+    olayout = opaged.Layout(layout.raw_block_size, layout.token_ratio, layout.key_rank, layout.value_rank,
+                            layout.raw_width)
+    nb = pc['nb']
+    order = sorted(range(len(nb)), key=lambda b: nb[b])
+    picks = order[len(nb) // 2 - sample // 2:len(nb) // 2 - sample // 2 + sample]
+    tables = pc['tables_cpu']
+    seqs = []
+    for b in picks:
+        used = (nb[b] + layout.slots - 1) // layout.slots
+        host_pool = pc['pool'][tables[b, :used].to(pc['pool'].device)].float().cpu()
+        seqs.append((b, nb[b], host_pool, np.arange(used, dtype=np.int64)))
+    up_k, up_v = pc['up_k'].float().cpu(), pc['up_v'].float().cpu()
+    q = pc['q'].float().cpu().transpose(1, 2)                       # [B, H, 1, D]
+    rk, rv = raw_k.float().cpu().transpose(1, 2), raw_v.float().cpu().transpose(1, 2)
+    width = torch.arange(layout.width)
+
+    def run():
+        for b, n, host_pool, table in seqs:
+            page, first = opaged.beacon_indices(olayout, table, 0, n)
+            rows = host_pool[torch.from_numpy(page)[:, None], torch.from_numpy(first)[:, None] + width[None]]
+            lk, lv = rows[:, :layout.key_rank], rows[:, layout.key_rank:]
+            m = pc['raw_count'][b]
+            eager_torch.latent_layer(q[b:b + 1], rk[b:b + 1, :m], rv[b:b + 1, :m], lk[None, :, None],
+                                     lv[None, :, None], up_k, up_v, scale, c['HKV'])
+    work = sum(n * 2 * layout.width + pc['raw_count'][b] * c['HKV'] * c['D'] * 2 * 2 for b, n, _, _ in seqs)
+    return cpu_baseline(torch, run, work, 'GB/s', 1e9,
+                        f'{sample} sequences of median length ({", ".join(str(nb[b]) for b in picks)} beacons): '
+                        f'page gather + torch fp32 eager latent decode')
+
+
+# ----------------------------------------------------------------------------- HBM ceiling
+
+CEILING_CONFIGS = [(4, 8), (8, 4), (16, 1), (16, 2), (32, 1)]     # (resident waves per CU, loads in flight)
+
+
+def ceiling_probe(torch, dev, gib=4, reps=10):
+    """Read rate of slimkv_probe_stream_read over a `gib` GiB buffer (far past
+    the 256 MB MALL) for each (waves per CU, loads in flight) configuration,
+    plain and non-temporal loads: {config: GB/s} and the best of each kind."""
+    import ctypes
+    from slimkv_amd import _lib
+    nbytes = gib << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(cu * 64 * 64, dtype=torch.int32, device=dev)
+    lib = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    rates = {}
+    for nt in (0, 1):
+        for waves, depth in CEILING_CONFIGS:
+            def launch():
+                _lib.check(lib.slimkv_probe_stream_read(ctypes.c_void_p(buf.data_ptr()), nbytes,
+                                                        ctypes.c_void_p(sink.data_ptr()), sink.numel(), waves,
+                                                        depth, nt, stream))
+            for _ in range(3):
+                launch()
+            a, b = _events(torch)
+            a.record()
+            for _ in range(reps):
+                launch()
+            b.record()
+            torch.cuda.synchronize()
+            rates[f"{'nt' if nt else 'plain'}_w{waves}_d{depth}"] = round(nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9, 1)
+    del buf
+    best = {kind: max(v for k, v in rates.items() if k.startswith(kind)) for kind in ('plain', 'nt')}
+    return rates, best
+
+
+def ceiling(args):
+    """The HBM read ceiling of this GPU: a grid-stride stream of 16-byte loads
+    (slimkv_probe_stream_read) over 4 GiB, the best of several resident-wave /
+    loads-in-flight configurations, plain and non-temporal."""
+    import torch
+    dev = torch.device('cuda:0')
+    t0 = time.perf_counter()
+    rates, best = ceiling_probe(torch, dev)
+    seconds = time.perf_counter() - t0
+    return _result('HBM read ceiling GB/s (grid-stride stream, 4 GiB)', best['plain'], 'GB/s', args, seconds,
+                   'u8', {'workload': 'stream read of a 4 GiB buffer, 16-byte loads',
+                          'configs': [list(c) for c in CEILING_CONFIGS]},
+                   hbm_frac=round(best['plain'] / HBM_PEAK_GBPS, 4), nt_gbps=best['nt'],
+                   nt_frac=round(best['nt'] / HBM_PEAK_GBPS, 4), rates=rates, clocks=_replays_clocks())
+
+
+def _replays_clocks():
+    from bench import gpu_clocks
+    return gpu_clocks()
 
 
 # ----------------------------------------------------------------------------- batch 1
@@ -405,8 +649,7 @@ def b1(args):
         replays, clocks = _replays(torch, graph.replay)
         ms = seconds * 1e3
         per_context[ctx] = {'ms_per_token': round(ms, 4), 'median_ms': replays['median_ms'],
-                            'reference_h20_ms': REFERENCE_B1_MS[ctx],
-                            'reference_over_ours': round(REFERENCE_B1_MS[ctx] / ms, 2)}
+                            'context_reference_h20_ms': REFERENCE_B1_MS[ctx]}
         del layers, ws, graph
         torch.cuda.empty_cache()
 
@@ -442,8 +685,7 @@ def b1(args):
             rec_token()
         rec_ms = _time_steps(torch, rec_graph.replay, args.steps, args.warmup) * 1e3
         per_context[ctx].update(recon_ms_per_token=round(rec_ms, 4),
-                                reference_h20_recon_ms=REFERENCE_B1_RECON_MS[ctx],
-                                recon_reference_over_ours=round(REFERENCE_B1_RECON_MS[ctx] / rec_ms, 2))
+                                context_reference_h20_recon_ms=REFERENCE_B1_RECON_MS[ctx])
         del rec_layers, rec_graph
         torch.cuda.empty_cache()
     first = per_context[32768]
@@ -452,11 +694,13 @@ def b1(args):
                    {'workload': 'batch-1 latent beacon decode, 32 layers per token, Llama-3.1-8B layer shape, '
                                 'per-layer rank drawn from {16, 32, 48}', 'contexts': sorted(REFERENCE_B1_MS),
                     'layer_ranks': ranks},
-                   higher_is_better=False, vs_baseline=round(first['ms_per_token'] / REFERENCE_B1_MS[32768], 4),
+                   higher_is_better=False, vs_baseline=None,
                    per_context={str(k): v for k, v in per_context.items()},
-                   reference_source='README.md:276-280 (H20, attention GPU kernel time per token)',
+                   context_reference_source='README.md:276-284 (H20): context only, not a like-for-like baseline -- '
+                                            'those per-token times include the QKV/O projections and cache '
+                                            'operations, this line times the attention core of 32 layers',
                    clocks=clocks)
 
 
 def run_workload(args):
-    return {'prefill': prefill, 'recon': recon, 'paged': paged, 'b1': b1}[args.workload](args)
+    return {'prefill': prefill, 'recon': recon, 'paged': paged, 'b1': b1, 'ceiling': ceiling}[args.workload](args)

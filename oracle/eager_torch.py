@@ -51,3 +51,26 @@ def latent_layer(q_rot, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, kv_heads)
     total = torch.logaddexp(raw_lse, lat_lse)
     return (torch.exp(raw_lse - total)[..., None] * raw_out.transpose(1, 2)
             + torch.exp(lat_lse - total)[..., None] * lat_out)
+
+
+def rotate(x, cos, sin):
+    """x * cos + rotate_half(x) * sin in fp32 (modeling_utils.py:347-351, 386-389)."""
+    half = x.shape[-1] // 2
+    return x * cos + torch.cat([-x[..., half:], x[..., :half]], dim=-1) * sin
+
+
+def recon_layer(q_rot, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, kv_heads, cos_rows=None, sin_rows=None):
+    """The reconstruction route in fp32 (LlamaAttention.forward after
+    materialize, slimkv/llama3/modeling_llama.py:1405-1483, upcast as the
+    eager softmax does): K = up_k(lat_k), rotated at the beacon positions when
+    cos_rows / sin_rows [Nl, D] are given, V = up_v(lat_v), attention over
+    [beacons ; raw rows].  q_rot [B,H,L,D]; raw_k/raw_v [B,Nr,Hkv,D];
+    lat_k/lat_v [B,Nl,R].  Returns out [B,L,H,D]."""
+    batch, n, _ = lat_k.shape
+    dim = up_k.shape[0] // kv_heads
+    k = (lat_k @ up_k.T).reshape(batch, n, kv_heads, dim)
+    if cos_rows is not None:
+        k = rotate(k, cos_rows[None, :, None], sin_rows[None, :, None])
+    v = (lat_v @ up_v.T).reshape(batch, n, kv_heads, dim)
+    out, _ = eager_forward(q_rot.transpose(1, 2), torch.cat([k, raw_k], dim=1), torch.cat([v, raw_v], dim=1), scale)
+    return out

@@ -199,6 +199,7 @@ SIGNATURES = {
                                                     ctypes.c_size_t, c_ptr]),
     'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
+    'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
 }
 
 ABI_VERSION = 7

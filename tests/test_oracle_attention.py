@@ -235,3 +235,32 @@ def test_eager_recon_layer_without_rounding_equals_grouped_eager_forward():
                                       0.37, causal=True)
     np.testing.assert_allclose(got, want.transpose(0, 2, 1, 3), rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(lse, want_lse, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize('rotate', [False, True])
+def test_torch_recon_restatement_agrees_with_numpy_oracle(rotate):
+    """The fp32 reconstruction route of the CPU baseline against the numpy
+    oracle: reconstruct (no bf16 boundaries), optional rotation at beacon
+    positions, float64 attention over [beacons ; raw rows]."""
+    import torch
+    from oracle import eager_torch
+    from oracle import rope as orope
+    B, H, Hkv, D, Nr, Nl, r = 2, 8, 2, 16, 5, 9, 4
+    q, raw_k, raw_v = rand(B, H, 1, D), rand(B, Nr, Hkv, D), rand(B, Nr, Hkv, D)
+    lat_k, lat_v = rand(B, Nl, Hkv * r), rand(B, Nl, Hkv * r)
+    uk, uv = rand(Hkv * D, Hkv * r), rand(Hkv * D, Hkv * r)
+    cos, sin = orope.tables(64, orope.inv_freq(D, 10000.0))
+    pos = np.arange(3, 3 + Nl)
+    t = lambda x: torch.tensor(np.asarray(x), dtype=torch.float32)
+    got = eager_torch.recon_layer(t(q), t(raw_k), t(raw_v), t(lat_k), t(lat_v), t(uk), t(uv), 0.3, Hkv,
+                                  t(cos[pos]) if rotate else None, t(sin[pos]) if rotate else None)
+    rk = oa.reconstruct(lat_k[:, None], uk, None, Hkv, D, bf16_boundaries=False)     # [B, Hkv, Nl, D]
+    if rotate:
+        half = D // 2
+        c, s = cos[pos].astype(np.float64), sin[pos].astype(np.float64)
+        rk = rk * c + np.concatenate([-rk[..., half:], rk[..., :half]], axis=-1) * s
+    rv = oa.reconstruct(lat_v[:, None], uv, None, Hkv, D, bf16_boundaries=False)
+    k = np.concatenate([rk.transpose(0, 2, 1, 3), raw_k], axis=1)
+    v = np.concatenate([rv.transpose(0, 2, 1, 3), raw_v], axis=1)
+    want, _ = oa.eager_forward(q.transpose(0, 2, 1, 3), k, v, 0.3)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-4, atol=1e-5)
