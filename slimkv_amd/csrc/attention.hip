@@ -63,7 +63,7 @@ struct Seg {
     int32_t* status;
     // Compact schedule: workgroup items enumerate only the non-empty splits of
     // each batch entry (needs seqlens); items past the last one exit at once.
-    int compact, batch;
+    int compact;
 };
 
 struct SplitParams {
@@ -98,11 +98,27 @@ struct TileRegs {
     u32x4 v[KS / 2];
 };
 
-// Loads are branch-free: an invalid piece reads a clamped in-bounds address and
-// is zeroed by a select, so the compiler can count outstanding loads across
-// the software pipeline instead of draining them (vmcnt(0)) at every join.
+// Loads are branch-free: an invalid piece reads a clamped in-bounds address.
+// Pieces that must read as zero are zeroed by a select where they are used,
+// never where they are loaded: a select at the load site would make the
+// compiler wait for the load there (vmcnt) and empty the software pipeline.
 __device__ __forceinline__ u32x4 zero_unless(bool ok, u32x4 v) {
     return u32x4{ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
+}
+
+// Key/value rows are read once per decode step.  Dense tiles of KS k-steps
+// read them with non-temporal loads (gfx950 `nt`) where that measured faster
+// (the rank-32 latent tiles: 30.6 against 32.5 us a C1 layer; wider and
+// narrower tiles and the paged rows ran slower with them).
+template <int KS>
+struct StreamLoads {
+    static constexpr bool value = KS == 4;
+};
+
+template <bool NT>
+__device__ __forceinline__ u32x4 tile_load(const uint16_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    else return *reinterpret_cast<const u32x4*>(p);
 }
 
 
@@ -160,20 +176,17 @@ __device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const RopeRow& t) {
 
 template <int KS>
 __device__ __forceinline__ void load_tile(TileRegs<KS>& t, const uint16_t* kbase, const uint16_t* vbase,
-                                          int64_t k_sn, int64_t v_sn, int r0, int r_end, int last_row,
-                                          int span_k, int span_v, int col, int grp, int lane, bool act) {
+                                          int64_t k_sn, int64_t v_sn, int r0, int last_row,
+                                          int span_k, int span_v, int col, int grp, int lane) {
     constexpr int VT = KS;
     // K: lane (row = col, group grp) takes elements [32c + 8*grp, +8) of the
     // tile's k range for c < KS/2 -- a row's four groups read 64 contiguous bytes.
     {
-        const int row = r0 + col;
-        const bool rv = act && row < r_end;
-        const uint16_t* src = kbase + (int64_t)min(row, last_row) * k_sn;
+        const uint16_t* src = kbase + (int64_t)min(r0 + col, last_row) * k_sn;
 #pragma unroll
         for (int c = 0; c < KS / 2; ++c) {
             const int kk = 32 * c + 8 * grp;
-            const bool ok = rv && kk + 8 <= span_k;
-            t.k[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src + (ok ? kk : 0)));
+            t.k[c] = tile_load<StreamLoads<KS>::value>(src + (kk + 8 <= span_k ? kk : 0));
         }
     }
     // V: 16 rows x 2*VT pieces of 16 bytes; piece p = 64c + lane is row
@@ -183,9 +196,8 @@ __device__ __forceinline__ void load_tile(TileRegs<KS>& t, const uint16_t* kbase
         const int p = 64 * c + lane;
         const int row = r0 + p / (2 * VT);
         const int pc = p % (2 * VT);
-        const bool ok = act && row < r_end && 8 * pc + 8 <= span_v;
-        const uint16_t* src = vbase + (int64_t)min(row, last_row) * v_sn + (ok ? 8 * pc : 0);
-        t.v[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src));
+        const uint16_t* src = vbase + (int64_t)min(row, last_row) * v_sn + (8 * pc + 8 <= span_v ? 8 * pc : 0);
+        t.v[c] = tile_load<StreamLoads<KS>::value>(src);
     }
 }
 
@@ -242,9 +254,8 @@ struct TilePair {
 // whatever the table holds.
 template <int KS>
 __device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages<KS>& pg, const Seg& sg,
-                                                const uint16_t* kpage, const uint16_t* vpage, int r0, int r_end,
-                                                int last_valid, int span_k, int span_v, int col, int grp, int lane,
-                                                bool act) {
+                                                const uint16_t* kpage, const uint16_t* vpage, int r0,
+                                                int last_valid, int span_k, int span_v, int col, int grp, int lane) {
     constexpr int VT = KS;
     auto row_base = [&](int32_t pid, int row) -> int64_t {
         const int r = min(row, last_valid);
@@ -252,14 +263,11 @@ __device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages
         return pid * sg.page_stride + (int64_t)slot * sg.k_sn;
     };
     {
-        const int row = r0 + col;
-        const bool rv = act && row < r_end;
-        const uint16_t* src = kpage + row_base(pg.k, row);
+        const uint16_t* src = kpage + row_base(pg.k, r0 + col);
 #pragma unroll
         for (int c = 0; c < KS / 2; ++c) {
             const int kk = 32 * c + 8 * grp;
-            const bool ok = rv && kk + 8 <= span_k;
-            t.k[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src + (ok ? kk : 0)));
+            t.k[c] = tile_load<false>(src + (kk + 8 <= span_k ? kk : 0));
         }
     }
 #pragma unroll
@@ -267,9 +275,8 @@ __device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages
         const int p = 64 * c + lane;
         const int row = r0 + p / (2 * VT);
         const int pc = p % (2 * VT);
-        const bool ok = act && row < r_end && 8 * pc + 8 <= span_v;
-        const uint16_t* src = vpage + row_base(pg.v[c], row) + (ok ? 8 * pc : 0);
-        t.v[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src));
+        const uint16_t* src = vpage + row_base(pg.v[c], row) + (8 * pc + 8 <= span_v ? 8 * pc : 0);
+        t.v[c] = tile_load<false>(src);
     }
 }
 
@@ -277,9 +284,8 @@ __device__ __forceinline__ void load_tile_paged(TileRegs<KS>& t, const TilePages
 // clamping (a lane's clamped row is at most 15 rows past r0c).
 template <int KS>
 __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& tp, const Seg& sg,
-                                               const uint16_t* kpage, const uint16_t* vpage, int r0, int r_end,
-                                               int last_valid, int span_k, int span_v, int col, int grp, int lane,
-                                               bool act) {
+                                               const uint16_t* kpage, const uint16_t* vpage, int r0,
+                                               int last_valid, int span_k, int span_v, int col, int grp, int lane) {
     constexpr int VT = KS;
     auto row_base = [&](int row) -> int64_t {
         int slot = tp.slot0 + (min(row, last_valid) - tp.r0c);
@@ -288,14 +294,11 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
         return (int64_t)(next ? tp.p1 : tp.p0) * sg.page_stride + (int64_t)slot * sg.k_sn;
     };
     {
-        const int row = r0 + col;
-        const bool rv = act && row < r_end;
-        const uint16_t* src = kpage + row_base(row);
+        const uint16_t* src = kpage + row_base(r0 + col);
 #pragma unroll
         for (int c = 0; c < KS / 2; ++c) {
             const int kk = 32 * c + 8 * grp;
-            const bool ok = rv && kk + 8 <= span_k;
-            t.k[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src + (ok ? kk : 0)));
+            t.k[c] = tile_load<false>(src + (kk + 8 <= span_k ? kk : 0));
         }
     }
 #pragma unroll
@@ -303,9 +306,8 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
         const int p = 64 * c + lane;
         const int row = r0 + p / (2 * VT);
         const int pc = p % (2 * VT);
-        const bool ok = act && row < r_end && 8 * pc + 8 <= span_v;
-        const uint16_t* src = vpage + row_base(row) + (ok ? 8 * pc : 0);
-        t.v[c] = zero_unless(ok, *reinterpret_cast<const u32x4*>(src));
+        const uint16_t* src = vpage + row_base(row) + (8 * pc + 8 <= span_v ? 8 * pc : 0);
+        t.v[c] = tile_load<false>(src);
     }
 }
 
@@ -316,29 +318,38 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
 // PAGED: 0 dense rows, 1 rows through per-lane page ids, 2 rows through the
 // tile's two pages (pages of at least 16 rows).
 template <int KS, int DEPTH, int PAGED = 0>
-__device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int Hq,
+__device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int Lq, int Hq,
                                               float scale_log2, char* lds) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
     constexpr int RS = SplitLds<KS>::RS;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // Everything derived from the wave index is wave-uniform: scalar registers,
+    // and scalar branches for the tile loop (a lane-divergent exit would let
+    // the last tile's prefetch reach the loop header and force a full wait
+    // for outstanding loads at the top of every iteration).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15;
     const int grp = lane >> 4;
 
+    // Wave items: (batch, split, slot) with the slot fastest, kWaves per
+    // workgroup -- the waves of a workgroup read the same key rows (different
+    // heads) of one split, or of consecutive splits when a split has fewer
+    // slots than the workgroup has waves.
     const int slots = sg.hk * sg.tiles;
-    const int groups = (slots + kWaves - 1) / kWaves;
-    int s, sgp, b;
+    const int64_t item = (int64_t)w * kWaves + wave;
+    const int slot = (int)(item % slots);
+    const int64_t split_item = item / slots;
+    int s, b;
     if (sg.compact) {
-        sgp = w % groups;
-        if (!locate_split(w / groups, sg.seqlens, sg.batch, sg.n, sg.rows_per_split, b, s)) return;
+        // wave-uniform: every lane of the wave has the same split_item
+        if (!locate_split((int)split_item, sg.seqlens, B, sg.n, sg.rows_per_split, b, s)) return;
+        b = __builtin_amdgcn_readfirstlane(b);
+        s = __builtin_amdgcn_readfirstlane(s);
     } else {
-        s = w % sg.splits;
-        const int rem = w / sg.splits;
-        sgp = rem % groups;
-        b = rem / groups;
+        s = (int)(split_item % sg.splits);
+        b = (int)(split_item / sg.splits);
+        if (b >= B) return;                  // waves never synchronise, so an idle one may leave
     }
-    const int slot = sgp * kWaves + wave;
-    if (slot >= slots) return;               // waves never synchronise, so an idle one may leave
     const int h = slot / sg.tiles;
     const int t = slot % sg.tiles;
 
@@ -388,15 +399,22 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
     const int r_end = Nb;
     const int vis = min(lim, r_end);
     const int last_row = sg.n - 1;
+    // The splits of sequence b start their walk over their tiles at tile
+    // b * ntile / B and wrap, so the B sequences' concurrent reads sit at
+    // staggered offsets of their rows instead of advancing in step (measured
+    // 1-1.5 us faster a rank-32 layer at one workgroup a CU).
+    const int phase = ntile > 0 ? (int)(((int64_t)b * ntile) / B) : 0;
+    auto tile_row = [&](int it) {
+        const int k = it + phase;
+        return r_begin + (k >= ntile ? k - ntile : k) * r_step;
+    };
 
     const uint16_t* kbase = sg.k + (int64_t)b * sg.k_sb + (int64_t)h * sg.k_sh + k_off;
     const uint16_t* vbase = sg.v + (int64_t)b * sg.v_sb + (int64_t)h * sg.v_sh + v_off;
 
     auto fetch = [&](TileRegs<KS>& tr, int it) {
-        const bool act = it < ntile;
-        const int r0 = act ? r_begin + it * r_step : r_begin;
-        load_tile<KS>(tr, kbase, vbase, sg.k_sn, sg.v_sn, r0, act ? r_end : r_begin, last_row, span_k, span_v,
-                      col, grp, lane, act);
+        const int r0 = it < ntile ? tile_row(it) : r_begin;
+        load_tile<KS>(tr, kbase, vbase, sg.k_sn, sg.v_sn, r0, last_row, span_k, span_v, col, grp, lane);
     };
     // Paged rows: the page ids of a tile are loaded two tiles ahead of its
     // data.  An entry outside the pool that a row of the sequence needs sets
@@ -413,7 +431,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
     const int last_page = PAGED == 2 ? last_valid / sg.slots : 0;
     auto load_pages = [&](auto& pg, int it) {
         const bool act = it < ntile;
-        const int r0 = act ? r_begin + it * r_step : r_begin;
+        const int r0 = act ? tile_row(it) : r_begin;
         if constexpr (PAGED == 2) {
             const int r0c = __builtin_amdgcn_readfirstlane(min(r0, last_valid));
             const int pi = __builtin_amdgcn_readfirstlane(r0c / sg.slots);
@@ -436,14 +454,11 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         }
     };
     auto fetch_paged = [&](TileRegs<KS>& tr, const auto& pg, int it) {
-        const bool act = it < ntile;
-        const int r0 = act ? r_begin + it * r_step : r_begin;
+        const int r0 = it < ntile ? tile_row(it) : r_begin;
         if constexpr (PAGED == 2)
-            load_tile_pair<KS>(tr, pg, sg, kbase, vbase, r0, act ? r_end : r_begin, last_valid, span_k, span_v, col,
-                               grp, lane, act);
+            load_tile_pair<KS>(tr, pg, sg, kbase, vbase, r0, last_valid, span_k, span_v, col, grp, lane);
         else
-            load_tile_paged<KS>(tr, pg, sg, kbase, vbase, r0, act ? r_end : r_begin, last_valid, span_k, span_v,
-                                col, grp, lane, act);
+            load_tile_paged<KS>(tr, pg, sg, kbase, vbase, r0, last_valid, span_k, span_v, col, grp, lane);
     };
     using PageIds = std::conditional_t<PAGED == 2, TilePair, TilePages<KS>>;
     PageIds pcur, poth;
@@ -479,14 +494,19 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
 
     uint16_t* vbuf = reinterpret_cast<uint16_t*>(lds) + wave * 2 * 16 * RS;
 
-    // One 16-key tile: V to LDS, scores, online softmax, P^T V^T.
+    // One 16-key tile: V to LDS, scores, online softmax, P^T V^T.  The tile's
+    // rows past the sequence were read from a clamped row: their scores are
+    // masked below, and their V pieces are zeroed here so that a non-finite
+    // value there cannot reach the product (0 * inf).  K pieces outside the
+    // span meet zero query elements.
     auto consume = [&](const TileRegs<KS>& tile, int it) {
-        const int r0 = r_begin + it * r_step;
+        const int r0 = tile_row(it);
         uint16_t* vb = vbuf + (it & 1) * 16 * RS;
 #pragma unroll
         for (int c = 0; c < VT / 2; ++c) {
             const int p = 64 * c + lane;
-            *reinterpret_cast<u32x4*>(vb + (p / (2 * VT)) * RS + 8 * (p % (2 * VT))) = tile.v[c];
+            *reinterpret_cast<u32x4*>(vb + (p / (2 * VT)) * RS + 8 * (p % (2 * VT))) =
+                zero_unless(r0 + p / (2 * VT) < r_end, tile.v[c]);
         }
         // Two independent accumulation chains halve the MFMA dependency latency.
         v4f sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
@@ -537,35 +557,43 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
         wave_lds_fence();
     };
 
+    // The tile loops run whole rounds of the register ring with no exit inside
+    // a round, then consume the tiles left in the ring: an exit between two
+    // tiles of a round would reach the loop header with that round's
+    // prefetch outstanding and force a full wait for loads there.
     if constexpr (PAGED) {
         TileRegs<KS> other;
-        for (int it = 0; it < ntile; it += 2) {
+        for (int it = 0; it + 1 < ntile; it += 2) {
             fetch_paged(other, poth, it + 1);
             load_pages(poth, it + 3);
             consume(cur, it);
-            if (it + 1 >= ntile) break;
             fetch_paged(cur, pcur, it + 2);
             load_pages(pcur, it + 4);
             consume(other, it + 1);
         }
+        if (ntile & 1) consume(cur, ntile - 1);
     } else if constexpr (DEPTH > 1) {
         // A ring of DEPTH register tiles: the loads of the next DEPTH - 1
         // tiles stay in flight while a tile is consumed (the ring index is
         // static in the unrolled body, so no register copies).  Loads past the
-        // last tile are issued anyway (clamped, zeroed) to keep the
-        // outstanding-load count uniform.
+        // last tile are issued anyway (clamped) to keep the outstanding-load
+        // count uniform; they are never consumed.
         TileRegs<KS> ring[DEPTH];
         ring[0] = cur;
 #pragma unroll
         for (int d = 1; d < DEPTH - 1; ++d) fetch(ring[d], d);
-        for (int it = 0; it < ntile; it += DEPTH) {
+        const int nfull = ntile - ntile % DEPTH;
+        for (int it = 0; it < nfull; it += DEPTH) {
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
                 fetch(ring[(d + DEPTH - 1) % DEPTH], it + d + DEPTH - 1);
                 consume(ring[d], it + d);
-                if (it + d + 1 >= ntile) break;
             }
         }
+        // ring[d] holds tile nfull + d for d < DEPTH - 1
+#pragma unroll
+        for (int d = 0; d < DEPTH - 1; ++d)
+            if (nfull + d < ntile) consume(ring[d], nfull + d);
     } else {
         for (int it = 0; it < ntile; ++it) {
             if (it) fetch(cur, it);
@@ -608,7 +636,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int Lq, int 
 // workgroups stream.
 template <int KA>
 struct SplitWaves {
-    static constexpr int value = KA <= 4 ? 4 : (KA <= 6 ? 3 : 1);
+    static constexpr int value = KA <= 4 ? 4 : (KA <= 6 ? 3 : (KA <= 12 ? 2 : 1));
 };
 
 // Register tiles in flight per latent wave (2 = ping-pong).
@@ -626,12 +654,12 @@ split_kernel(SplitParams prm) {
     int w = blockIdx.x;
     if constexpr (KB > 0) {
         if (w < prm.seg[1].nwg) {
-            split_segment<KB, 1>(prm.seg[1], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+            split_segment<KB, 1>(prm.seg[1], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
             return;
         }
         w -= prm.seg[1].nwg;
     }
-    split_segment<KA, SplitDepth<KA>::value, PAGED>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+    split_segment<KA, SplitDepth<KA>::value, PAGED>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -938,7 +966,7 @@ recon_split_kernel(SplitParams prm, ReconSeg rs) {
     __shared__ __attribute__((aligned(16))) char lds[LA > LB ? LA : LB];
     int w = blockIdx.x;
     if (w < prm.seg[0].nwg) {
-        split_segment<8, false>(prm.seg[0], w, prm.Lq, prm.Hq, prm.scale_log2, lds);
+        split_segment<8, 1>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
         return;
     }
     w -= prm.seg[0].nwg;
@@ -1581,6 +1609,12 @@ struct SegPlan {
     int tiles, cols, splits, rows_per_split, nwg, wown, ks;
 };
 
+// Workgroups covering B * splits * slots wave items, kWaves per workgroup.
+int wave_item_groups(int B, int splits, int slots) {
+    const int64_t items = (int64_t)B * splits * slots;
+    return (int)((items + kWaves - 1) / kWaves);
+}
+
 // Split the key range so the launch holds a few workgroups per CU.
 SegPlan plan_segment(int B, int hk, int P, int cols, int n, int span_k, int wown, int req_splits,
                      int target_wg) {
@@ -1589,11 +1623,13 @@ SegPlan plan_segment(int B, int hk, int P, int cols, int n, int span_k, int wown
     sp.tiles = (P + sp.cols - 1) / sp.cols;
     sp.ks = round_even_tile(span_k);
     sp.wown = wown;
-    const int groups = B * ((hk * sp.tiles + kWaves - 1) / kWaves);
+    // workgroups per split index: kWaves wave items (slots) per workgroup
+    const int64_t slot_items = (int64_t)B * hk * sp.tiles;
     int splits = req_splits;
     if (splits <= 0) {
         const int max_by_rows = std::max(1, (n + 15) / 16);
-        splits = std::max(1, std::min(max_by_rows, (target_wg + groups - 1) / groups));
+        const int64_t fit = ((int64_t)target_wg * kWaves + slot_items - 1) / slot_items;
+        splits = (int)std::max<int64_t>(1, std::min<int64_t>(max_by_rows, fit));
         splits = std::min(splits, kMaxSplits);
     }
     splits = std::min(splits, kMaxSplits);
@@ -1602,7 +1638,7 @@ SegPlan plan_segment(int B, int hk, int P, int cols, int n, int span_k, int wown
     splits = std::max(1, (n + rps - 1) / rps);
     sp.splits = splits;
     sp.rows_per_split = rps;
-    sp.nwg = groups * splits;
+    sp.nwg = wave_item_groups(B, splits, hk * sp.tiles);
     return sp;
 }
 
@@ -1874,7 +1910,8 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
         return worst;
     };
     // Eight packed rows per tile: 32 heads give four tiles, one per wave of a
-    // workgroup, all streaming the same latent rows.
+    // workgroup, all streaming the same latent rows.  (Sixteen rows -- four KV
+    // heads a wave -- measured no faster at rank 16 and slower at rank 48.)
     const int cols = 8;
     const int span = span_of(cols);
     const int lat_ks = round_even_tile(span);
@@ -1882,11 +1919,20 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     const int64_t nl = std::max<int64_t>(a->lat_keys, 1);
     const int has_lat = a->lat_keys > 0;
     const int slots = cu * split_occupancy(has_lat ? lat_ks : 8, has_lat ? 8 : 0);
-    // Raw workgroups sit first in the grid; the latent splits fill the remaining
-    // resident slots so every workgroup starts in the first wave of residency.
-    const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
+    // Raw rows: splits of three 16-row tiles.
+    const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 47) / 48);
     const int raw_wg = (int)B * ((int)(Hkv + kWaves - 1) / kWaves) * raw_req0;
-    int lat_target = std::max(slots - raw_wg, slots / 2);
+    // Dense rows: a whole number of latent workgroups per CU.  Each CU streams
+    // its workgroups' rows at about the same rate, so a launch whose
+    // workgroups do not spread evenly over the CUs lasts as long as its most
+    // loaded CU (rank-32 layer, B16: 16 splits = 256 workgroups, one a CU,
+    // 25.4 us; 18 splits 34.4 us; 43 splits filling the resident slots
+    // 30.6 us).  Tiles of 64 latent columns and wider take one workgroup a CU,
+    // narrower ones two.
+    int lat_target = cu * (lat_ks <= 2 ? 2 : 1);
+    // Paged rows (compact schedule): the splits of all sequences fill the
+    // resident slots left by the raw workgroups.
+    int fill_target = std::max(slots - raw_wg, slots / 2);
     // Keep the latent split count within the fast combine's reach (one latent
     // partial register pass, and one split per combine thread with the raw
     // ones): at small batches the slots would otherwise fill with ever shorter
@@ -1895,26 +1941,33 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     int fast_cap = kMaxSplits;
     if (wown % 8 == 0 && wown <= kFastLatW)
         fast_cap = std::max(1, std::min(fast_lat_splits(wown, 256), 256 - raw_req0));
-    const int lat_groups = (int)B * ((((P + cols - 1) / cols) + kWaves - 1) / kWaves);
-    if (a->lat_splits <= 0) lat_target = std::min<int64_t>(lat_target, (int64_t)lat_groups * fast_cap);
-    p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, a->lat_splits, lat_target);
+    // workgroups per latent split index (a wave per column tile)
+    const int64_t lat_tiles = (int64_t)B * ((P + cols - 1) / cols);
+    if (a->lat_splits <= 0) {
+        lat_target = (int)std::min<int64_t>(lat_target, (lat_tiles * fast_cap + kWaves - 1) / kWaves);
+        fill_target = (int)std::min<int64_t>(fill_target, (lat_tiles * fast_cap + kWaves - 1) / kWaves);
+    }
+    // Whole workgroups per CU: round the split count down, never up.
+    int lat_req = a->lat_splits;
+    if (lat_req <= 0 && !pg)
+        lat_req = (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplits, (int64_t)lat_target * kWaves / lat_tiles));
+    p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, lat_req, lat_target);
     if (pg && a->lat_splits <= 0) {
         // Compact schedule: size the splits from the total row count so the
         // non-empty splits of all sequences fill the resident slots once.
         const int64_t total = pg->rows_total > 0 ? pg->rows_total : B * nl;
-        int64_t rps = (total + lat_target - 1) / lat_target;
+        int64_t rps = (total + fill_target - 1) / fill_target;
         rps = std::max<int64_t>(rps, (nl + std::min(kMaxSplits, fast_cap) - 1) / std::min(kMaxSplits, fast_cap));
         rps = std::max<int64_t>(16, (rps + 15) / 16 * 16);
-        const int groups = p->lat.nwg / p->lat.splits;
         p->lat.rows_per_split = (int)rps;
         p->lat.splits = (int)((nl + rps - 1) / rps);
-        p->lat.nwg = groups * p->lat.splits;
+        p->lat.nwg = wave_item_groups((int)B, p->lat.splits, p->lat.tiles);
     }
-    // Raw: one column tile per KV head over the full head width, one split per
-    // 16 keys so every raw wave issues all of its loads at once (the raw set is
-    // sinks + tail + current token).
-    const int raw_req = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
-    p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req, 0);
+    // Raw: one column tile per KV head over the full head width (the raw set
+    // is sinks + tail + current token).  Splits of three tiles measured 2-3 us
+    // faster a layer than one split per tile: a third of the raw partials and
+    // workgroups, with the raw rows still read long before the latent ones.
+    p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req0, 0);
     if (p->raw.tiles != 1 || p->raw.ks != 8) return fail(SLIMKV_EUNSUP, "raw tile shape");
     p->wq = rk;
     int parts = 1;
@@ -2007,8 +2060,8 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     prm.B = B; prm.Lq = Lq; prm.Hq = Hq;
     prm.scale_log2 = (float)(a->scale * 1.4426950408889634);
     prm.nseg = has_lat ? 2 : 1;
-    // Latent rows (the bulk) are segment 0 so they take the first residency
-    // slots; the short raw segment follows.
+    // Latent rows (the bulk, pipelined) are segment 0; the short raw segment is
+    // segment 1, whose workgroups split_kernel places first in the grid.
     Seg& r = prm.seg[has_lat ? 1 : 0];
     r.q = q_rot; r.q_sb = (int64_t)Lq * Hq * D; r.q_sl = (int64_t)Hq * D; r.q_sh = D;
     r.k = static_cast<const uint16_t*>(a->raw_k); r.k_sb = a->rk_sb; r.k_sn = a->rk_sn; r.k_sh = a->rk_sh;
@@ -2046,7 +2099,7 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
             l.slots = (int)pg->slots;
             l.slots_shift = (pg->slots & (pg->slots - 1)) == 0 ? __builtin_ctzll((unsigned long long)pg->slots) : -1;
             l.status = pg->status;
-            l.compact = 1; l.batch = B;
+            l.compact = 1;
         }
         ka = p.lat.ks;
         kb = 8;
@@ -2249,6 +2302,8 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
         const int fast_cap = std::max(1, std::min(fast_lat_splits(wv, 256), 256 - raw_req));
         if (a->lat_splits <= 0) slots = std::min<int64_t>(slots, (int64_t)B * ((Hkv + kWaves - 1) / kWaves) * fast_cap);
         p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, wv, a->lat_splits, slots);
+        // recon_split_kernel: a workgroup per (b, group of kWaves KV heads, split)
+        p->rec.nwg = (int)B * (int)((Hkv + kWaves - 1) / kWaves) * p->rec.splits;
     } else {
         p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, (int)D, a->lat_splits,
                               cu * split_occupancy(8, 8));

@@ -53,8 +53,9 @@ def test_two_calls_in_a_row_match_the_workspace_entry_point(device, cases):
 
 
 def test_call_larger_than_the_scratch_is_refused(device):
-    """64 sequences with 1024 raw rows need 64 raw splits of 512 fp32 partial
-    bytes per query head: about 68 MB of workspace, over the 32 MiB scratch."""
+    """64 sequences with 1024 raw rows read in 64 raw splits (asked for) need
+    512 fp32 partial bytes per split and query head: about 68 MB of workspace,
+    over the 32 MiB scratch."""
     from slimkv_amd import _lib, kernels
     case = latent_case(batch=2, context=600, tail=20, seed=73, device=device)
     B, Nr = 64, 1024
@@ -64,7 +65,7 @@ def test_call_larger_than_the_scratch_is_refused(device):
     lat = torch.randn(B, 16, 256, generator=gen, device=device).to(torch.bfloat16)
     pos = torch.full((B, 1), 599, dtype=torch.int64, device=device)
     a, out, lse, keep = kernels._latent_args(q, raw, raw, lat, lat, case.up_k, case.up_v, case.scale, None, None,
-                                             True, False, pos, case.cos, case.sin, None, None, 0, 0, None, None)
+                                             True, False, pos, case.cos, case.sin, None, None, 64, 0, None, None)
     need = _lib.lib().slimkv_latent_decode_workspace(ctypes.byref(a))
     assert need > _lib.NOALLOC_SCRATCH_BYTES
     out.fill_(3.0)
