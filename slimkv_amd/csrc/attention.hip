@@ -1910,17 +1910,19 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
         return worst;
     };
     // Eight packed rows per tile: 32 heads give four tiles, one per wave of a
-    // workgroup, all streaming the same latent rows.  (Sixteen rows -- four KV
-    // heads a wave -- measured no faster at rank 16 and slower at rank 48.)
-    const int cols = 8;
+    // workgroup, all streaming the same latent rows.  Block-diagonal ranks up
+    // to 16 take sixteen rows (four KV heads a wave), so a wave's tile is 64
+    // latent columns wide as at rank 32 (rank-16 C1 layer 27.7 -> 24.4 us);
+    // at rank 48 sixteen rows measured slower.
+    const int cols = bd && std::max(rk, rv) <= 16 ? 16 : 8;
     const int span = span_of(cols);
     const int lat_ks = round_even_tile(span);
     if (lat_ks < 0) return fail(SLIMKV_EUNSUP, "latent width not supported");
     const int64_t nl = std::max<int64_t>(a->lat_keys, 1);
     const int has_lat = a->lat_keys > 0;
     const int slots = cu * split_occupancy(has_lat ? lat_ks : 8, has_lat ? 8 : 0);
-    // Raw rows: splits of three 16-row tiles.
-    const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 47) / 48);
+    // Raw rows: splits of two 16-row tiles.
+    const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 31) / 32);
     const int raw_wg = (int)B * ((int)(Hkv + kWaves - 1) / kWaves) * raw_req0;
     // Dense rows: a whole number of latent workgroups per CU.  Each CU streams
     // its workgroups' rows at about the same rate, so a launch whose
@@ -1964,9 +1966,10 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
         p->lat.nwg = wave_item_groups((int)B, p->lat.splits, p->lat.tiles);
     }
     // Raw: one column tile per KV head over the full head width (the raw set
-    // is sinks + tail + current token).  Splits of three tiles measured 2-3 us
-    // faster a layer than one split per tile: a third of the raw partials and
-    // workgroups, with the raw rows still read long before the latent ones.
+    // is sinks + tail + current token).  Splits of two tiles measured 2-4 us
+    // faster a layer than one split per tile (and 1-2 us faster than three):
+    // fewer raw partials and workgroups, with the raw rows still read long
+    // before the latent ones.
     p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req0, 0);
     if (p->raw.tiles != 1 || p->raw.ks != 8) return fail(SLIMKV_EUNSUP, "raw tile shape");
     p->wq = rk;
