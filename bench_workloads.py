@@ -541,7 +541,10 @@ def ceiling_probe(torch, dev, gib=4, reps=10):
     from slimkv_amd import _lib
     nbytes = gib << 30
     buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    buf.fill_(1)
+    # filled 256 MiB a launch: writes of a known size for scaling the
+    # rocprofv3 WRITE_SIZE counter (as the stream reads scale FETCH_SIZE)
+    for chunk in buf.split(256 << 20):
+        chunk.fill_(1)
     cu = torch.cuda.get_device_properties(dev).multi_processor_count
     sink = torch.empty(cu * 64 * 64, dtype=torch.int32, device=dev)
     lib = _lib.lib()

@@ -558,12 +558,14 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     };
 
     // The tile loops run whole rounds of the register ring with no exit inside
-    // a round, then consume the tiles left in the ring: an exit between two
-    // tiles of a round would reach the loop header with that round's
-    // prefetch outstanding and force a full wait for loads there.
+    // a round, then finish the last tiles outside the loop: an exit between
+    // two tiles of a round would reach the loop header with that round's
+    // prefetch outstanding and force a full wait for loads there.  No tile
+    // past the split's last one is fetched.
     if constexpr (PAGED) {
         TileRegs<KS> other;
-        for (int it = 0; it + 1 < ntile; it += 2) {
+        int it = 0;
+        for (; it + 2 < ntile; it += 2) {
             fetch_paged(other, poth, it + 1);
             load_pages(poth, it + 3);
             consume(cur, it);
@@ -571,29 +573,35 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
             load_pages(pcur, it + 4);
             consume(other, it + 1);
         }
-        if (ntile & 1) consume(cur, ntile - 1);
+        if (it < ntile) {
+            if (it + 1 < ntile) fetch_paged(other, poth, it + 1);
+            consume(cur, it);
+            if (it + 1 < ntile) consume(other, it + 1);
+        }
     } else if constexpr (DEPTH > 1) {
         // A ring of DEPTH register tiles: the loads of the next DEPTH - 1
         // tiles stay in flight while a tile is consumed (the ring index is
-        // static in the unrolled body, so no register copies).  Loads past the
-        // last tile are issued anyway (clamped) to keep the outstanding-load
-        // count uniform; they are never consumed.
+        // static in the unrolled body, so no register copies).  At the top of
+        // a round ring[d] holds tile it + d for d < DEPTH - 1.
         TileRegs<KS> ring[DEPTH];
         ring[0] = cur;
 #pragma unroll
         for (int d = 1; d < DEPTH - 1; ++d) fetch(ring[d], d);
-        const int nfull = ntile - ntile % DEPTH;
-        for (int it = 0; it < nfull; it += DEPTH) {
+        int it = 0;
+        for (; it + 2 * DEPTH - 2 < ntile; it += DEPTH) {
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
                 fetch(ring[(d + DEPTH - 1) % DEPTH], it + d + DEPTH - 1);
                 consume(ring[d], it + d);
             }
         }
-        // ring[d] holds tile nfull + d for d < DEPTH - 1
+        // at most 2 * DEPTH - 2 tiles are left
 #pragma unroll
-        for (int d = 0; d < DEPTH - 1; ++d)
-            if (nfull + d < ntile) consume(ring[d], nfull + d);
+        for (int d = 0; d < 2 * DEPTH - 2; ++d) {
+            if (it + d >= ntile) break;
+            if (it + d + DEPTH - 1 < ntile) fetch(ring[(d + DEPTH - 1) % DEPTH], it + d + DEPTH - 1);
+            consume(ring[d % DEPTH], it + d);
+        }
     } else {
         for (int it = 0; it < ntile; ++it) {
             if (it) fetch(cur, it);
