@@ -254,11 +254,18 @@ int slimkv_reconstruct(const slimkv_reconstruct_args* a, void* stream);
  * RotaryEmbedding, modeling_utils.py:369-376).  Otherwise the workspace holds
  * the rebuilt K (and V).
  * ---------------------------------------------------------------------- */
+/* rope_fp32 (fused route with rotated beacon keys): 0 rebuilds and rotates
+ * each key with the reference's bf16 steps (bf16(acc + bias), then
+ * bf16(bf16(x c) + bf16(rotate_half(x) s)): the bits ReconstructionCache
+ * .materialize writes); 1 adds the bias and rotates in fp32 and rounds once
+ * (about a third of the per-key arithmetic; keys within one bf16 rounding of
+ * the exact rotation). */
 typedef struct slimkv_recon_decode_args {
     slimkv_latent_decode_args base;
     const int64_t* beacon_positions; int64_t bpos_sb;   /* [B, Nl] or NULL */
     const uint32_t* rope_pairs;                          /* [rope_rows, 128] or NULL */
     int32_t rope_repeats;                                /* 1: every cos/sin row is its first half twice */
+    int32_t rope_fp32;                                   /* 1: fp32 rotation, one rounding */
 } slimkv_recon_decode_args;
 
 /* One-time packing of RoPE tables for the fused reconstruction decode (no

@@ -75,7 +75,7 @@ ReconstructArgs = _struct('slimkv_reconstruct_args', [
 ReconDecodeArgs = _struct('slimkv_recon_decode_args', [
     ('base', LatentDecodeArgs),
     ('beacon_positions', c_ptr), ('bpos_sb', c_i64),
-    ('rope_pairs', c_ptr), ('rope_repeats', c_i32),
+    ('rope_pairs', c_ptr), ('rope_repeats', c_i32), ('rope_fp32', c_i32),
 ])
 
 PagedLatentDecodeArgs = _struct('slimkv_paged_latent_decode_args', [
@@ -202,7 +202,7 @@ SIGNATURES = {
     'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20

@@ -525,8 +525,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
             sv[i] = x;
             tmax = fmaxf(tmax, x);
         }
-        tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-        tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+        tmax = rows_max(tmax);
         const float mnew = fmaxf(m, tmax);
         const float mref = mnew == kNegInf ? 0.f : mnew;
         const float alpha = fast_exp2(m - mref);
@@ -613,8 +612,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
         if (bad) report_bad_page(sg.status);
     }
     // Column sums: every lane group holds a quarter of the keys.
-    lsum += shfl_xor_f(lsum, 16);
-    lsum += shfl_xor_f(lsum, 32);
+    lsum = rows_sum(lsum);
     if (!colv) return;
     const int pr = j * Lq + lq;
     const int64_t slot_out = ((int64_t)b * Hq * Lq + pr) * sg.splits + s;
@@ -681,7 +679,10 @@ split_kernel(SplitParams prm) {
 // ends with d = 16t + 4grp + i, so d and d + 64 share a lane), adds the bias,
 // rounds to bf16 and rotates at the beacon's position with the reference's
 // bf16 steps -- the same bits the up-projection kernel writes -- and feeds the
-// result straight in as the A operand of the score MFMA.  V stays latent: the
+// result straight in as the A operand of the score MFMA (ROPE = 1).  ROPE = 2
+// adds the bias and rotates in fp32 and rounds once into the operand: about a
+// third of the per-tile VALU work, keys within one bf16 rounding of the exact
+// rotation (the reference's steps round five times).  V stays latent: the
 // P.V MFMA accumulates the rv-wide latent sum that the combine lifts through
 // W_V.  RoPE reads (bf16 cos | bf16 sin << 16) pairs prepared once per table,
 // only the first half of each row: the fused route is taken for rotate-half
@@ -713,7 +714,7 @@ struct ReconTile {
 // two tiles do not cover the memory latency at two waves per SIMD.
 constexpr int kReconRing = 4;
 
-template <int KSR, int VL, bool ROPE>
+template <int KSR, int VL, int ROPE>
 __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq, int Hq, float scale_log2,
                                               char* lds) {
     constexpr int D = 128;
@@ -800,6 +801,14 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         bias2[tt][0] = bb.x;
         bias2[tt][1] = bb.y;
     }
+    // ROPE == 2: the bias is the rebuild's initial accumulator (fp32), so no
+    // per-tile bias arithmetic.
+    v4f kinit[8];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+        kinit[tt] = ROPE == 2 ? v4f{lo_bf16(bias2[tt][0]), hi_bf16(bias2[tt][0]), lo_bf16(bias2[tt][1]),
+                                    hi_bf16(bias2[tt][1])}
+                              : v4f{0.f, 0.f, 0.f, 0.f};
     // Rotated query of the column (B operand of the scores): d = 16t + 4grp + [0, 4).
     u32x2 qop[8];
     {
@@ -839,7 +848,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         // rebuild the K tile
         v4f kc[8];
 #pragma unroll
-        for (int tt = 0; tt < 8; ++tt) kc[tt] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int tt = 0; tt < 8; ++tt) kc[tt] = kinit[tt];
 #pragma unroll
         for (int ks = 0; ks < KSR; ++ks) {
             const v4s bop = as_v4s(t.k[ks].x, t.k[ks].y);
@@ -847,7 +856,25 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
             for (int tt = 0; tt < 8; ++tt) kc[tt] = mfma16(as_v4s(wa[tt][ks].x, wa[tt][ks].y), bop, kc[tt]);
         }
         u32x2 kop[8];
-        if constexpr (ROPE) {
+        if constexpr (ROPE == 2) {
+            // x = acc + bias (the bias was the accumulator's start), y[d] =
+            // x[d] c - x[d + 64] s, y[d + 64] = x[d + 64] c + x[d] s, in fp32
+            // with the table's bf16 (c, s); one rounding when packed.
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const uint32_t cw[4] = {cs[tt].x, cs[tt].y, cs[tt].z, cs[tt].w};
+                float ya[4], yb[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float c = lo_bf16(cw[i]), sn = hi_bf16(cw[i]);
+                    const float xa = kc[tt][i], xz = kc[tt + 4][i];
+                    ya[i] = fmaf(xa, c, -xz * sn);
+                    yb[i] = fmaf(xz, c, xa * sn);
+                }
+                kop[tt] = u32x2{pack_bf16(ya[0], ya[1]), pack_bf16(ya[2], ya[3])};
+                kop[tt + 4] = u32x2{pack_bf16(yb[0], yb[1]), pack_bf16(yb[2], yb[3])};
+            }
+        } else if constexpr (ROPE == 1) {
             // x = bf16(acc + bias) as floats (a missing bias is held as +0: x + 0
             // is x except that -0 becomes +0).  rotate_half pairs d with d + 64
             // (t with t + 4) under the same (c, s):
@@ -902,8 +929,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
             sv[i] = xv;
             tmax = fmaxf(tmax, xv);
         }
-        tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-        tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+        tmax = rows_max(tmax);
         const float mnew = fmaxf(m, tmax);
         const float mref = mnew == kNegInf ? 0.f : mnew;
         const float alpha = fast_exp2(m - mref);
@@ -947,8 +973,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         }
     }
 
-    lsum += shfl_xor_f(lsum, 16);
-    lsum += shfl_xor_f(lsum, 32);
+    lsum = rows_sum(lsum);
     if (!colv) return;
     const int prow = j * Lq + lq;
     const int64_t slot_out = ((int64_t)b * Hq * Lq + prow) * sg.splits + s;
@@ -966,7 +991,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
 }
 
 // Raw rows (split_segment, head_dim 128) first in the grid, then the beacon splits.
-template <int KSR, int VL, bool ROPE>
+template <int KSR, int VL, int ROPE>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 recon_split_kernel(SplitParams prm, ReconSeg rs) {
     constexpr int LA = kWaves * 2 * 16 * (32 * VL + 8) * 2;
@@ -1775,7 +1800,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 7; }
+extern "C" int slimkv_abi_version(void) { return 8; }
 
 extern "C" size_t slimkv_attention_workspace(const slimkv_attention_args* a) {
     AttnPlan plan{};
@@ -2266,8 +2291,6 @@ bool recon_fused_ok(const slimkv_recon_decode_args* r) {
     return true;
 }
 
-int recon_occupancy(int ksr, int vl);
-
 // V is linear in its latent, so sum_n p_n (U_V l_n + b) = U_V (sum_n p_n l_n) + b sum_n p_n:
 // the split kernel can attend over the latent rows and the combine lifts once per
 // (b, head).  K cannot follow when beacon keys are rotated after the
@@ -2299,22 +2322,27 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     if (g * Lq > kMaxRows) return fail(SLIMKV_EUNSUP, "more than 16 query rows per KV head");
     const int cu = device_cu_count();
     const int nl = (int)std::max<int64_t>(a->lat_keys, 1);
-    const int raw_req = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 15) / 16);
+    // raw rows in splits of two 16-row tiles (as the latent decode)
+    const int raw_req = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 31) / 32);
     p->raw = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, (int)a->raw_keys, (int)D, (int)D, raw_req, 0);
     p->fused = recon_fused_ok(r) ? 1 : 0;
     if (p->fused) {
         p->ksr = (int)(a->rank_k / Hkv / 16);
         p->vl = (int)(a->rank_v / Hkv / 32);
-        // The beacon splits are arithmetic-bound (rebuild + RoPE per tile), so
-        // they take every resident slot; the short raw workgroups run ahead of them.
-        int slots = cu * recon_occupancy(p->ksr, p->vl);
+        // One beacon workgroup per CU (the split count rounded down): a
+        // launch whose workgroups do not spread evenly over the CUs lasts as
+        // long as its most loaded CU, and two per CU measured slower than one
+        // (C2 layer: 16 splits, one a CU, 35.3 us; 32 splits 37.8 us; 24 or
+        // 40 splits 47-52 us).  The short raw workgroups run ahead of them.
+        const int64_t groups = (int64_t)B * ((Hkv + kWaves - 1) / kWaves);
         // as for the latent decode: stay within the fast combine's split count
         const int wv = 32 * p->vl;
         const int fast_cap = std::max(1, std::min(fast_lat_splits(wv, 256), 256 - raw_req));
-        if (a->lat_splits <= 0) slots = std::min<int64_t>(slots, (int64_t)B * ((Hkv + kWaves - 1) / kWaves) * fast_cap);
-        p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, wv, a->lat_splits, slots);
+        int req = a->lat_splits;
+        if (req <= 0) req = (int)std::max<int64_t>(1, std::min<int64_t>({(int64_t)cu / groups, fast_cap, kMaxSplits}));
+        p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, wv, req, 0);
         // recon_split_kernel: a workgroup per (b, group of kWaves KV heads, split)
-        p->rec.nwg = (int)B * (int)((Hkv + kWaves - 1) / kWaves) * p->rec.splits;
+        p->rec.nwg = (int)(groups * p->rec.splits);
     } else {
         p->rec = plan_segment((int)B, (int)Hkv, (int)Lq * g, 16, nl, (int)D, (int)D, a->lat_splits,
                               cu * split_occupancy(8, 8));
@@ -2333,26 +2361,6 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
     p->bacc_off = off; off = align256(off + br * D * 4);
     p->total = off;
     return SLIMKV_OK;
-}
-
-int recon_occupancy(int ksr, int vl) {
-    static std::mutex mu;
-    static std::vector<std::pair<int, int>> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    const int key = (dev << 8) | (ksr << 4) | vl;
-    std::lock_guard<std::mutex> lock(mu);
-    for (auto& kv : cache)
-        if (kv.first == key) return kv.second;
-    const void* fn = nullptr;
-#define SLIMKV_FN(K, V) if (ksr == K && vl == V) fn = reinterpret_cast<const void*>(&recon_split_kernel<K, V, true>);
-    SLIMKV_FN(1, 1) SLIMKV_FN(2, 1) SLIMKV_FN(3, 1) SLIMKV_FN(1, 2) SLIMKV_FN(2, 2)
-#undef SLIMKV_FN
-    int blocks = 0;
-    if (!fn || hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, kThreads, 0) != hipSuccess || blocks < 1)
-        blocks = 1;
-    cache.push_back({key, blocks});
-    return blocks;
 }
 
 // Raw rows and rebuilt-per-tile beacon rows in one launch, then the combine
@@ -2395,8 +2403,12 @@ int recon_fused_run(const slimkv_recon_decode_args* r, const ReconPlan& p, char*
     if (stages & SLIMKV_STAGE_ATTEND) {
 #define SLIMKV_LAUNCH(K, V)                                                                                       \
     if (p.ksr == K && p.vl == V) {                                                                                \
-        if (bs.pairs) hipLaunchKernelGGL((recon_split_kernel<K, V, true>), dim3(grid), dim3(kThreads), 0, st, prm, bs); \
-        else hipLaunchKernelGGL((recon_split_kernel<K, V, false>), dim3(grid), dim3(kThreads), 0, st, prm, bs);       \
+        if (bs.pairs && r->rope_fp32)                                                                              \
+            hipLaunchKernelGGL((recon_split_kernel<K, V, 2>), dim3(grid), dim3(kThreads), 0, st, prm, bs);           \
+        else if (bs.pairs)                                                                                        \
+            hipLaunchKernelGGL((recon_split_kernel<K, V, 1>), dim3(grid), dim3(kThreads), 0, st, prm, bs);           \
+        else                                                                                                      \
+            hipLaunchKernelGGL((recon_split_kernel<K, V, 0>), dim3(grid), dim3(kThreads), 0, st, prm, bs);           \
     }
         SLIMKV_LAUNCH(1, 1) SLIMKV_LAUNCH(2, 1) SLIMKV_LAUNCH(3, 1) SLIMKV_LAUNCH(1, 2) SLIMKV_LAUNCH(2, 2)
 #undef SLIMKV_LAUNCH

@@ -66,6 +66,26 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
     return __shfl_xor(v, mask, 64);
 }
 
+// Reductions over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32,
+// l ^ 48) with gfx950's row swaps (v_permlane16_swap / v_permlane32_swap,
+// VALU instructions: no LDS round trip).  With both operands equal a swap
+// hands lane l the pair (x_l, x_l^16) (resp. x_l^32) in an order symmetric
+// over the pair, so every lane of the group ends with the same value, summed
+// as (x_l + x_l^16) + (x_l^32 + x_l^48) as the xor shuffles would.
+__device__ __forceinline__ float rows_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ int64_t clamp_i64(int64_t x, int64_t lo, int64_t hi) {
     return x < lo ? lo : (x > hi ? hi : x);
 }

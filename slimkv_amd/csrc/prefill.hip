@@ -240,8 +240,7 @@ prefill_kernel(PrefillParams p) {
                         mx = fmaxf(mx, x);
                     }
             }
-            mx = fmaxf(mx, shfl_xor_f(mx, 16));
-            mx = fmaxf(mx, shfl_xor_f(mx, 32));
+            mx = rows_max(mx);
             const float m_new = fmaxf(m[nt], mx * p.scale_log2);
             const float base = m_new == kNegInf ? 0.f : m_new;
             const float alpha = fast_exp2(m[nt] - base);
@@ -292,8 +291,7 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         float tot = l[nt];
-        tot += shfl_xor_f(tot, 16);
-        tot += shfl_xor_f(tot, 32);
+        tot = rows_sum(tot);
         const float inv = tot > 0.f ? 1.f / tot : 0.f;
         const int qi = q0 + 16 * nt + col;
         if (qi >= p.Lq) continue;

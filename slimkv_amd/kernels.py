@@ -406,10 +406,13 @@ def reconstruct(latent, weight, bias=None, *, kv_heads, out=None, dst_rows=None,
 def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_positions=None, up_k_bias=None,
                  up_v_bias=None, block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
                  raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None, workspace=None,
-                 stages=_lib.STAGE_ALL):
+                 stages=_lib.STAGE_ALL, reference_rounding=False):
     """Reconstruction decode: rebuild beacon K (RoPE'd at beacon_positions
     [B, Nl] when given) and V, then attend over [beacons ; raw rows].
-    `stages` as latent_decode."""
+    `stages` as latent_decode.  On the fused route (block-diagonal bases)
+    rotated beacon keys are rebuilt in fp32 and rounded once, unless
+    reference_rounding asks for the reference's bf16 steps (the bits
+    ReconstructionCache.materialize writes, modeling_llama.py:1405-1483)."""
     base, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
                                         block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
                                         lat_lengths, raw_splits, lat_splits, out, lse, prepared_bases=False)
@@ -422,7 +425,7 @@ def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_pos
         pairs, repeats = prepare_rope_pairs(cos, sin)
     a = _lib.ReconDecodeArgs(base, _ptr(beacon_positions),
                              0 if beacon_positions is None else beacon_positions.stride(0), _ptr(pairs),
-                             int(pairs is not None and repeats))
+                             int(pairs is not None and repeats), int(not reference_rounding))
     nbytes = lib().slimkv_recon_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)

@@ -28,6 +28,7 @@ import torch
 from oracle import attention as oa
 from oracle import paged as opaged
 from oracle import rope as orope
+from oracle.bf16 import round_bf16
 from tests.helpers import assert_close, assert_lse_close, bits, to_np
 
 pytestmark = pytest.mark.gpu
@@ -86,18 +87,25 @@ def test_c2_recon_decode_full_size_sampled_rows(device):
     for b in (0, 5):
         sl = slice(b, b + 1)
         q_rot = _rot_at(layer['q'][sl].transpose(1, 2), cos, sin, CTX)             # [1, H, 1, D]
+        # the reference's keys (bf16 up-projection, bf16 RoPE steps) and the
+        # fused route's fp32 rotation (float64 model, one rounding)
         rk = oa.reconstruct(to_np(layer['lat_k'][sl])[:, None], to_np(layer['up_k']), None, HKV, D)
         rk = orope.rotate_bf16(rk[0].astype(np.float32), cn[bp][None], sn[bp][None]).astype(np.float64)[None]
+        xk = oa.reconstruct(to_np(layer['lat_k'][sl])[:, None], to_np(layer['up_k']), None, HKV, D,
+                            bf16_boundaries=False)[0]
+        c64, s64 = round_bf16(cn[bp][None]).astype(np.float64), round_bf16(sn[bp][None]).astype(np.float64)
+        fk = round_bf16(xk * c64 + orope.rotate_half(xk) * s64).astype(np.float64)[None]
         rv = oa.reconstruct(to_np(layer['lat_v'][sl])[:, None], to_np(layer['up_v']), None, HKV, D)
-        k = np.concatenate([rk, to_np(layer['raw_k'][sl].transpose(1, 2))], axis=2)
-        v = np.concatenate([rv, to_np(layer['raw_v'][sl].transpose(1, 2))], axis=2)
-        exact, exact_lse = oa.eager_forward(q_rot.transpose(0, 2, 1, 3), k.transpose(0, 2, 1, 3),
-                                            v.transpose(0, 2, 1, 3), scale)
-        eager, _ = oa.eager_recon_layer(q_rot, k, v, scale)
         got = to_np(out[sl])                                                          # [1, 1, H, D]
-        assert_close(got, exact, what=f'C2 row {b} vs float64')
-        assert_close(got, eager.transpose(0, 2, 1, 3), what=f'C2 row {b} vs eager bf16')
-        assert_lse_close(to_np(lse[sl]), exact_lse, what=f'C2 row {b}')
+        for name, keys in (('reference keys', rk), ('fp32-rotated keys', fk)):
+            k = np.concatenate([keys, to_np(layer['raw_k'][sl].transpose(1, 2))], axis=2)
+            v = np.concatenate([rv, to_np(layer['raw_v'][sl].transpose(1, 2))], axis=2)
+            exact, exact_lse = oa.eager_forward(q_rot.transpose(0, 2, 1, 3), k.transpose(0, 2, 1, 3),
+                                                v.transpose(0, 2, 1, 3), scale)
+            eager, _ = oa.eager_recon_layer(q_rot, k, v, scale)
+            assert_close(got, exact, what=f'C2 row {b} vs float64, {name}')
+            assert_close(got, eager.transpose(0, 2, 1, 3), what=f'C2 row {b} vs eager bf16, {name}')
+            assert_lse_close(to_np(lse[sl]), exact_lse, what=f'C2 row {b}, {name}')
 
 
 # ----------------------------------------------------------------------------- C3

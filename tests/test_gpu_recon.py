@@ -92,17 +92,34 @@ def test_reconstruct_scatter_and_rope_epilogue(device, n):
     assert (to_np(out)[:, untouched] == 0).all()
 
 
-def _recon_oracles(case, q_rot, k_rot, beacon_pos, lat_causal, bk=None, bv=None):
+def _rotate_fp32_model(x, cos_rows, sin_rows):
+    """The fused route's fp32 rotation in float64: the rebuilt key before any
+    rounding, the tables' bf16 (cos, sin), x*c + rotate_half(x)*s, one bf16
+    rounding at the end."""
+    c = round_bf16(cos_rows).astype(np.float64)
+    s = round_bf16(sin_rows).astype(np.float64)
+    return round_bf16(x * c + orope.rotate_half(x) * s).astype(np.float64)
+
+
+def _recon_oracles(case, q_rot, k_rot, beacon_pos, lat_causal, bk=None, bv=None, rounding='reference'):
     """Float64 attention over [rebuilt beacons ; raw rows] and the reference
-    eager formulation with bf16 scores/probabilities."""
+    eager formulation with bf16 scores/probabilities.  Rotated beacon keys are
+    rebuilt as the reference does (bf16 up-projection, then its bf16 RoPE
+    steps) or, rounding='fp32', as the fused route's fp32 rotation (float64
+    rebuild with bias, rotated, rounded once)."""
     Hkv, D = case.kv_heads, 128
-    rk = oa.reconstruct(to_np(case.lat_k)[:, None], to_np(case.up_k), None if bk is None else to_np(bk), Hkv, D)
+    bk_np = None if bk is None else to_np(bk)
+    exact_k = rounding == 'fp32' and beacon_pos is not None
+    rk = oa.reconstruct(to_np(case.lat_k)[:, None], to_np(case.up_k), bk_np, Hkv, D, bf16_boundaries=not exact_k)
     rv = oa.reconstruct(to_np(case.lat_v)[:, None], to_np(case.up_v), None if bv is None else to_np(bv), Hkv, D)
     if beacon_pos is not None:
         c, s = to_np(case.cos).astype(np.float32), to_np(case.sin).astype(np.float32)
         bp = beacon_pos.cpu().numpy()
-        rk = np.stack([orope.rotate_bf16(rk[b].astype(np.float32), c[bp[b]][None], s[bp[b]][None])
-                       for b in range(rk.shape[0])]).astype(np.float64)
+        if exact_k:
+            rk = np.stack([_rotate_fp32_model(rk[b], c[bp[b]][None], s[bp[b]][None]) for b in range(rk.shape[0])])
+        else:
+            rk = np.stack([orope.rotate_bf16(rk[b].astype(np.float32), c[bp[b]][None], s[bp[b]][None])
+                           for b in range(rk.shape[0])]).astype(np.float64)
     raw_k, raw_v = to_np(k_rot), to_np(case.raw_v.transpose(1, 2))
     q = to_np(q_rot)                                                  # [B, H, L, D]
     B, H, L, _ = q.shape
@@ -130,10 +147,11 @@ def _rotate(case):
                                case.q_positions, raw_idx, case.sinks, history)
 
 
-@pytest.mark.parametrize('beacon_rope', [True, False])
-def test_recon_decode_qwen14b_layer_shape(device, beacon_rope):
+@pytest.mark.parametrize('beacon_rope,reference_rounding', [(True, False), (True, True), (False, False)])
+def test_recon_decode_qwen14b_layer_shape(device, beacon_rope, reference_rounding):
     """Qwen2.5-14B attention layer shape: 40 query / 8 KV heads (GQA 5), r 32,
-    4 sinks + 128 tail, K-RoPE on the rebuilt beacons at their slot positions."""
+    4 sinks + 128 tail, K-RoPE on the rebuilt beacons at their slot positions
+    (fp32 rotation, or the reference's bf16 steps)."""
     from slimkv_amd import kernels
     case = latent_case(batch=4, heads=40, context=4096 + 132, tail=128, seed=31, device=device)
     q_rot, k_rot = _rotate(case)
@@ -141,9 +159,11 @@ def test_recon_decode_qwen14b_layer_shape(device, beacon_rope):
     bpos = (torch.arange(nl, device=device) * 4 + 4)[None].expand(4, -1).contiguous() if beacon_rope else None
     out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
                                     case.up_v, case.scale, beacon_positions=bpos, block_diagonal=True,
-                                    q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+                                    q_positions=case.q_positions, cos=case.cos, sin=case.sin,
+                                    reference_rounding=reference_rounding)
     torch.cuda.synchronize()
-    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, False)
+    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, False,
+                                         rounding='reference' if reference_rounding else 'fp32')
     got = to_np(out.transpose(1, 2))
     assert_close(got, exact, what='vs float64')
     assert_close(got, eager, what='vs bf16 eager')
@@ -180,9 +200,10 @@ def test_recon_decode_insertion_step_with_biases_general_weights(device, rank):
     assert_lse_close(to_np(lse), lse_e)
 
 
+@pytest.mark.parametrize('reference_rounding', [False, True])
 @pytest.mark.parametrize('rk,rv,bias,insertion', [(32, 32, True, True), (16, 64, False, False), (48, 32, True, False),
                                                   (32, 64, False, True)])
-def test_recon_decode_fused_block_diagonal_variants(device, rk, rv, bias, insertion):
+def test_recon_decode_fused_block_diagonal_variants(device, rk, rv, bias, insertion, reference_rounding):
     """Block-diagonal bases take the fused route (K rebuilt and rotated per tile
     inside the attention kernel, V lifted after the sum): K ranks 16/32/48, V
     ranks 32/64, K/V biases, the two-query insertion step with a causal beacon
@@ -205,9 +226,10 @@ def test_recon_decode_fused_block_diagonal_variants(device, rk, rv, bias, insert
     out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
                                     case.up_v, case.scale, beacon_positions=bpos, up_k_bias=bk, up_v_bias=bv,
                                     block_diagonal=True, lat_causal=insertion, q_positions=case.q_positions,
-                                    cos=case.cos, sin=case.sin)
+                                    cos=case.cos, sin=case.sin, reference_rounding=reference_rounding)
     torch.cuda.synchronize()
-    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, insertion, bk, bv)
+    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, insertion, bk, bv,
+                                         rounding='reference' if reference_rounding else 'fp32')
     got = to_np(out.transpose(1, 2))
     assert_close(got, exact, what='vs float64')
     assert_close(got, eager, what='vs bf16 eager')
@@ -234,7 +256,8 @@ def test_recon_decode_fused_ragged_lengths(device):
         sub = SimpleNamespace(kv_heads=case.kv_heads, scale=case.scale, cos=case.cos, sin=case.sin,
                               lat_k=case.lat_k[b:b + 1, :nb], lat_v=case.lat_v[b:b + 1, :nb],
                               up_k=case.up_k, up_v=case.up_v, raw_v=case.raw_v[b:b + 1, :rb])
-        exact, _, lse_e = _recon_oracles(sub, q_rot[b:b + 1], k_rot[b:b + 1, :, :rb], bpos[b:b + 1, :nb], False)
+        exact, _, lse_e = _recon_oracles(sub, q_rot[b:b + 1], k_rot[b:b + 1, :, :rb], bpos[b:b + 1, :nb], False,
+                                         rounding='fp32')
         assert_close(to_np(out.transpose(1, 2))[b:b + 1], exact, what=f'sequence {b}')
         assert_lse_close(to_np(lse)[b:b + 1], lse_e)
 
