@@ -656,10 +656,11 @@ def b1(args):
         del graph
 
         # The reference's per-token scope (README.md:284): the same 32 layers
-        # with their QKV projection (one GEMM over the concatenated q/k/v
-        # weights), the new token's K RoPE, its appends to the raw cache
-        # (rotated K, plain K, V), the fused decode and the output projection;
-        # no norm, MLP or LM head.  Weights are synthetic (Llama-3.1-8B shapes,
+        # with their QKV projection, the new token's K RoPE and its appends to
+        # the raw cache (rotated K, plain K, V) -- one kernels.decode_qkv
+        # launch over the concatenated q/k/v weights, as StaticDecode runs it --
+        # the fused decode and the output projection (kernels.linear_rows); no
+        # norm, MLP or LM head.  Weights are synthetic (Llama-3.1-8B shapes,
         # hidden 4096, q 4096, k/v 1024).
         hidden = HQ * D
         slot = torch.full((1,), raw - 1, dtype=torch.int64, device=dev)
@@ -670,23 +671,19 @@ def b1(args):
                           ).to(torch.bfloat16)
             L['w_o'] = (torch.randn(hidden, hidden, generator=gen, device=dev) * hidden ** -0.5).to(torch.bfloat16)
             L['plain_k'] = L['raw_k'].clone()
-            L['o'] = torch.empty(1, 1, hidden, dtype=torch.bfloat16, device=dev)
+            L['q_new'] = torch.empty(1, hidden, dtype=torch.bfloat16, device=dev)
+            L['o'] = torch.empty(1, hidden, dtype=torch.bfloat16, device=dev)
+        token_pos = pos.view(1)
 
         def full_token():
             rows = kernels.query_rope_rows(cos, sin, pos)
             for L in layers:
-                qkv = torch.nn.functional.linear(L['x'], L['w_qkv'])
-                q = qkv[..., :hidden].view(1, 1, HQ, D)
-                k = qkv[..., hidden:hidden + HKV * D].view(1, 1, HKV, D)
-                v = qkv[..., hidden + HKV * D:].view(1, 1, HKV, D)
-                _, k_rot = kernels.rope_decode(q.transpose(1, 2), k.transpose(1, 2), cos, sin, pos, None, 0, 0)
-                L['raw_k'].index_copy_(1, slot, k_rot.transpose(1, 2))
-                L['plain_k'].index_copy_(1, slot, k)
-                L['raw_v'].index_copy_(1, slot, v)
-                kernels.latent_decode(q, L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'],
-                                      scale, block_diagonal=True, cos=rows[0], sin=rows[1], out=L['out'],
-                                      lse=L['lse'], workspace=ws)
-                torch.nn.functional.linear(L['out'].view(1, 1, hidden), L['w_o'], out=L['o'])
+                q = kernels.decode_qkv(L['x'].view(1, hidden), L['w_qkv'], None, HQ, HKV, cos, sin, token_pos,
+                                       L['raw_k'], L['raw_v'], slot, plain_k=L['plain_k'], q_out=L['q_new'])
+                kernels.latent_decode(q.view(1, 1, HQ, D), L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'],
+                                      L['up_k'], L['up_v'], scale, block_diagonal=True, cos=rows[0], sin=rows[1],
+                                      out=L['out'], lse=L['lse'], workspace=ws)
+                kernels.linear_rows(L['out'].view(1, hidden), L['w_o'], out=L['o'])
         full_token()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())

@@ -348,6 +348,52 @@ typedef struct slimkv_merge_args {
 int slimkv_merge(const slimkv_merge_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Projections of a decode step's rows (one token per sequence of a lockstep
+ * batch, m <= 4): out[m, n] = x[m, :] . W[n, :] (+ bias[n]), W the
+ * nn.Linear weight [N, K] bf16 row-major, fp32 accumulation, one bf16
+ * rounding.  N a multiple of 128, K a multiple of 8; x rows and W 16-byte
+ * aligned.  Replaces the nn.Linear calls on the step's rows, such as o_proj
+ * in StaticDecode.forward (slimkv/llama3/static_decode.py:193-198).
+ * x [m, K] (row stride x_sm), out [m, N] (row stride o_sm).
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_linear_rows_args {
+    const void* x; int64_t x_sm;
+    const void* weight; const void* bias;   /* [N, K]; bias [N] or NULL */
+    void* out; int64_t o_sm;
+    int64_t m, n, k;
+} slimkv_linear_rows_args;
+
+int slimkv_linear_rows(const slimkv_linear_rows_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * The new token's query/key/value projection with its key RoPE and raw-cache
+ * appends, one launch.  Over W = [W_q; W_k; W_v] ([(Hq + 2 Hkv) * 128, K],
+ * bias likewise or NULL) it writes q = x W_q^T (+ b_q) to `q` (unrotated:
+ * the decode rotates it), the key k = bf16(x W_k^T (+ b_k)) rotated at
+ * positions[m] with the reference's bf16 steps (the bits of
+ * slimkv_rope_decode) to raw_k[m, slot], the unrotated key to
+ * plain_k[m, slot] (when given) and v = x W_v^T (+ b_v) to raw_v[m, slot],
+ * slot = *slot_index (device int64).  Replaces q_proj / k_proj / v_proj,
+ * fused_rope and the raw-cache index_copy_ appends of StaticDecode.forward
+ * (slimkv/llama3/static_decode.py:148-163).  head_dim 128; x [m, K], m <= 4;
+ * q [m, Hq * 128] (row stride q_sm); the caches [m, capacity, Hkv, 128] share
+ * strides (c_sm, c_sn); cos/sin [rope_rows, 128] fp32; positions [m] (stride
+ * pos_sm), clamped into the tables.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_decode_qkv_args {
+    const void* x; int64_t x_sm;
+    const void* weight; const void* bias;
+    void* q; int64_t q_sm;
+    void* raw_k; void* plain_k; void* raw_v; int64_t c_sm, c_sn;
+    const int64_t* slot_index;
+    const float* cos; const float* sin; int64_t rope_rows;
+    const int64_t* positions; int64_t pos_sm;
+    int64_t m, k, heads, kv_heads, head_dim;
+} slimkv_decode_qkv_args;
+
+int slimkv_decode_qkv(const slimkv_decode_qkv_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
  * Prefill attention: causal (bottom-right aligned) GQA attention over a full
  * window, head_dim 128, bf16 in/out, fp32 accumulation and softmax.
  * Replaces the flash_attn_func call of LlamaFlashAttention2._flash_attention_forward

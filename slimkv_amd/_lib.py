@@ -78,6 +78,18 @@ ReconDecodeArgs = _struct('slimkv_recon_decode_args', [
     ('rope_pairs', c_ptr), ('rope_repeats', c_i32), ('rope_fp32', c_i32),
 ])
 
+LinearRowsArgs = _struct('slimkv_linear_rows_args', [
+    ('x', c_ptr), ('x_sm', c_i64), ('weight', c_ptr), ('bias', c_ptr), ('out', c_ptr), ('o_sm', c_i64),
+    *_i64s('m', 'n', 'k'),
+])
+
+DecodeQKVArgs = _struct('slimkv_decode_qkv_args', [
+    ('x', c_ptr), ('x_sm', c_i64), ('weight', c_ptr), ('bias', c_ptr), ('q', c_ptr), ('q_sm', c_i64),
+    ('raw_k', c_ptr), ('plain_k', c_ptr), ('raw_v', c_ptr), *_i64s('c_sm', 'c_sn'),
+    ('slot_index', c_ptr), ('cos', c_ptr), ('sin', c_ptr), ('rope_rows', c_i64),
+    ('positions', c_ptr), ('pos_sm', c_i64), *_i64s('m', 'k', 'heads', 'kv_heads', 'head_dim'),
+])
+
 PagedLatentDecodeArgs = _struct('slimkv_paged_latent_decode_args', [
     ('base', LatentDecodeArgs),
     ('pages', c_ptr), *_i64s('num_pages', 'page_stride'),
@@ -190,6 +202,8 @@ SIGNATURES = {
     'slimkv_recon_decode_stages': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), ctypes.c_int, c_ptr,
                                                   ctypes.c_size_t, c_ptr]),
     'slimkv_rope_decode': (ctypes.c_int, [ctypes.POINTER(RopeDecodeArgs), c_ptr]),
+    'slimkv_linear_rows': (ctypes.c_int, [ctypes.POINTER(LinearRowsArgs), c_ptr]),
+    'slimkv_decode_qkv': (ctypes.c_int, [ctypes.POINTER(DecodeQKVArgs), c_ptr]),
     'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
     'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),
     'slimkv_prefill_attention': (ctypes.c_int, [ctypes.POINTER(PrefillAttentionArgs), c_ptr]),
@@ -202,7 +216,7 @@ SIGNATURES = {
     'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20

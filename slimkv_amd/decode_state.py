@@ -157,8 +157,13 @@ class LatentDecodeCache:
         self.plain_k.index_copy_(1, self.raw_index, raw_k)
         self.raw_v.index_copy_(1, self.raw_index, raw_v)
         if lat_k is not None:
-            self.lat_k.index_copy_(1, self.latent_index, lat_k)
-            self.lat_v.index_copy_(1, self.latent_index, lat_v)
+            self.write_latents(lat_k, lat_v)
+
+    def write_latents(self, lat_k, lat_v):
+        """Store the step's beacon latents [B, n, R] at the prepared slots
+        (when the raw rows were appended by kernels.decode_qkv)."""
+        self.lat_k.index_copy_(1, self.latent_index, lat_k)
+        self.lat_v.index_copy_(1, self.latent_index, lat_v)
 
     def commit(self, plan, refresh_sink=False, cos=None, sin=None):
         """update_memory (memory.py:233-278): keep the raw row and beacons, or

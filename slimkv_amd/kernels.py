@@ -484,6 +484,60 @@ def rope_decode(q, k, cos, sin, query_positions, raw_indices, sink, history):
     return oq, ok
 
 
+def linear_rows(x, weight, bias=None, out=None):
+    """Projection of a decode step's rows: x [..., K] (at most 4 rows) ->
+    out [..., N] = x W^T (+ bias), W the nn.Linear weight [N, K] bf16
+    (N a multiple of 128), fp32 accumulation, one bf16 rounding."""
+    _need_device(x, weight, bias)
+    _need_bf16(x, weight)
+    N, K = weight.shape
+    if x.shape[-1] != K or weight.stride(-1) != 1 or weight.stride(0) != K:
+        raise ValueError('x [..., K] against a contiguous weight [N, K] required')
+    rows = x.reshape(-1, K)
+    if rows.stride(-1) != 1:
+        rows = rows.contiguous()
+    if out is None:
+        out = torch.empty(*x.shape[:-1], N, dtype=BF16, device=x.device)
+    flat = out.view(-1, N)
+    if bias is not None and (bias.dtype != BF16 or not bias.is_contiguous() or bias.numel() != N):
+        raise ValueError('bias must be a contiguous bf16 [N]')
+    a = _lib.LinearRowsArgs(_ptr(rows), rows.stride(0), _ptr(weight), _ptr(bias), _ptr(flat), flat.stride(0),
+                            rows.shape[0], N, K)
+    check(lib().slimkv_linear_rows(ctypes.byref(a), _lib.stream_handle(x.device)))
+    return out
+
+
+def decode_qkv(x, weight, bias, heads, kv_heads, cos, sin, positions, raw_k, raw_v, slot_index, plain_k=None,
+               q_out=None):
+    """The new token's q/k/v projection, key RoPE and raw-cache appends in one
+    launch.  x [B, K] (B <= 4 rows), weight = cat([W_q, W_k, W_v]) [(Hq + 2 Hkv)
+    * 128, K] (bias likewise or None), positions [B] int64, caches
+    [B, capacity, Hkv, 128] (rotated K, V and optionally unrotated K) written at
+    slot = slot_index[0] (device int64).  Returns q [B, Hq * 128] unrotated."""
+    _need_device(x, weight, bias, cos, sin, positions, raw_k, raw_v, slot_index, plain_k)
+    _need_bf16(x, weight, raw_k, raw_v)
+    B, K = x.shape
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    caches = [c for c in (raw_k, raw_v, plain_k) if c is not None]
+    if any(c.stride() != raw_k.stride() or c.shape != raw_k.shape for c in caches) or raw_k.stride(-1) != 1 \
+            or raw_k.stride(2) != 128 or raw_k.shape[2] != kv_heads or raw_k.shape[0] != B:
+        raise ValueError('the caches must share shape [B, capacity, Hkv, 128] and strides')
+    if q_out is None:
+        q_out = torch.empty(B, heads * 128, dtype=BF16, device=x.device)
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or not cos.is_contiguous() or \
+            not sin.is_contiguous() or cos.shape != sin.shape or cos.shape[-1] != 128:
+        raise ValueError('RoPE tables must be contiguous fp32 [rows, 128]')
+    pos = positions.to(torch.int64)
+    slot = slot_index.to(torch.int64)
+    a = _lib.DecodeQKVArgs(_ptr(x), x.stride(0), _ptr(weight), _ptr(bias), _ptr(q_out), q_out.stride(0),
+                           _ptr(raw_k), _ptr(plain_k), _ptr(raw_v), raw_k.stride(0), raw_k.stride(1), _ptr(slot),
+                           _ptr(cos), _ptr(sin), cos.shape[0], _ptr(pos), pos.stride(0) if pos.dim() else 1,
+                           B, K, heads, kv_heads, 128)
+    check(lib().slimkv_decode_qkv(ctypes.byref(a), _lib.stream_handle(x.device)))
+    return q_out
+
+
 def prefill_rope(q, k, cos, sin, positions, roles, sink):
     """q [B,Hq,Lq,D], k [B,Hk,Nk,D]; outputs keep the input strides (empty_like)."""
     _need_device(q, k, cos, sin, positions, roles)

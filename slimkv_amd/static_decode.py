@@ -30,6 +30,33 @@ def _tables(rope, device):
     return cos.contiguous(), sin.contiguous()
 
 
+def _bf16_linear(m, rows):
+    """nn.Linear with contiguous bf16 weight (and bias) that the decode
+    projection kernels take for `rows` rows (out features a multiple of 128)."""
+    return (isinstance(m, torch.nn.Linear) and m.weight.dtype == torch.bfloat16 and m.weight.is_contiguous()
+            and m.out_features % 128 == 0 and m.in_features % 8 == 0 and rows <= 4
+            and (m.bias is None or (m.bias.dtype == torch.bfloat16 and m.bias.is_contiguous())))
+
+
+def _fused_qkv(attn, rows):
+    """(weight, bias) of the layer's q/k/v projections concatenated for the
+    one-launch decode projection (kernels.decode_qkv), or None when the layer
+    does not fit it.  The weights are copied once, when the stream is built."""
+    mods = (attn.q_proj, attn.k_proj, attn.v_proj)
+    if attn.head_dim != 128 or not all(_bf16_linear(m, rows) for m in mods):
+        return None
+    if len({m.in_features for m in mods}) != 1 or len({m.bias is None for m in mods}) != 1:
+        return None
+    if (attn.q_proj.out_features != attn.num_heads * 128 or
+            attn.k_proj.out_features != attn.num_key_value_heads * 128 or
+            attn.v_proj.out_features != attn.num_key_value_heads * 128):
+        return None
+    with torch.no_grad():
+        weight = torch.cat([m.weight for m in mods]).contiguous()
+        bias = None if attn.q_proj.bias is None else torch.cat([m.bias for m in mods]).contiguous()
+    return weight, bias
+
+
 class StaticDecode:
     """Lockstep decode stream; unsupported calls keep the ordinary model path."""
 
@@ -43,11 +70,19 @@ class StaticDecode:
         self.raw_capacity = max(model.config.beacon_window + model.config.beacon_sink_size + 1, raw_capacity or 0)
         self.positions = torch.zeros(batch, 2, dtype=torch.long, device=device)
         self.caches = []
+        # The new token's q/k/v projection, key RoPE and raw-cache appends run as
+        # one launch over concatenated weights, and the output projection of
+        # the token's row as a weight-streaming kernel (kernels.decode_qkv /
+        # linear_rows), where the layer's projections allow it.
+        self.qkv = []
+        self.o_rows = []
         for layer in model.model.layers:
             attn = layer.self_attn
             self.caches.append(LatentDecodeCache(
                 batch, attn.num_key_value_heads, attn.head_dim, attn.beacon_k_up_proj.in_features,
                 attn.beacon_v_up_proj.in_features, self.raw_capacity, capacity, device, attn.q_proj.weight.dtype))
+            self.qkv.append(_fused_qkv(attn, batch))
+            self.o_rows.append(_bf16_linear(attn.o_proj, batch))
 
     @staticmethod
     def eligible(model, ids, past, kwargs):
@@ -98,34 +133,54 @@ class StaticDecode:
         if size:
             hidden = torch.cat([hidden, model.model.beacon_embed_tokens(ids[:, 1:] - model.config.vocab_size)], dim=1)
         B = hidden.shape[0]
-        for cache, layer in zip(self.caches, model.model.layers):
+        for cache, layer, fused, o_rows in zip(self.caches, model.model.layers, self.qkv, self.o_rows):
             residual = hidden
             normalized = layer.input_layernorm(hidden)
             attn = layer.self_attn
-            q = attn.q_proj(normalized)
-            if size and 'q' in attn.config.beacon_param:
-                q = torch.cat([q[:, :1], attn.beacon_q_proj(normalized[:, 1:])], dim=1)
-            q = q.view(B, length, attn.num_heads, attn.head_dim)
-            raw_k = attn.k_proj(normalized[:, :1]).view(B, 1, attn.num_key_value_heads, attn.head_dim)
-            raw_v = attn.v_proj(normalized[:, :1]).view(B, 1, attn.num_key_value_heads, attn.head_dim)
-            cos, sin = _tables(attn.rotary_emb, q.device)
-            q_rot, k_rot = kernels.rope_decode(q.transpose(1, 2), raw_k.transpose(1, 2), cos, sin, positions, None,
-                                               0, 0)
+            cos, sin = _tables(attn.rotary_emb, hidden.device)
             kl = vl = None
             if size:
                 kd = attn.beacon_kv_down_proj if attn._use_shared_kv_down_proj() else attn.beacon_k_down_proj
                 vd = attn.beacon_kv_down_proj if attn._use_shared_kv_down_proj() else attn.beacon_v_down_proj
                 kl, vl = kd(normalized[:, 1:]), vd(normalized[:, 1:])
-            cache.write(k_rot.transpose(1, 2), raw_k, raw_v, kl, vl)
+            if fused is not None:
+                # q of the token (unrotated: the decode rotates it), its key
+                # rotated and appended with its value in the same launch
+                q = kernels.decode_qkv(normalized[:, 0], fused[0], fused[1], attn.num_heads,
+                                       attn.num_key_value_heads, cos, sin, positions[:, 0], cache.raw_k, cache.raw_v,
+                                       cache.raw_index, plain_k=cache.plain_k).view(B, 1, attn.num_heads, 128)
+                if size:
+                    qb = attn.beacon_q_proj if 'q' in attn.config.beacon_param else attn.q_proj
+                    q = torch.cat([q, qb(normalized[:, 1:]).view(B, size, attn.num_heads, 128)], dim=1)
+                if size:
+                    cache.write_latents(kl, vl)
+                rotation = dict(q_positions=positions, cos=cos, sin=sin)
+            else:
+                q = attn.q_proj(normalized)
+                if size and 'q' in attn.config.beacon_param:
+                    q = torch.cat([q[:, :1], attn.beacon_q_proj(normalized[:, 1:])], dim=1)
+                q = q.view(B, length, attn.num_heads, attn.head_dim)
+                raw_k = attn.k_proj(normalized[:, :1]).view(B, 1, attn.num_key_value_heads, attn.head_dim)
+                raw_v = attn.v_proj(normalized[:, :1]).view(B, 1, attn.num_key_value_heads, attn.head_dim)
+                q_rot, k_rot = kernels.rope_decode(q.transpose(1, 2), raw_k.transpose(1, 2), cos, sin, positions,
+                                                   None, 0, 0)
+                cache.write(k_rot.transpose(1, 2), raw_k, raw_v, kl, vl)
+                q = q_rot.transpose(1, 2)
+                rotation = dict(q_positions=None, cos=None, sin=None)
             uk, uv = attn.beacon_k_up_proj, attn.beacon_v_up_proj
-            out, _ = cache.attend(q_rot.transpose(1, 2), uk.weight, uv.weight, 1.0 / math.sqrt(attn.head_dim),
-                                  q_positions=None, cos=None, sin=None, size=size, up_k_bias=uk.bias,
-                                  up_v_bias=uv.bias)
+            out, _ = cache.attend(q, uk.weight, uv.weight, 1.0 / math.sqrt(attn.head_dim), size=size,
+                                  up_k_bias=uk.bias, up_v_bias=uv.bias, **rotation)
             merged = out.reshape(B, length, attn.hidden_size)
-            output = attn.o_proj(merged)
-            if size and 'o' in attn.config.beacon_param:
-                beacon_output = attn.beacon_o_proj(merged)
-                output = torch.cat([output[:, :1], beacon_output[:, 1:]], dim=1)
+            if o_rows:
+                output = kernels.linear_rows(merged[:, 0], attn.o_proj.weight, attn.o_proj.bias)[:, None]
+                if size:
+                    ob = attn.beacon_o_proj if 'o' in attn.config.beacon_param else attn.o_proj
+                    output = torch.cat([output, ob(merged[:, 1:])], dim=1)
+            else:
+                output = attn.o_proj(merged)
+                if size and 'o' in attn.config.beacon_param:
+                    beacon_output = attn.beacon_o_proj(merged)
+                    output = torch.cat([output[:, :1], beacon_output[:, 1:]], dim=1)
             hidden = layer._decode_tail(output, residual)
         hidden = model.model.norm(hidden)
         return hidden if return_normalized_hidden else model.lm_head(hidden).float()

@@ -36,3 +36,19 @@ def assert_lse_close(actual, expected, atol=2e-3, what=''):
     if fin.any():
         err = np.abs(actual[fin] - expected[fin]).max()
         assert err <= atol, f'{what}: LSE err {err:.3e} > {atol}'
+
+
+def neighbour_of_exact(actual, exact, rounded, abs_terms):
+    """Every bf16 output is one of the two bf16 neighbours of the float64 GEMM
+    result up to the fp32 accumulation error (any fp32-accumulating GEMM -- this
+    kernel or hipBLASLt -- can land on either side of a near-tie, and near a
+    cancellation the error is absolute), and almost all equal its correct
+    rounding.  abs_terms: the GEMM of absolute values (sum |w||x|)."""
+    a, x = np.asarray(actual, np.float64), np.asarray(exact, np.float64)
+    mag = np.maximum(np.abs(x), 1e-30)
+    ulp = 2.0 ** (np.floor(np.log2(mag)) - 7)
+    accumulation = np.asarray(abs_terms, np.float64) * 2.0 ** -20
+    err = np.abs(a - x)
+    bad = err >= ulp * 1.0001 + accumulation
+    assert not bad.any(), list(zip(a[bad][:4], x[bad][:4]))
+    assert (a == np.asarray(rounded, np.float64)).mean() > 0.98

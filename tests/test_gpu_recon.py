@@ -17,25 +17,9 @@ from oracle import attention as oa
 from oracle import rope as orope
 from oracle.bf16 import round_bf16
 from slimkv_amd.workloads import block_diagonal, latent_case, orthonormal_columns, rope_tables
-from tests.helpers import assert_close, assert_lse_close, to_np
+from tests.helpers import assert_close, assert_lse_close, neighbour_of_exact, to_np
 
 pytestmark = pytest.mark.gpu
-
-
-def _neighbour_of_exact(actual, exact, rounded, abs_terms):
-    """Every bf16 output is one of the two bf16 neighbours of the float64 GEMM
-    result up to the fp32 accumulation error (any fp32-accumulating GEMM -- this
-    kernel or hipBLASLt -- can land on either side of a near-tie, and near a
-    cancellation the error is absolute), and almost all equal its correct
-    rounding.  abs_terms: the GEMM of absolute values (sum |w||x|)."""
-    a, x = np.asarray(actual, np.float64), np.asarray(exact, np.float64)
-    mag = np.maximum(np.abs(x), 1e-30)
-    ulp = 2.0 ** (np.floor(np.log2(mag)) - 7)
-    accumulation = np.asarray(abs_terms, np.float64) * 2.0 ** -20
-    err = np.abs(a - x)
-    bad = err >= ulp * 1.0001 + accumulation
-    assert not bad.any(), list(zip(a[bad][:4], x[bad][:4]))
-    assert (a == np.asarray(rounded, np.float64)).mean() > 0.98
 
 
 @pytest.mark.parametrize('bd,rank,bias,B,n', [(True, 32, False, 2, 203), (True, 48, True, 2, 203),
@@ -62,7 +46,7 @@ def test_reconstruct_matches_oracle_gemm(device, bd, rank, bias, B, n):
     exact = oa.reconstruct(to_np(lat)[:, None], to_np(w), bias_np, Hkv, D, bf16_boundaries=False)
     rounded = oa.reconstruct(to_np(lat)[:, None], to_np(w), bias_np, Hkv, D)
     abs_terms = oa.reconstruct(np.abs(to_np(lat))[:, None], np.abs(to_np(w)), None, Hkv, D, bf16_boundaries=False)
-    _neighbour_of_exact(to_np(out).transpose(0, 2, 1, 3), exact, rounded, abs_terms)
+    neighbour_of_exact(to_np(out).transpose(0, 2, 1, 3), exact, rounded, abs_terms)
 
 
 @pytest.mark.parametrize('n', [37, 4099])
