@@ -1953,10 +1953,12 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     if (lat_ks < 0) return fail(SLIMKV_EUNSUP, "latent width not supported");
     const int64_t nl = std::max<int64_t>(a->lat_keys, 1);
     const int has_lat = a->lat_keys > 0;
-    const int slots = cu * split_occupancy(has_lat ? lat_ks : 8, has_lat ? 8 : 0);
-    // Raw rows: splits of two 16-row tiles.
-    const int raw_req0 = a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + 31) / 32);
-    const int raw_wg = (int)B * ((int)(Hkv + kWaves - 1) / kWaves) * raw_req0;
+    // Raw rows: splits of two 16-row tiles (four beside paged rows, whose
+    // many short sequences would otherwise launch a raw workgroup per 32 rows
+    // of every sequence: 64 sequences, 138 against 144 us a step).
+    const int raw_rows = pg ? 64 : 32;
+    const int raw_req0 =
+        a->raw_splits > 0 ? a->raw_splits : (int)std::max<int64_t>(1, (a->raw_keys + raw_rows - 1) / raw_rows);
     // Dense rows: a whole number of latent workgroups per CU.  Each CU streams
     // its workgroups' rows at about the same rate, so a launch whose
     // workgroups do not spread evenly over the CUs lasts as long as its most
@@ -1965,9 +1967,12 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     // 30.6 us).  Tiles of 64 latent columns and wider take one workgroup a CU,
     // narrower ones two.
     int lat_target = cu * (lat_ks <= 2 ? 2 : 1);
-    // Paged rows (compact schedule): the splits of all sequences fill the
-    // resident slots left by the raw workgroups.
-    int fill_target = std::max(slots - raw_wg, slots / 2);
+    // Paged rows (compact schedule): 3.5 split items per CU.  The page reads
+    // (2 KiB chunks through the table) want more workgroups in flight than the
+    // dense rows do; 64 sequences of U[1K, 128K] tokens ran a step in 143 us at
+    // 3.5 per CU, 149 us at 3, 156-165 us at 4 and 174 us filling the slots
+    // left by the raw workgroups.
+    int fill_target = cu * 7 / 2;
     // Keep the latent split count within the fast combine's reach (one latent
     // partial register pass, and one split per combine thread with the raw
     // ones): at small batches the slots would otherwise fill with ever shorter
@@ -1989,7 +1994,7 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     p->lat = plan_segment((int)B, 1, P, cols, (int)nl, span, rv, lat_req, lat_target);
     if (pg && a->lat_splits <= 0) {
         // Compact schedule: size the splits from the total row count so the
-        // non-empty splits of all sequences fill the resident slots once.
+        // non-empty splits of all sequences make about fill_target items.
         const int64_t total = pg->rows_total > 0 ? pg->rows_total : B * nl;
         int64_t rps = (total + fill_target - 1) / fill_target;
         rps = std::max<int64_t>(rps, (nl + std::min(kMaxSplits, fast_cap) - 1) / std::min(kMaxSplits, fast_cap));

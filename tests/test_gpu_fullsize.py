@@ -255,7 +255,7 @@ def test_c4_paged_full_size_indices_and_parity(device):
         assert torch.equal(raw_v[b, :, :n], want[:, 1].transpose(0, 1))
     # 2. the paged decode reads the same rows: bit-identical to gather + decode
     scale = D ** -0.5
-    common = dict(block_diagonal=True, raw_lengths=pc['raw_len'])
+    common = dict(block_diagonal=True, raw_lengths=pc['raw_len'], raw_splits=4)   # one split plan on both sides
     dense = kernels.latent_decode(pc['q'], raw_k.transpose(1, 2), raw_v.transpose(1, 2), lat_k, lat_v, pc['up_k'],
                                   pc['up_v'], scale, lat_lengths=pc['lat_len'], lat_splits=48, **common)
     paged = kernels.paged_latent_decode(pc['q'], raw_k.transpose(1, 2), raw_v.transpose(1, 2), pc['pool'],

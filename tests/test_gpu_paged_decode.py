@@ -77,13 +77,15 @@ def test_paged_equals_gather_then_decode_bitwise(device, layout_args, lengths, s
     c = _case(device, layout_args, lengths, raw_lengths, seed=len(lengths) + splits)
     lat_k, lat_v = _dense(c)
     scale = D ** -0.5
+    # the same split plan on both sides (the automatic plans differ: paged rows
+    # take a compact schedule and longer raw splits)
     want, want_lse = kernels.latent_decode(c['q'], c['raw_k'], c['raw_v'], lat_k, lat_v, c['up_k'], c['up_v'],
                                            scale, block_diagonal=True, raw_lengths=c['raw_lengths'],
-                                           lat_lengths=c['lengths'], lat_splits=splits)
+                                           lat_lengths=c['lengths'], lat_splits=splits, raw_splits=2)
     got, got_lse = kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'],
                                                c['lengths'], c['lat_keys'], c['layout'], c['up_k'], c['up_v'],
                                                scale, block_diagonal=True, raw_lengths=c['raw_lengths'],
-                                               lat_splits=splits)
+                                               lat_splits=splits, raw_splits=2)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.equal(got_lse, want_lse)
