@@ -22,6 +22,8 @@ def assert_close(actual, expected, max_abs=MAX_ABS, mean_abs=MEAN_ABS, what=''):
     assert actual.shape == expected.shape, (actual.shape, expected.shape)
     assert np.isfinite(actual).all(), f'{what}: non-finite output'
     err = np.abs(actual - expected)
+    if what:
+        print(f'{what}: max abs err {err.max():.3e}, mean abs err {err.mean():.3e}', flush=True)
     assert err.max() <= max_abs, f'{what}: max abs err {err.max():.3e} > {max_abs}'
     assert err.mean() <= mean_abs, f'{what}: mean abs err {err.mean():.3e} > {mean_abs}'
     return err.max(), err.mean()
