@@ -120,6 +120,12 @@ int slimkv_attention_forward(const slimkv_attention_args* a, void* workspace,
  * up_k_t  optional [Hkv, Rk/Hkv, D] per-head transposed K bases made by
  *         slimkv_prepare_latent_bases; with block_diagonal the query
  *         absorption then runs on MFMA in one wavefront per (b, KV head).
+ * lat_k2 / lat_v2 optional second latent segment: rows [lat_split, lat_keys)
+ *         of every sequence lie there (row i at index i - lat_split, strides
+ *         lk2_sb/lk2_sn, lv2_sb/lv2_sn) and rows [0, lat_split) at lat_k /
+ *         lat_v, so a growing history and the current window are read where
+ *         they lie instead of being joined each step (fa2_decode.py:133-135
+ *         concatenates them); 0 < lat_split < lat_keys; dense rows only.
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_latent_decode_args {
     const void* q;  int64_t q_sb, q_sl, q_sh;
@@ -143,6 +149,9 @@ typedef struct slimkv_latent_decode_args {
     float* lse;
     int32_t raw_splits, lat_splits; /* 0 = automatic */
     const void* up_k_t;
+    const void* lat_k2; int64_t lk2_sb, lk2_sn;
+    const void* lat_v2; int64_t lv2_sb, lv2_sn;
+    int64_t lat_split;
 } slimkv_latent_decode_args;
 
 size_t slimkv_latent_decode_workspace(const slimkv_latent_decode_args* a);
@@ -346,6 +355,41 @@ typedef struct slimkv_merge_args {
 } slimkv_merge_args;
 
 int slimkv_merge(const slimkv_merge_args* a, void* stream);
+
+/* Element types of the dtype-generic entry points below. */
+#define SLIMKV_DTYPE_BF16 0
+#define SLIMKV_DTYPE_F16 1
+#define SLIMKV_DTYPE_F32 2
+
+/* slimkv_merge for bf16, fp16 or fp32 branch outputs of type `dtype`, out in
+ * the same type (contiguous [B, H, L, D]; any width, element strides).
+ * Replaces merge_attention's torch arithmetic (slimkv/llama3/fa2_decode.py:
+ * 57-66), which the reference runs wherever its fused merge does not apply. */
+int slimkv_merge_typed(const slimkv_merge_args* a, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * fp32 eager attention.
+ * Replaces latent_decode.eager_forward (slimkv/llama3/latent_decode.py:16-41),
+ * the reference's fp32 attention: q [B, Lq, Hq, R], k [B, N, Hk, R],
+ * v [B, N, Hk, Rv] of one dtype (element strides, last dim contiguous) meet in
+ * fp32; bottom-right causal mask when `causal`; rows that see no key give LSE
+ * -inf and a zero output.  out [B, Lq, Hq, Rv] in the inputs' dtype (element
+ * strides), lse [B, Hq, Lq] fp32 contiguous; `scores` is a workspace of
+ * B * Hq * Lq * N floats.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_eager_attention_args {
+    const void* q; int64_t q_sb, q_sl, q_sh;
+    const void* k; int64_t k_sb, k_sn, k_sh;
+    const void* v; int64_t v_sb, v_sn, v_sh;
+    void* out; int64_t o_sb, o_sl, o_sh;
+    float* lse;
+    float* scores;
+    int64_t batch, queries, heads, kv_heads, keys, rank, rank_v;
+    double scale;
+    int32_t dtype, causal;
+} slimkv_eager_attention_args;
+
+int slimkv_eager_attention(const slimkv_eager_attention_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * Projections of a decode step's rows (one token per sequence of a lockstep

@@ -59,6 +59,9 @@ LatentDecodeArgs = _struct('slimkv_latent_decode_args', [
     ('lse', c_ptr),
     ('raw_splits', c_i32), ('lat_splits', c_i32),
     ('up_k_t', c_ptr),
+    ('lat_k2', c_ptr), *_i64s('lk2_sb', 'lk2_sn'),
+    ('lat_v2', c_ptr), *_i64s('lv2_sb', 'lv2_sn'),
+    ('lat_split', c_i64),
 ])
 
 ReconstructArgs = _struct('slimkv_reconstruct_args', [
@@ -127,6 +130,22 @@ MergeArgs = _struct('slimkv_merge_args', [
     ('out', c_ptr),
     *_i64s('batch', 'heads', 'length', 'dim'),
 ])
+
+EagerAttentionArgs = _struct('slimkv_eager_attention_args', [
+    ('q', c_ptr), *_i64s('q_sb', 'q_sl', 'q_sh'),
+    ('k', c_ptr), *_i64s('k_sb', 'k_sn', 'k_sh'),
+    ('v', c_ptr), *_i64s('v_sb', 'v_sn', 'v_sh'),
+    ('out', c_ptr), *_i64s('o_sb', 'o_sl', 'o_sh'),
+    ('lse', c_ptr),
+    ('scores', c_ptr),
+    *_i64s('batch', 'queries', 'heads', 'kv_heads', 'keys', 'rank', 'rank_v'),
+    ('scale', c_f64),
+    ('dtype', c_i32),
+    ('causal', c_i32),
+])
+
+# Element types of the dtype-generic entry points (SLIMKV_DTYPE_*).
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
 
 PrefillAttentionArgs = _struct('slimkv_prefill_attention_args', [
     ('q', c_ptr), *_i64s('q_sb', 'q_sl', 'q_sh'),
@@ -206,6 +225,8 @@ SIGNATURES = {
     'slimkv_decode_qkv': (ctypes.c_int, [ctypes.POINTER(DecodeQKVArgs), c_ptr]),
     'slimkv_prefill_rope': (ctypes.c_int, [ctypes.POINTER(PrefillRopeArgs), c_ptr]),
     'slimkv_merge': (ctypes.c_int, [ctypes.POINTER(MergeArgs), c_ptr]),
+    'slimkv_merge_typed': (ctypes.c_int, [ctypes.POINTER(MergeArgs), ctypes.c_int, c_ptr]),
+    'slimkv_eager_attention': (ctypes.c_int, [ctypes.POINTER(EagerAttentionArgs), c_ptr]),
     'slimkv_prefill_attention': (ctypes.c_int, [ctypes.POINTER(PrefillAttentionArgs), c_ptr]),
     'slimkv_down_project_workspace': (ctypes.c_size_t, [ctypes.POINTER(DownProjectArgs)]),
     'slimkv_down_project': (ctypes.c_int, [ctypes.POINTER(DownProjectArgs), c_ptr, ctypes.c_size_t, c_ptr]),
@@ -216,7 +237,7 @@ SIGNATURES = {
     'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20

@@ -14,7 +14,7 @@ PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / 'csrc'
 LIBRARY = PACKAGE / 'libslimkv_hip.so'
 SOURCES = ['attention.hip', 'rope.hip', 'recon.hip', 'paged.hip', 'prefill.hip', 'down.hip', 'project.hip',
-           'probe.hip']
+           'eager.hip', 'probe.hip']
 
 FLAGS = [
     '--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared',

@@ -64,6 +64,11 @@ struct Seg {
     // Compact schedule: workgroup items enumerate only the non-empty splits of
     // each batch entry (needs seqlens); items past the last one exit at once.
     int compact;
+    // Two-segment rows (SEG2 instances): rows [0, n1) of a sequence at k / v,
+    // rows [n1, n) at k2 / v2, row i at index i - n1 there.
+    const uint16_t* k2; int64_t k2_sb, k2_sn;
+    const uint16_t* v2; int64_t v2_sb, v2_sn;
+    int n1;
 };
 
 struct SplitParams {
@@ -174,15 +179,29 @@ __device__ __forceinline__ void rope_operand(u32x4 (&x)[4], const RopeRow& t) {
     }
 }
 
-template <int KS>
-__device__ __forceinline__ void load_tile(TileRegs<KS>& t, const uint16_t* kbase, const uint16_t* vbase,
-                                          int64_t k_sn, int64_t v_sn, int r0, int last_row,
+// Row addresses of dense rows: one tensor, or two tensors split at row n1
+// (a sequence's history and its current window, each read where it lies).
+struct OneRows {
+    const uint16_t* base; int64_t sn;
+    __device__ __forceinline__ const uint16_t* row(int r) const { return base + (int64_t)r * sn; }
+};
+struct TwoRows {
+    const uint16_t* base; int64_t sn;
+    const uint16_t* base2; int64_t sn2;
+    int n1;
+    __device__ __forceinline__ const uint16_t* row(int r) const {
+        return r < n1 ? base + (int64_t)r * sn : base2 + (int64_t)(r - n1) * sn2;
+    }
+};
+
+template <int KS, class Rows>
+__device__ __forceinline__ void load_tile(TileRegs<KS>& t, const Rows& krows, const Rows& vrows, int r0, int last_row,
                                           int span_k, int span_v, int col, int grp, int lane) {
     constexpr int VT = KS;
     // K: lane (row = col, group grp) takes elements [32c + 8*grp, +8) of the
     // tile's k range for c < KS/2 -- a row's four groups read 64 contiguous bytes.
     {
-        const uint16_t* src = kbase + (int64_t)min(r0 + col, last_row) * k_sn;
+        const uint16_t* src = krows.row(min(r0 + col, last_row));
 #pragma unroll
         for (int c = 0; c < KS / 2; ++c) {
             const int kk = 32 * c + 8 * grp;
@@ -196,7 +215,7 @@ __device__ __forceinline__ void load_tile(TileRegs<KS>& t, const uint16_t* kbase
         const int p = 64 * c + lane;
         const int row = r0 + p / (2 * VT);
         const int pc = p % (2 * VT);
-        const uint16_t* src = vbase + (int64_t)min(row, last_row) * v_sn + (8 * pc + 8 <= span_v ? 8 * pc : 0);
+        const uint16_t* src = vrows.row(min(row, last_row)) + (8 * pc + 8 <= span_v ? 8 * pc : 0);
         t.v[c] = tile_load<StreamLoads<KS>::value>(src);
     }
 }
@@ -317,7 +336,7 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
 // never exchange data, and write their own partials.
 // PAGED: 0 dense rows, 1 rows through per-lane page ids, 2 rows through the
 // tile's two pages (pages of at least 16 rows).
-template <int KS, int DEPTH, int PAGED = 0>
+template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int Lq, int Hq,
                                               float scale_log2, char* lds) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
@@ -414,7 +433,15 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
 
     auto fetch = [&](TileRegs<KS>& tr, int it) {
         const int r0 = it < ntile ? tile_row(it) : r_begin;
-        load_tile<KS>(tr, kbase, vbase, sg.k_sn, sg.v_sn, r0, last_row, span_k, span_v, col, grp, lane);
+        if constexpr (SEG2) {
+            const uint16_t* k2 = sg.k2 + (int64_t)b * sg.k2_sb + (int64_t)h * sg.k_sh + k_off;
+            const uint16_t* v2 = sg.v2 + (int64_t)b * sg.v2_sb + (int64_t)h * sg.v_sh + v_off;
+            load_tile<KS>(tr, TwoRows{kbase, sg.k_sn, k2, sg.k2_sn, sg.n1}, TwoRows{vbase, sg.v_sn, v2, sg.v2_sn, sg.n1},
+                          r0, last_row, span_k, span_v, col, grp, lane);
+        } else {
+            load_tile<KS>(tr, OneRows{kbase, sg.k_sn}, OneRows{vbase, sg.v_sn}, r0, last_row, span_k, span_v, col,
+                          grp, lane);
+        }
     };
     // Paged rows: the page ids of a tile are loaded two tiles ahead of its
     // data.  An entry outside the pool that a row of the sequence needs sets
@@ -651,7 +678,7 @@ struct SplitDepth {
     static constexpr int value = 2;
 };
 
-template <int KA, int KB, int PAGED = 0>
+template <int KA, int KB, int PAGED = 0, int SEG2 = 0>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SplitWaves<KA>::value)))
 split_kernel(SplitParams prm) {
     constexpr int LA = SplitLds<KA>::bytes;
@@ -665,7 +692,7 @@ split_kernel(SplitParams prm) {
         }
         w -= prm.seg[1].nwg;
     }
-    split_segment<KA, SplitDepth<KA>::value, PAGED>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
+    split_segment<KA, SplitDepth<KA>::value, PAGED, SEG2>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -1603,6 +1630,7 @@ namespace {
 thread_local std::string g_error;
 
 hipError_t dispatch_split(int ka, int kb, const struct SplitParams& prm, int grid, hipStream_t st);
+hipError_t dispatch_split_seg2(int ka, const struct SplitParams& prm, int grid, hipStream_t st);
 template <int MODE>
 hipError_t launch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
     switch (ka) {
@@ -1620,8 +1648,10 @@ hipError_t dispatch_split_paged(int ka, const SplitParams& prm, int grid, hipStr
     return prm.seg[0].slots >= 16 ? launch_split_paged<2>(ka, prm, grid, st) : launch_split_paged<1>(ka, prm, grid, st);
 }
 
-hipError_t launch_split_any(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st, bool paged = false) {
-    return paged ? dispatch_split_paged(ka, prm, grid, st) : dispatch_split(ka, kb, prm, grid, st);
+hipError_t launch_split_any(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st, bool paged = false,
+                            bool seg2 = false) {
+    if (paged) return dispatch_split_paged(ka, prm, grid, st);
+    return seg2 ? dispatch_split_seg2(ka, prm, grid, st) : dispatch_split(ka, kb, prm, grid, st);
 }
 
 int round_even_tile(int width) {
@@ -1675,10 +1705,24 @@ SegPlan plan_segment(int B, int hk, int P, int cols, int n, int span_k, int wown
     return sp;
 }
 
-template <int KA, int KB>
+template <int KA, int KB, int SEG2 = 0>
 hipError_t launch_split(const SplitParams& prm, int grid, hipStream_t st) {
-    hipLaunchKernelGGL((split_kernel<KA, KB>), dim3(grid), dim3(kThreads), 0, st, prm);
+    hipLaunchKernelGGL((split_kernel<KA, KB, 0, SEG2>), dim3(grid), dim3(kThreads), 0, st, prm);
     return hipGetLastError();
+}
+
+// Latent rows in two tensors (the fused decode's dense rows only).
+hipError_t dispatch_split_seg2(int ka, const SplitParams& prm, int grid, hipStream_t st) {
+    switch (ka) {
+        case 2: return launch_split<2, 8, 1>(prm, grid, st);
+        case 4: return launch_split<4, 8, 1>(prm, grid, st);
+        case 6: return launch_split<6, 8, 1>(prm, grid, st);
+        case 8: return launch_split<8, 8, 1>(prm, grid, st);
+        case 12: return launch_split<12, 8, 1>(prm, grid, st);
+        case 16: return launch_split<16, 8, 1>(prm, grid, st);
+        case 24: return launch_split<24, 8, 1>(prm, grid, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t dispatch_split(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st) {
@@ -1800,7 +1844,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 9; }
+extern "C" int slimkv_abi_version(void) { return 10; }
 
 extern "C" size_t slimkv_attention_workspace(const slimkv_attention_args* a) {
     AttnPlan plan{};
@@ -1912,6 +1956,15 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
         return fail(SLIMKV_EINVAL, "invalid key counts");
     if (a->raw_keys <= 0) return fail(SLIMKV_EINVAL, "the raw branch always holds the current token");
     if (!pg && a->lat_keys > 0 && (!a->lat_k || !a->lat_v)) return fail(SLIMKV_EINVAL, "null latent pointer");
+    if (a->lat_k2 || a->lat_v2) {
+        if (pg) return fail(SLIMKV_EINVAL, "paged rows take no second latent segment");
+        if (!a->lat_k2 || !a->lat_v2 || a->lat_split <= 0 || a->lat_split >= a->lat_keys)
+            return fail(SLIMKV_EINVAL, "a second latent segment needs both tensors and 0 < lat_split < lat_keys");
+        if (!aligned8(a->lk2_sb) || !aligned8(a->lk2_sn) || !aligned8(a->lv2_sb) || !aligned8(a->lv2_sn) ||
+            !ptr_aligned16(a->lat_k2) || !ptr_aligned16(a->lat_v2))
+            return fail(SLIMKV_EINVAL, "second latent segment: strides must be multiples of 8 elements, 16-byte aligned");
+        if (a->lat_keys >= ((int64_t)1 << 31)) return fail(SLIMKV_EINVAL, "too many latent rows");
+    }
     if (a->cos && (!a->sin || a->rope_rows <= 0)) return fail(SLIMKV_EINVAL, "RoPE needs sin and a table size");
     if (a->cos && !a->q_positions && a->rope_rows < B * Lq)
         return fail(SLIMKV_EINVAL, "without query positions the RoPE tables hold one row per query");
@@ -2133,6 +2186,11 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
         l.part_acc = reinterpret_cast<float*>(ws + p.lacc_off);
         l.wown = bd ? Rv / Hkv : Rv;
         l.nwg = p.lat.nwg;
+        if (a->lat_k2) {
+            l.k2 = static_cast<const uint16_t*>(a->lat_k2); l.k2_sb = a->lk2_sb; l.k2_sn = a->lk2_sn;
+            l.v2 = static_cast<const uint16_t*>(a->lat_v2); l.v2_sb = a->lv2_sb; l.v2_sn = a->lv2_sn;
+            l.n1 = (int)a->lat_split;
+        }
         if (pg) {
             l.k = pg->pages + pg->sink; l.v = pg->pages + pg->sink + Rk;
             l.k_sb = l.v_sb = 0; l.k_sn = l.v_sn = Rk + Rv;
@@ -2149,7 +2207,8 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     if (paged && ka > 8) return fail(SLIMKV_EUNSUP, "paged decode handles latent tiles up to 128 wide");
     const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
     if (stages & SLIMKV_STAGE_ATTEND) {
-        rc = check_hip(launch_split_any(ka, kb, prm, grid, st, paged), "split kernel launch");
+        rc = check_hip(launch_split_any(ka, kb, prm, grid, st, paged, has_lat && a->lat_k2 != nullptr),
+                       "split kernel launch");
         if (rc != SLIMKV_OK) return rc;
     }
     if (!(stages & SLIMKV_STAGE_COMBINE)) return SLIMKV_OK;

@@ -1,17 +1,19 @@
 """Drop-in for slimkv.llama3.decode_ops: fused decode RoPE and LSE merge.
 
-Same contract as slimkv/llama3/decode_ops.py:14-48: the functions return None
-(the caller's torch path) only where the reference does -- tensors off the GPU,
-a dtype other than bf16, or autograd in use.  Device bf16 tensors always run
-the HIP kernels (bit-exact RoPE, fp32 merge).
+Contract of slimkv/llama3/decode_ops.py:14-48: the functions return None (the
+caller's torch path) for tensors off the GPU, a dtype other than bf16 / fp16,
+or autograd in use.  The merge runs the HIP kernel for device bf16 and fp16
+tensors (fp32 arithmetic, one rounding), as the reference's fused merge does.
+The RoPE kernel is bf16-exact only: fp16 RoPE returns None, and the caller
+rotates with its own module, as it does where the reference lacks Triton.
 """
 import torch
 
 from . import kernels
 
 
-def _skip(x, *others):
-    return (not x.is_cuda or x.dtype != torch.bfloat16
+def _skip(x, *others, dtypes=(torch.bfloat16,)):
+    return (not x.is_cuda or x.dtype not in dtypes
             or (torch.is_grad_enabled() and any(t.requires_grad for t in (x, *others))))
 
 
@@ -27,6 +29,6 @@ def fused_rope(q, k, rope, query_positions, raw_indices, sink, history):
 
 def fused_merge(raw, raw_lse, latent, latent_lse):
     """raw/latent [B,H,L,D], LSEs [B,H,L] -> merged [B,H,L,D] in raw.dtype."""
-    if _skip(raw, latent):
+    if _skip(raw, latent, dtypes=(torch.bfloat16, torch.float16)) or latent.dtype != raw.dtype:
         return None
     return kernels.merge(raw, raw_lse, latent, latent_lse)

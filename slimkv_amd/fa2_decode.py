@@ -57,12 +57,23 @@ def project_value(output, weight, kv_heads):
 
 
 def merge_attention(raw_out, raw_lse, latent_out, latent_lse):
-    """Outputs BHQD, LSE BHQ; merged in fp32, rounded once (fa2_decode.py:57-66)."""
+    """Outputs BHQD, LSE BHQ; merged in fp32, rounded once (fa2_decode.py:57-66).
+
+    Where the reference's fused merge does not apply (fp32 outputs) it merges
+    with torch arithmetic; here every dtype (bf16, fp16, fp32) runs the HIP
+    merge.  CPU tensors and autograd raise: this library has no CPU or
+    gradient path."""
     from .decode_ops import fused_merge
     fused = fused_merge(raw_out, raw_lse, latent_out, latent_lse)
-    if fused is None:
-        raise ValueError('slimkv_amd merges device bf16 tensors only')
-    return fused
+    if fused is not None:
+        return fused
+    if not (raw_out.is_cuda and latent_out.is_cuda):
+        raise ValueError('slimkv_amd merges on the GPU; CPU tensors are not supported')
+    if torch.is_grad_enabled() and (raw_out.requires_grad or latent_out.requires_grad):
+        raise ValueError('slimkv_amd merge is inference-only (no autograd)')
+    if latent_out.dtype != raw_out.dtype:
+        latent_out = latent_out.to(raw_out.dtype)
+    return kernels.merge(raw_out, raw_lse, latent_out, latent_lse)
 
 
 def eligible(attention, hidden_states, past_key_value, output_attentions):
@@ -131,21 +142,27 @@ def decode(attention, hidden, position_ids, past_key_value, forward=None):
     q = q.reshape(batch, length, heads, dim).transpose(1, 2)
     raw_k = cat_tensor([pk.sink, pk.raw, new_k], dim=2)
     raw_v = cat_tensor([pv.sink, pv.raw, new_v], dim=2)
-    latent_k = cat_tensor([pk.history, pk.window, kl], dim=2)
-    latent_v = cat_tensor([pv.history, pv.window, vl], dim=2)
     sink_len = 0 if pk.sink is None else pk.sink.shape[2]
     history_len = 0 if pk.history is None else pk.history.shape[2]
     q, raw_k = _rotate(attention, q, raw_k, position_ids, length, pk, sink_len, history_len)
     scale = 1.0 / math.sqrt(dim)
     if forward is None:
+        # The history's latent rows are read where they lie (first segment);
+        # only the current window and the new beacon are joined (second).
+        window_k = cat_tensor([pk.window, kl], dim=2)
+        window_v = cat_tensor([pv.window, vl], dim=2)
+        hist_k = None if pk.history is None else pk.history[:, 0]
+        hist_v = None if pv.history is None else pv.history[:, 0]
         out, _ = kernels.latent_decode(
-            q.transpose(1, 2), raw_k.transpose(1, 2), raw_v.transpose(1, 2),
-            None if latent_k is None else latent_k[:, 0], None if latent_v is None else latent_v[:, 0],
+            q.transpose(1, 2), raw_k.transpose(1, 2), raw_v.transpose(1, 2), hist_k, hist_v,
             uk.weight, uv.weight, scale, up_k_bias=uk.bias, up_v_bias=uv.bias,
             block_diagonal=is_block_diagonal(uk.weight, kv_heads) and is_block_diagonal(uv.weight, kv_heads),
-            lat_causal=bool(size))
+            lat_causal=bool(size), lat_k2=None if window_k is None else window_k[:, 0],
+            lat_v2=None if window_v is None else window_v[:, 0])
         output = out.reshape(batch, length, attention.hidden_size)
         return attention.o_proj_with_beacon(output, size, indices), None, update
+    latent_k = cat_tensor([pk.history, pk.window, kl], dim=2)
+    latent_v = cat_tensor([pv.history, pv.window, vl], dim=2)
     # Two-branch composition with a caller-supplied attention forward.
     raw_out, raw_lse = forward(q.transpose(1, 2), raw_k.transpose(1, 2), raw_v.transpose(1, 2), scale, False)
     raw_out = raw_out[..., :dim].transpose(1, 2)

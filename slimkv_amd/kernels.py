@@ -201,22 +201,38 @@ def prepare_latent_bases(up_k, kv_heads):
     return bases
 
 
+def _latent_rows(lat_k, lat_v, Rk, Rv):
+    lat_k, lat_v = _last_contiguous(lat_k), _last_contiguous(lat_v)
+    if lat_k.dim() == 4:
+        lat_k, lat_v = lat_k.squeeze(2), lat_v.squeeze(2)
+    if lat_k.shape[-1] != Rk or lat_v.shape[-1] != Rv:
+        raise ValueError('latent widths differ from the up-projection ranks')
+    return lat_k, lat_v
+
+
 def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias, block_diagonal,
                  lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse,
-                 prepared_bases=True, lat_rows=None):
-    _need_device(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v)
-    _need_bf16(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, up_k_bias, up_v_bias)
+                 prepared_bases=True, lat_rows=None, lat_k2=None, lat_v2=None):
+    _need_device(q, raw_k, raw_v, lat_k, lat_v, lat_k2, lat_v2, up_k, up_v)
+    _need_bf16(q, raw_k, raw_v, lat_k, lat_v, lat_k2, lat_v2, up_k, up_v, up_k_bias, up_v_bias)
     B, Lq, Hq, D = q.shape
     Nr, Hkv = raw_k.shape[1], raw_k.shape[2]
     Rk, Rv = up_k.shape[1], up_v.shape[1]
+    # a second latent segment joins the first one's rows; an empty segment drops out
+    if lat_k2 is not None and lat_k2.shape[1] == 0:
+        lat_k2 = lat_v2 = None
+    if lat_k2 is not None and (lat_k is None or lat_k.shape[1] == 0):
+        lat_k, lat_v, lat_k2, lat_v2 = lat_k2, lat_v2, None, None
     Nl = (0 if lat_rows is None else int(lat_rows)) if lat_k is None else lat_k.shape[1]
+    split = 0
     q, raw_k, raw_v = (_last_contiguous(x) for x in (q, raw_k, raw_v))
     if lat_k is not None:
-        lat_k, lat_v = _last_contiguous(lat_k), _last_contiguous(lat_v)
-        if lat_k.dim() == 4:
-            lat_k, lat_v = lat_k.squeeze(2), lat_v.squeeze(2)
-        if lat_k.shape[-1] != Rk or lat_v.shape[-1] != Rv:
-            raise ValueError('latent widths differ from the up-projection ranks')
+        lat_k, lat_v = _latent_rows(lat_k, lat_v, Rk, Rv)
+    if lat_k2 is not None:
+        lat_k2, lat_v2 = _latent_rows(lat_k2, lat_v2, Rk, Rv)
+        if lat_k2.shape[0] != lat_k.shape[0]:
+            raise ValueError('latent segments differ in batch size')
+        split, Nl = Nl, Nl + lat_k2.shape[1]
     up_k, up_v = up_k.contiguous(), up_v.contiguous()
     if out is None:
         out = torch.empty(B, Lq, Hq, D, dtype=BF16, device=q.device)
@@ -250,8 +266,10 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
         _ptr(lat_lengths), Nl, int(bool(lat_causal)), int(bool(block_diagonal)),
         _ptr(up_k), _ptr(up_k_bias), _ptr(up_v), _ptr(up_v_bias),
         B, Lq, Hq, Hkv, D, Rk, Rv, float(scale),
-        _ptr(out), *out.stride()[:3], _ptr(lse), int(raw_splits), int(lat_splits), _ptr(bases))
-    keep = (q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, cos, sin, q_positions, bases)
+        _ptr(out), *out.stride()[:3], _ptr(lse), int(raw_splits), int(lat_splits), _ptr(bases),
+        _ptr(lat_k2), *(lat_k2.stride()[:2] if lat_k2 is not None else (0, 0)),
+        _ptr(lat_v2), *(lat_v2.stride()[:2] if lat_v2 is not None else (0, 0)), split)
+    keep = (q, raw_k, raw_v, lat_k, lat_v, lat_k2, lat_v2, up_k, up_v, cos, sin, q_positions, bases)
     return a, out, lse, keep
 
 
@@ -271,7 +289,7 @@ def query_rope_rows(cos, sin, q_positions):
 def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias=None, up_v_bias=None,
                   block_diagonal=False, lat_causal=False, q_positions=None, cos=None, sin=None,
                   raw_lengths=None, lat_lengths=None, raw_splits=0, lat_splits=0, out=None, lse=None,
-                  workspace=None, prepared_bases=True, stages=_lib.STAGE_ALL):
+                  workspace=None, prepared_bases=True, stages=_lib.STAGE_ALL, lat_k2=None, lat_v2=None):
     """Fused latent beacon decode for one layer.
 
     q [B,Lq,Hq,D] (rotated in-kernel at q_positions when cos/sin are given;
@@ -284,11 +302,14 @@ def latent_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, up_k_bias
     block-diagonal bases the query absorption runs on MFMA from per-head bases
     prepared once per weight (`prepared_bases`, the default).  `stages`
     (a mask of _lib.STAGE_*) runs part of the call; the stages of one decode
-    hand over through `workspace`, which is then required.
+    hand over through `workspace`, which is then required.  lat_k2 / lat_v2
+    [B, N2, R*] hold latent rows that follow lat_k / lat_v's (a history and
+    the current window read where they lie, without joining them).
     """
     a, out, lse, keep = _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias,
                                      block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
-                                     lat_lengths, raw_splits, lat_splits, out, lse, prepared_bases)
+                                     lat_lengths, raw_splits, lat_splits, out, lse, prepared_bases,
+                                     lat_k2=lat_k2, lat_v2=lat_v2)
     nbytes = lib().slimkv_latent_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)
@@ -555,10 +576,22 @@ def prefill_rope(q, k, cos, sin, positions, roles, sink):
     return oq, ok
 
 
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+
+def _dtype_code(*tensors):
+    dt = tensors[0].dtype
+    if dt not in _DTYPES or any(t.dtype != dt for t in tensors):
+        raise ValueError(f'expected one of bfloat16, float16, float32 for every tensor, found '
+                         f'{[t.dtype for t in tensors]}')
+    return _DTYPES[dt]
+
+
 def merge(raw, raw_lse, latent, latent_lse):
-    """raw/latent [B,H,L,D] bf16, LSEs [B,H,L] fp32 -> contiguous [B,H,L,D] bf16."""
+    """raw/latent [B,H,L,D] (bf16, fp16 or fp32), LSEs [B,H,L] -> contiguous
+    [B,H,L,D] in the branches' dtype, merged in fp32 and rounded once."""
     _need_device(raw, latent, raw_lse, latent_lse)
-    _need_bf16(raw, latent)
+    code = _dtype_code(raw, latent)
     raw, latent = _last_contiguous(raw), _last_contiguous(latent)
     raw_lse, latent_lse = raw_lse.float(), latent_lse.float()
     out = torch.empty(raw.shape, dtype=raw.dtype, device=raw.device)
@@ -566,8 +599,34 @@ def merge(raw, raw_lse, latent, latent_lse):
         _ptr(raw), *raw.stride()[:3], _ptr(latent), *latent.stride()[:3],
         _ptr(raw_lse), *raw_lse.stride(), _ptr(latent_lse), *latent_lse.stride(),
         _ptr(out), *raw.shape)
-    check(lib().slimkv_merge(ctypes.byref(a), _lib.stream_handle(raw.device)))
+    vector = (code == _lib.DTYPE_BF16 and raw.shape[-1] % 8 == 0
+              and all(x % 8 == 0 for x in (*raw.stride()[:3], *latent.stride()[:3]))
+              and all(t.data_ptr() % 16 == 0 for t in (raw, latent, out)))
+    if vector:
+        check(lib().slimkv_merge(ctypes.byref(a), _lib.stream_handle(raw.device)))
+    else:
+        check(lib().slimkv_merge_typed(ctypes.byref(a), code, _lib.stream_handle(raw.device)))
     return out
+
+
+def eager_attention(q, k, v, scale, causal=False):
+    """fp32 attention (latent_decode.eager_forward arithmetic) for bf16, fp16 or
+    fp32 BSHD tensors: q [B,Lq,H,R], k [B,N,Hk,R], v [B,N,Hk,Rv] ->
+    (out [B,Lq,H,Rv] in q's dtype, lse [B,H,Lq] fp32)."""
+    _need_device(q, k, v)
+    code = _dtype_code(q, k, v)
+    q, k, v = (_last_contiguous(x) for x in (q, k, v))
+    B, Lq, H, R = q.shape
+    N, Hk = k.shape[1], k.shape[2]
+    out = torch.empty(B, Lq, H, v.shape[-1], dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device)
+    scores = torch.empty(max(B * H * Lq * N, 1), dtype=torch.float32, device=q.device)
+    a = _lib.EagerAttentionArgs(
+        _ptr(q), *q.stride()[:3], _ptr(k), *k.stride()[:3], _ptr(v), *v.stride()[:3],
+        _ptr(out), *out.stride()[:3], _ptr(lse), _ptr(scores),
+        B, Lq, H, Hk, N, R, v.shape[-1], float(scale), code, int(bool(causal)))
+    check(lib().slimkv_eager_attention(ctypes.byref(a), _lib.stream_handle(q.device)))
+    return out, lse
 
 
 def default_scale(head_dim):

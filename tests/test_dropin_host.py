@@ -50,6 +50,18 @@ def test_fused_ops_defer_to_caller_off_gpu_and_kernels_refuse_cpu():
         kernels.attention_forward(q.transpose(1, 2), k.transpose(1, 2), k.transpose(1, 2), 0.1)
 
 
+def test_eager_forward_refuses_cpu_tensors():
+    """The reference's eager_forward also runs on the CPU; this library has no
+    CPU path, so CPU tensors raise before anything is launched."""
+    from slimkv_amd.latent_decode import eager_forward
+    q = torch.zeros(1, 1, 4, 32)
+    k = torch.zeros(1, 3, 2, 32)
+    with pytest.raises(ValueError, match='GPU'):
+        eager_forward(q, k, k, 0.1)
+    with pytest.raises(ValueError, match='shapes'):
+        eager_forward(q, k[..., :16], k, 0.1)
+
+
 def test_prepare_metadata_gate():
     from slimkv_amd.prefill_ops import prepare_metadata
     config = SimpleNamespace(beacon_prefill_fast=True, _slimkv_decode_step=False,

@@ -33,7 +33,8 @@ def test_library_exports_every_declared_symbol():
 def STRUCTS(_lib):
     return (_lib.AttentionArgs, _lib.LatentDecodeArgs, _lib.ReconstructArgs, _lib.ReconDecodeArgs,
             _lib.RopeDecodeArgs, _lib.PrefillRopeArgs, _lib.MergeArgs, _lib.PrefillAttentionArgs, _lib.DownProjectArgs,
-            _lib.BeaconPagesArgs, _lib.RawPagesArgs, _lib.PagedLatentDecodeArgs, _lib.PageRows)
+            _lib.BeaconPagesArgs, _lib.RawPagesArgs, _lib.PagedLatentDecodeArgs, _lib.PageRows, _lib.LinearRowsArgs,
+            _lib.DecodeQKVArgs, _lib.EagerAttentionArgs)
 
 
 def test_struct_layouts_match_header_field_order():
