@@ -64,8 +64,13 @@ struct Seg {
     // Compact schedule: workgroup items enumerate only the non-empty splits of
     // each batch entry (needs seqlens); items past the last one exit at once.
     int compact;
-    // Two-segment rows (SEG2 instances): rows [0, n1) of a sequence at k / v,
-    // rows [n1, n) at k2 / v2, row i at index i - n1 there.
+};
+
+// Second row segment of the bulk segment (SEG2 instances): rows [0, n1) of a
+// sequence at Seg::k / v, rows [n1, n) here, row i at index i - n1.  Kept at
+// the end of SplitParams so that the other instances read their arguments at
+// the same offsets as without it.
+struct SegRows2 {
     const uint16_t* k2; int64_t k2_sb, k2_sn;
     const uint16_t* v2; int64_t v2_sb, v2_sn;
     int n1;
@@ -76,6 +81,7 @@ struct SplitParams {
     int nseg;
     int B, Lq, Hq;
     float scale_log2;
+    SegRows2 two;
 };
 
 constexpr int kWaves = 4;
@@ -338,7 +344,7 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
 // tile's two pages (pages of at least 16 rows).
 template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int Lq, int Hq,
-                                              float scale_log2, char* lds) {
+                                              float scale_log2, char* lds, const SegRows2* two = nullptr) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
     constexpr int RS = SplitLds<KS>::RS;
     const int lane = threadIdx.x & 63;
@@ -434,10 +440,11 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     auto fetch = [&](TileRegs<KS>& tr, int it) {
         const int r0 = it < ntile ? tile_row(it) : r_begin;
         if constexpr (SEG2) {
-            const uint16_t* k2 = sg.k2 + (int64_t)b * sg.k2_sb + (int64_t)h * sg.k_sh + k_off;
-            const uint16_t* v2 = sg.v2 + (int64_t)b * sg.v2_sb + (int64_t)h * sg.v_sh + v_off;
-            load_tile<KS>(tr, TwoRows{kbase, sg.k_sn, k2, sg.k2_sn, sg.n1}, TwoRows{vbase, sg.v_sn, v2, sg.v2_sn, sg.n1},
-                          r0, last_row, span_k, span_v, col, grp, lane);
+            const uint16_t* k2 = two->k2 + (int64_t)b * two->k2_sb + (int64_t)h * sg.k_sh + k_off;
+            const uint16_t* v2 = two->v2 + (int64_t)b * two->v2_sb + (int64_t)h * sg.v_sh + v_off;
+            load_tile<KS>(tr, TwoRows{kbase, sg.k_sn, k2, two->k2_sn, two->n1},
+                          TwoRows{vbase, sg.v_sn, v2, two->v2_sn, two->n1}, r0, last_row, span_k, span_v, col, grp,
+                          lane);
         } else {
             load_tile<KS>(tr, OneRows{kbase, sg.k_sn}, OneRows{vbase, sg.v_sn}, r0, last_row, span_k, span_v, col,
                           grp, lane);
@@ -692,7 +699,8 @@ split_kernel(SplitParams prm) {
         }
         w -= prm.seg[1].nwg;
     }
-    split_segment<KA, SplitDepth<KA>::value, PAGED, SEG2>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
+    split_segment<KA, SplitDepth<KA>::value, PAGED, SEG2>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds,
+                                                          &prm.two);
 }
 
 // ---------------------------------------------------------------------------
@@ -740,6 +748,14 @@ struct ReconTile {
 // Tiles in flight per wavefront: the rebuild's arithmetic is long enough that
 // two tiles do not cover the memory latency at two waves per SIMD.
 constexpr int kReconRing = 4;
+
+// Instances whose two tiles in flight (the software pipeline of recon_segment)
+// fit the register budget without spilling; the others run each tile's two
+// phases back to back.
+template <int KSR, int VL>
+struct ReconPipeline {
+    static constexpr bool value = (KSR <= 2 && VL == 1) || (KSR == 1 && VL == 2);
+};
 
 template <int KSR, int VL, int ROPE>
 __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq, int Hq, float scale_log2,
@@ -863,7 +879,9 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
     for (int i = 0; i < 2 * VL; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
     uint16_t* vbuf = reinterpret_cast<uint16_t*>(lds) + wave * 2 * 16 * RSV;
 
-    auto consume = [&](const ReconTile<KSR, VL>& t, const u32x4 (&cs)[4], int it) {
+    // Phase A of tile it: its V rows into LDS buffer it & 1, its K rebuilt,
+    // biased and rotated into the score MFMA's operand kop.
+    auto phase_a = [&](const ReconTile<KSR, VL>& t, const u32x4 (&cs)[4], int it, u32x2 (&kop)[8]) {
         const int r0 = r_begin + it * r_step;
         const int re = it < ntile ? r_end : r_begin;
         uint16_t* vb = vbuf + (it & 1) * 16 * RSV;
@@ -882,7 +900,6 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
 #pragma unroll
             for (int tt = 0; tt < 8; ++tt) kc[tt] = mfma16(as_v4s(wa[tt][ks].x, wa[tt][ks].y), bop, kc[tt]);
         }
-        u32x2 kop[8];
         if constexpr (ROPE == 2) {
             // x = acc + bias (the bias was the accumulator's start), y[d] =
             // x[d] c - x[d + 64] s, y[d + 64] = x[d + 64] c + x[d] s, in fp32
@@ -939,6 +956,11 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
                 kop[tt] = u32x2{w2[0], w2[1]};
             }
         }
+    };
+    // Phase B of tile it: scores, online softmax, P V from LDS buffer it & 1.
+    auto phase_b = [&](const u32x2 (&kop)[8], int it) {
+        const int r0 = r_begin + it * r_step;
+        uint16_t* vb = vbuf + (it & 1) * 16 * RSV;
         // scores S^T[key, col]
         v4f sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -990,13 +1012,35 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
     // Whole rounds of the ring, branch-free: tiles past the split's end are
     // loaded clamped and zeroed and every key in them is masked, so they leave
     // the running softmax unchanged.
-    for (int it = 0; it < ntile; it += kReconRing) {
+    u32x2 kop[2][8];
+    if constexpr (ReconPipeline<KSR, VL>::value) {
+        // Software pipeline: phase A of tile t + 1 (rebuild MFMAs, rotation) is
+        // issued beside phase B of tile t (score MFMAs, softmax, P V), so the
+        // one wavefront of a SIMD keeps the matrix cores and the VALU busy
+        // together (C2 layer: 36.0 -> 35.1 us).  The last round's phase A of
+        // the tile after it is unused.
+        phase_a(ring[0], pairs[0], 0, kop[0]);
+        fetch(ring[0], kReconRing);
+        if constexpr (ROPE) fetch_pairs(pairs[0], ring[2].pos);
+        for (int it = 0; it < ntile; it += kReconRing) {
 #pragma unroll
-        for (int u = 0; u < kReconRing; ++u) {
-            consume(ring[u], pairs[u & 1], it + u);
-            fetch(ring[u], it + u + kReconRing);
-            if constexpr (ROPE) fetch_pairs(pairs[u & 1], ring[(u + 2) % kReconRing].pos);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int u = 0; u < kReconRing; ++u) {
+                phase_a(ring[(u + 1) % kReconRing], pairs[(u + 1) & 1], it + u + 1, kop[(u + 1) & 1]);
+                fetch(ring[(u + 1) % kReconRing], it + u + 1 + kReconRing);
+                if constexpr (ROPE) fetch_pairs(pairs[(u + 1) & 1], ring[(u + 3) % kReconRing].pos);
+                phase_b(kop[u & 1], it + u);
+            }
+        }
+    } else {
+        for (int it = 0; it < ntile; it += kReconRing) {
+#pragma unroll
+            for (int u = 0; u < kReconRing; ++u) {
+                phase_a(ring[u], pairs[u & 1], it + u, kop[0]);
+                phase_b(kop[0], it + u);
+                fetch(ring[u], it + u + kReconRing);
+                if constexpr (ROPE) fetch_pairs(pairs[u & 1], ring[(u + 2) % kReconRing].pos);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 
@@ -2187,9 +2231,9 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
         l.wown = bd ? Rv / Hkv : Rv;
         l.nwg = p.lat.nwg;
         if (a->lat_k2) {
-            l.k2 = static_cast<const uint16_t*>(a->lat_k2); l.k2_sb = a->lk2_sb; l.k2_sn = a->lk2_sn;
-            l.v2 = static_cast<const uint16_t*>(a->lat_v2); l.v2_sb = a->lv2_sb; l.v2_sn = a->lv2_sn;
-            l.n1 = (int)a->lat_split;
+            prm.two.k2 = static_cast<const uint16_t*>(a->lat_k2); prm.two.k2_sb = a->lk2_sb; prm.two.k2_sn = a->lk2_sn;
+            prm.two.v2 = static_cast<const uint16_t*>(a->lat_v2); prm.two.v2_sb = a->lv2_sb; prm.two.v2_sn = a->lv2_sn;
+            prm.two.n1 = (int)a->lat_split;
         }
         if (pg) {
             l.k = pg->pages + pg->sink; l.v = pg->pages + pg->sink + Rk;

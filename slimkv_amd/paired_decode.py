@@ -1,8 +1,17 @@
-"""Drop-in for slimkv.llama3.paired_decode (Q2 as two Q1 rows over shared KV).
+"""Drop-in for slimkv.llama3.paired_decode (the two-query insertion step).
 
-original_splits restates slimkv/llama3/paired_decode.py:7-28 (host arithmetic).
-paired_attention (:30-43) calls the given forward with batch-stride-0 K/V and
-per-row lengths [N-1, N]; the HIP forward supports both directly.
+original_splits restates slimkv/llama3/paired_decode.py:7-28 (host arithmetic,
+kept for callers that size FA2 launches with it).
+
+paired_attention (:30-43): the reference runs the insertion step's causal Q2
+attention as two Q1 sequences over one K/V view (lengths [N-1, N]) with the
+split count FA2 would pick for the unpacked Q2 launch, so that the packed
+launch keeps the unpacked one's reduction order.  The HIP attention takes the
+two queries of a step natively (GQA rows packed with both query positions), so
+here the unpacked bottom-right causal Q2 launch itself is made: the raw query
+sees N - 1 keys, the Beacon query N, and the result has, by construction, the
+bits of the non-paired causal call (StaticDecode.attention's other branch,
+static_decode.py:86-90).  No FA2 split heuristic is involved.
 """
 import math
 from functools import lru_cache
@@ -32,9 +41,11 @@ def original_splits(width, key_length, query_heads, sm_count):
 
 
 def paired_attention(forward, q, k, v, scale, paired_lengths, sm_count):
+    """q [1, 2, H, W] (raw query, then the Beacon query), k/v [1, N_cap, Hk, W];
+    paired_lengths: device int32 [N - 1, N] as StaticDecode fills it
+    (static_decode.py:223-224) -- the Beacon query sees one key more.  Returns
+    (out [1, 2, H, W], lse [1, H, 2]).  `sm_count` is not needed."""
     if q.shape[:2] != (1, 2) or k.shape[0] != 1:
         raise ValueError('Paired decode requires B1 and exactly two queries.')
-    splits = original_splits(q.shape[-1], k.shape[1], q.shape[2], sm_count)
-    output, lse = forward(q.transpose(0, 1), k.expand(2, -1, -1, -1), v.expand(2, -1, -1, -1), scale, False,
-                          splits, True, paired_lengths)
-    return output.transpose(0, 1), lse.squeeze(-1).transpose(0, 1).unsqueeze(0)
+    output, lse = forward(q, k, v, scale, True, 0, True, paired_lengths[1:])
+    return output, lse

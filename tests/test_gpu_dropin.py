@@ -158,14 +158,22 @@ def test_extension_forward_and_paired_attention(device):
     from slimkv_amd.paired_decode import paired_attention
     gen = torch.Generator(device=device).manual_seed(2)
     q = torch.randn(1, 2, 32, 256, generator=gen, device=device).to(torch.bfloat16)
-    k = torch.randn(1, 77, 1, 256, generator=gen, device=device).to(torch.bfloat16)
-    v = torch.randn(1, 77, 1, 256, generator=gen, device=device).to(torch.bfloat16)
+    # a padded cache buffer: 77 valid rows of 100
+    k = torch.randn(1, 100, 1, 256, generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn(1, 100, 1, 256, generator=gen, device=device).to(torch.bfloat16)
     lengths = torch.tensor([76, 77], dtype=torch.int32, device=device)
     out, lse = paired_attention(ext.forward, q, k, v, 0.0625, lengths, 256)
+    # the non-paired causal launch (StaticDecode's other branch): the same bits
+    uo, ul = ext.forward(q, k, v, 0.0625, True, 0, True, lengths[1:])
     torch.cuda.synchronize()
-    eo, el = oa.eager_forward(to_np(q), to_np(k), to_np(v), 0.0625, True)
+    assert torch.equal(out, uo) and torch.equal(lse, ul)
+    eo, el = oa.eager_forward(to_np(q), to_np(k[:, :77]), to_np(v[:, :77]), 0.0625, True)
     assert_close(to_np(out), eo)
     np.testing.assert_allclose(to_np(lse), el, atol=2e-3)
+    # the raw query's row excludes the Beacon key: it equals a one-query launch over 76 keys
+    ro, rl = ext.forward(q[:, :1], k[:, :76], v[:, :76], 0.0625, False)
+    torch.cuda.synchronize()
+    assert_close(to_np(out[:, :1]), to_np(ro))
 
 
 def test_fused_prefill_rope_through_metadata(device):
