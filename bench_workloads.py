@@ -444,19 +444,27 @@ def paged(args):
         decode()
 
     def paged_call(stages=_STAGE_ALL, workspace=None):
-        kernels.paged_latent_decode(q, raw_k.transpose(1, 2), raw_v.transpose(1, 2), pool, tables, lat_len, max_nb,
-                                    layout, up_k, up_v, scale, rows_total=sum(nb), block_diagonal=True,
-                                    raw_lengths=raw_len, out=out, status=status, stages=stages, workspace=workspace)
+        # beacon rows and raw rows (sinks, tail, current token) both read by
+        # the decode through their block tables: no gather step
+        kernels.paged_latent_decode(q, None, None, pool, tables, lat_len, max_nb, layout, up_k, up_v, scale,
+                                    rows_total=sum(nb), block_diagonal=True, raw_lengths=raw_len, out=out,
+                                    status=status, stages=stages, workspace=workspace, raw_pages=raw.pages,
+                                    raw_tables=raw_tables, raw_keys=max_raw)
 
     def direct_step():
-        # raw rows (sinks + tail) still come out of their pages into a small dense
-        # buffer; the beacon rows are read by the decode straight from the pages
+        paged_call()
+
+    def raw_gather_step():
+        # the raw rows gathered into a small dense buffer first
         kernels.raw_pages(raw.pages, raw_tables, raw_k, raw_v, start=0, count=max_raw, to_pages=False,
                           lengths=raw_len, status=status)
-        paged_call()
+        kernels.paged_latent_decode(q, raw_k.transpose(1, 2), raw_v.transpose(1, 2), pool, tables, lat_len, max_nb,
+                                    layout, up_k, up_v, scale, rows_total=sum(nb), block_diagonal=True,
+                                    raw_lengths=raw_len, out=out, status=status)
 
     seconds = _time_steps(torch, direct_step, args.steps, args.warmup)
     replays, clocks = _replays(torch, direct_step)
+    raw_gather_s = _time_steps(torch, raw_gather_step, args.steps, args.warmup)
     restore_s = _time_steps(torch, restore_step, args.steps, args.warmup)
     decode_s = _time_steps(torch, decode, args.steps, args.warmup)
     # the split kernel alone (attend stage): the pool (2.4 GB) is far larger
@@ -472,15 +480,17 @@ def paged(args):
     gbps = algo / seconds / 1e9
     achieved = split_bytes / attend_s / 1e9
     result = _result('paged latent decode GB/s, 64 seqs ctx U[1K,128K] t8', gbps, 'GB/s', args, seconds, 'bf16',
-                     {'workload': 'paged decode: beacon rows read from the pages by the fused latent decode, '
-                                  'raw rows gathered, t8, rank 32',
+                     {'workload': 'paged decode: beacon and raw rows read from their pages by the fused latent '
+                                  'decode, t8, rank 32',
                       'sequences': NSEQ, 'page_layout': [16, RATIO, R, R, HKV * D], 'pool_pages': POOL,
                       'beacons_total': sum(nb)},
                      hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), bytes_per_step=algo,
                      roofline={'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                                'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
-                               'kernel': 'split_kernel<KA,8,paged> (attend stage)', 'avg_us': round(attend_s * 1e6, 2),
+                               'kernel': 'split_kernel<KA,8,paged,0,raw pages> (attend stage)', 'avg_us': round(attend_s * 1e6, 2),
                                'bytes_per_launch': split_bytes},
+                     raw_gather_path_gbps=round(algo / raw_gather_s / 1e9, 1),
+                     raw_gather_path_ms=round(raw_gather_s * 1e3, 4),
                      restore_path_gbps=round(algo / restore_s / 1e9, 1), restore_path_ms=round(restore_s * 1e3, 4),
                      dense_decode_only_gbps=round(algo / decode_s / 1e9, 1), replays=replays, clocks=clocks)
     if not args.no_cpu:

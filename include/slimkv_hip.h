@@ -194,6 +194,17 @@ int slimkv_latent_decode_noalloc(const slimkv_latent_decode_args* a, void* strea
  * it (sizes the key splits; 0 = unknown), never needed for correctness.
  * With the same base.lat_splits the result is bit-identical to gathering the
  * rows and calling slimkv_latent_decode.
+ * raw_pages (optional): the raw rows (sinks, tail, current token) read through
+ * raw pages as well, replacing RawPages.read (paged_cache.py:111-127) into
+ * base.raw_k / raw_v (then ignored, NULL allowed): row r of sequence b is
+ * token r % raw_block_size (a power of two, at least 16) of block
+ * raw_table[b * raw_t_sb + r / raw_block_size] (raw_t_cols entries per row,
+ * at least ceil(base.raw_keys / raw_block_size)); K at raw_pages +
+ * block * raw_block_stride + token * raw_token_stride + head *
+ * raw_head_stride, V raw_kind_stride further (RawPages' [blocks, block, 2,
+ * Hkv, D] pages).  Block ids follow the same rules; base.raw_lengths holds
+ * the raw rows per sequence.  With the same split counts the result is
+ * bit-identical to reading the raw rows into dense tensors first.
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_paged_latent_decode_args {
     slimkv_latent_decode_args base;
@@ -202,6 +213,9 @@ typedef struct slimkv_paged_latent_decode_args {
     int64_t slots, sink_elements;
     int64_t rows_total;
     int32_t* status;   /* optional: SLIMKV_STATUS_BAD_PAGE on an index error */
+    const void* raw_pages; int64_t raw_num_blocks, raw_block_size;
+    int64_t raw_block_stride, raw_token_stride, raw_kind_stride, raw_head_stride;
+    const int64_t* raw_table; int64_t raw_t_sb, raw_t_cols;
 } slimkv_paged_latent_decode_args;
 
 size_t slimkv_paged_latent_decode_workspace(const slimkv_paged_latent_decode_args* a);

@@ -99,6 +99,9 @@ PagedLatentDecodeArgs = _struct('slimkv_paged_latent_decode_args', [
     ('table', c_ptr), *_i64s('t_sb', 't_cols'),
     *_i64s('slots', 'sink_elements', 'rows_total'),
     ('status', c_ptr),
+    ('raw_pages', c_ptr), *_i64s('raw_num_blocks', 'raw_block_size'),
+    *_i64s('raw_block_stride', 'raw_token_stride', 'raw_kind_stride', 'raw_head_stride'),
+    ('raw_table', c_ptr), *_i64s('raw_t_sb', 'raw_t_cols'),
 ])
 
 RopeDecodeArgs = _struct('slimkv_rope_decode_args', [

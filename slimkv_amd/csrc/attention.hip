@@ -76,12 +76,25 @@ struct SegRows2 {
     int n1;
 };
 
+// Raw rows read through raw pages (RAWPG instances, the raw segment of the
+// paged decode): row r of sequence b is token r % block of block
+// table[b][r / block] in pages [blocks, block, 2, Hkv, D] (Seg::k / v point
+// at the pool's K and V halves, Seg::k_sn is the token stride).  Block ids
+// follow torch's indexing; an entry outside the pool that a row needs is
+// reported in Seg::status and read as block 0.
+struct RawPagesArg {
+    const int64_t* table; int64_t t_sb;
+    int64_t blk_stride, num_blocks;
+    int block_shift;                                 // block = 1 << block_shift tokens
+};
+
 struct SplitParams {
     Seg seg[2];
     int nseg;
     int B, Lq, Hq;
     float scale_log2;
     SegRows2 two;
+    RawPagesArg rawp;
 };
 
 constexpr int kWaves = 4;
@@ -197,6 +210,20 @@ struct TwoRows {
     int n1;
     __device__ __forceinline__ const uint16_t* row(int r) const {
         return r < n1 ? base + (int64_t)r * sn : base2 + (int64_t)(r - n1) * sn2;
+    }
+};
+
+struct RawPageRows {
+    const uint16_t* base;                            // the pool's K or V half, head offset included
+    const int64_t* tab;                              // the sequence's block table row
+    int64_t blk_stride, tok_stride, num_blocks;
+    int shift, last_valid;
+    bool* bad;
+    __device__ __forceinline__ const uint16_t* row(int r) const {
+        const int rc = min(r, last_valid);
+        const int64_t blk = table_page(tab[rc >> shift], num_blocks);
+        *bad |= blk < 0;
+        return base + (blk < 0 ? 0 : blk) * blk_stride + (int64_t)(rc & ((1 << shift) - 1)) * tok_stride;
     }
 };
 
@@ -342,9 +369,10 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
 // never exchange data, and write their own partials.
 // PAGED: 0 dense rows, 1 rows through per-lane page ids, 2 rows through the
 // tile's two pages (pages of at least 16 rows).
-template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0>
+template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0, int RAWPG = 0>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int Lq, int Hq,
-                                              float scale_log2, char* lds, const SegRows2* two = nullptr) {
+                                              float scale_log2, char* lds, const SegRows2* two = nullptr,
+                                              const RawPagesArg* rawp = nullptr) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
     constexpr int RS = SplitLds<KS>::RS;
     const int lane = threadIdx.x & 63;
@@ -437,9 +465,16 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     const uint16_t* kbase = sg.k + (int64_t)b * sg.k_sb + (int64_t)h * sg.k_sh + k_off;
     const uint16_t* vbase = sg.v + (int64_t)b * sg.v_sb + (int64_t)h * sg.v_sh + v_off;
 
+    bool bad = false;
     auto fetch = [&](TileRegs<KS>& tr, int it) {
         const int r0 = it < ntile ? tile_row(it) : r_begin;
-        if constexpr (SEG2) {
+        if constexpr (RAWPG) {
+            const int64_t* tb = rawp->table + (int64_t)b * rawp->t_sb;
+            const int lv = Nb > 0 ? Nb - 1 : 0;
+            load_tile<KS>(tr, RawPageRows{kbase, tb, rawp->blk_stride, sg.k_sn, rawp->num_blocks, rawp->block_shift, lv, &bad},
+                          RawPageRows{vbase, tb, rawp->blk_stride, sg.v_sn, rawp->num_blocks, rawp->block_shift, lv, &bad},
+                          r0, last_row, span_k, span_v, col, grp, lane);
+        } else if constexpr (SEG2) {
             const uint16_t* k2 = two->k2 + (int64_t)b * two->k2_sb + (int64_t)h * sg.k_sh + k_off;
             const uint16_t* v2 = two->v2 + (int64_t)b * two->v2_sb + (int64_t)h * sg.v_sh + v_off;
             load_tile<KS>(tr, TwoRows{kbase, sg.k_sn, k2, two->k2_sn, two->n1},
@@ -455,7 +490,6 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     // `bad` (reported once the split is done) and is read as page 0.
     const int64_t* tab = PAGED ? sg.table + (int64_t)b * sg.t_sb : nullptr;
     const int last_valid = Nb > 0 ? Nb - 1 : 0;
-    bool bad = false;
     auto page_of = [&](int row, bool used) -> int32_t {
         const int r = min(row, last_valid);
         const int64_t p = table_page(tab[sg.slots_shift >= 0 ? (r >> sg.slots_shift) : r / sg.slots], sg.num_pages);
@@ -642,7 +676,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
         }
     }
 
-    if constexpr (PAGED) {
+    if constexpr (PAGED || RAWPG) {
         if (bad) report_bad_page(sg.status);
     }
     // Column sums: every lane group holds a quarter of the keys.
@@ -685,7 +719,7 @@ struct SplitDepth {
     static constexpr int value = 2;
 };
 
-template <int KA, int KB, int PAGED = 0, int SEG2 = 0>
+template <int KA, int KB, int PAGED = 0, int SEG2 = 0, int RAWPG = 0>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SplitWaves<KA>::value)))
 split_kernel(SplitParams prm) {
     constexpr int LA = SplitLds<KA>::bytes;
@@ -694,7 +728,8 @@ split_kernel(SplitParams prm) {
     int w = blockIdx.x;
     if constexpr (KB > 0) {
         if (w < prm.seg[1].nwg) {
-            split_segment<KB, 1>(prm.seg[1], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
+            split_segment<KB, 1, 0, 0, RAWPG>(prm.seg[1], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds, nullptr,
+                                              &prm.rawp);
             return;
         }
         w -= prm.seg[1].nwg;
@@ -1675,21 +1710,25 @@ thread_local std::string g_error;
 
 hipError_t dispatch_split(int ka, int kb, const struct SplitParams& prm, int grid, hipStream_t st);
 hipError_t dispatch_split_seg2(int ka, const struct SplitParams& prm, int grid, hipStream_t st);
-template <int MODE>
+template <int MODE, int RAWPG>
 hipError_t launch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
     switch (ka) {
-        case 2: hipLaunchKernelGGL((split_kernel<2, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
-        case 4: hipLaunchKernelGGL((split_kernel<4, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
-        case 6: hipLaunchKernelGGL((split_kernel<6, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
-        case 8: hipLaunchKernelGGL((split_kernel<8, 8, MODE>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 2: hipLaunchKernelGGL((split_kernel<2, 8, MODE, 0, RAWPG>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 4: hipLaunchKernelGGL((split_kernel<4, 8, MODE, 0, RAWPG>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 6: hipLaunchKernelGGL((split_kernel<6, 8, MODE, 0, RAWPG>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 8: hipLaunchKernelGGL((split_kernel<8, 8, MODE, 0, RAWPG>), dim3(grid), dim3(kThreads), 0, st, prm); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-// Pages of at least 16 rows take the two-pages-per-tile addressing.
+// Pages of at least 16 rows take the two-pages-per-tile addressing; raw rows
+// come from dense tensors or through raw pages.
 hipError_t dispatch_split_paged(int ka, const SplitParams& prm, int grid, hipStream_t st) {
-    return prm.seg[0].slots >= 16 ? launch_split_paged<2>(ka, prm, grid, st) : launch_split_paged<1>(ka, prm, grid, st);
+    const bool raw_pages = prm.rawp.table != nullptr;
+    if (prm.seg[0].slots >= 16)
+        return raw_pages ? launch_split_paged<2, 1>(ka, prm, grid, st) : launch_split_paged<2, 0>(ka, prm, grid, st);
+    return raw_pages ? launch_split_paged<1, 1>(ka, prm, grid, st) : launch_split_paged<1, 0>(ka, prm, grid, st);
 }
 
 hipError_t launch_split_any(int ka, int kb, const SplitParams& prm, int grid, hipStream_t st, bool paged = false,
@@ -1962,6 +2001,10 @@ struct PagedRows {
     const int64_t* table; int64_t t_sb, t_cols;
     int64_t slots, sink, rows_total;
     int32_t* status;
+    // raw rows through raw pages (raw_pages null: dense base.raw_k / raw_v)
+    const uint16_t* raw_pages; int64_t raw_blocks, raw_block;
+    int64_t raw_blk_stride, raw_tok_stride, raw_kind_stride, raw_head_stride;
+    const int64_t* raw_table; int64_t raw_t_sb, raw_t_cols;
 };
 
 int check_paged(const slimkv_latent_decode_args* a, const PagedRows* pg) {
@@ -1977,11 +2020,26 @@ int check_paged(const slimkv_latent_decode_args* a, const PagedRows* pg) {
     if (a->lat_keys > 0 && (a->lat_keys + pg->slots - 1) / pg->slots > pg->t_cols)
         return fail(SLIMKV_EINVAL, "block table narrower than the beacon count");
     if (pg->slots > (1 << 20) || pg->rows_total < 0) return fail(SLIMKV_EINVAL, "invalid page geometry");
+    if (pg->raw_pages) {
+        const int64_t blk = pg->raw_block;
+        if (!pg->raw_table || !a->raw_lengths) return fail(SLIMKV_EINVAL, "raw pages need a raw table and raw lengths");
+        if (a->lat_keys <= 0) return fail(SLIMKV_EUNSUP, "raw pages are read beside beacon rows (lat_keys > 0)");
+        if (blk < 16 || blk > (1 << 20) || (blk & (blk - 1)) || pg->raw_blocks <= 0 || pg->raw_blocks >= ((int64_t)1 << 31) ||
+            pg->raw_t_cols <= 0 || pg->raw_t_sb < pg->raw_t_cols)
+            return fail(SLIMKV_EINVAL, "invalid raw page geometry (block size a power of two >= 16)");
+        if ((a->raw_keys + blk - 1) / blk > pg->raw_t_cols)
+            return fail(SLIMKV_EINVAL, "raw block table narrower than the raw row count");
+        if (!aligned8(pg->raw_blk_stride) || !aligned8(pg->raw_tok_stride) || !aligned8(pg->raw_kind_stride) ||
+            !aligned8(pg->raw_head_stride) || !ptr_aligned16(pg->raw_pages))
+            return fail(SLIMKV_EINVAL, "raw page strides must be multiples of 8 elements, pages 16-byte aligned");
+        if (pg->raw_blocks > ((int64_t)1 << 40) / std::max<int64_t>(pg->raw_blk_stride, 1))
+            return fail(SLIMKV_EINVAL, "raw page pool too large");
+    }
     return SLIMKV_OK;
 }
 
 int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRows* pg = nullptr) {
-    if (!a || !a->q || !a->raw_k || !a->raw_v || !a->out || !a->up_k || !a->up_v)
+    if (!a || !a->q || !a->out || !a->up_k || !a->up_v || ((!a->raw_k || !a->raw_v) && !(pg && pg->raw_pages)))
         return fail(SLIMKV_EINVAL, "null tensor pointer");
     if (pg) {
         const int rc = check_paged(a, pg);
@@ -2212,6 +2270,15 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     r.part_acc = reinterpret_cast<float*>(ws + p.racc_off);
     r.wown = D;
     r.nwg = p.raw.nwg;
+    if (pg && pg->raw_pages && has_lat) {
+        r.k = pg->raw_pages; r.k_sb = 0; r.k_sn = pg->raw_tok_stride; r.k_sh = pg->raw_head_stride;
+        r.v = pg->raw_pages + pg->raw_kind_stride; r.v_sb = 0; r.v_sn = pg->raw_tok_stride;
+        r.v_sh = pg->raw_head_stride;
+        r.status = pg->status;
+        prm.rawp.table = pg->raw_table; prm.rawp.t_sb = pg->raw_t_sb;
+        prm.rawp.blk_stride = pg->raw_blk_stride; prm.rawp.num_blocks = pg->raw_blocks;
+        prm.rawp.block_shift = __builtin_ctzll((unsigned long long)pg->raw_block);
+    }
     int ka = 8, kb = 0;
     if (has_lat) {
         Seg& l = prm.seg[0];
@@ -2279,7 +2346,10 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
 
 PagedRows paged_rows(const slimkv_paged_latent_decode_args* a) {
     return PagedRows{static_cast<const uint16_t*>(a->pages), a->num_pages, a->page_stride, a->table, a->t_sb,
-                     a->t_cols, a->slots, a->sink_elements, a->rows_total, a->status};
+                     a->t_cols, a->slots, a->sink_elements, a->rows_total, a->status,
+                     static_cast<const uint16_t*>(a->raw_pages), a->raw_num_blocks, a->raw_block_size,
+                     a->raw_block_stride, a->raw_token_stride, a->raw_kind_stride, a->raw_head_stride, a->raw_table,
+                     a->raw_t_sb, a->raw_t_cols};
 }
 
 }  // namespace

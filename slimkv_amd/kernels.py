@@ -212,11 +212,13 @@ def _latent_rows(lat_k, lat_v, Rk, Rv):
 
 def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up_v_bias, block_diagonal,
                  lat_causal, q_positions, cos, sin, raw_lengths, lat_lengths, raw_splits, lat_splits, out, lse,
-                 prepared_bases=True, lat_rows=None, lat_k2=None, lat_v2=None):
+                 prepared_bases=True, lat_rows=None, lat_k2=None, lat_v2=None, raw_shape=None):
+    """raw_shape = (raw rows, KV heads) when the raw rows are read through raw
+    pages (raw_k / raw_v None)."""
     _need_device(q, raw_k, raw_v, lat_k, lat_v, lat_k2, lat_v2, up_k, up_v)
     _need_bf16(q, raw_k, raw_v, lat_k, lat_v, lat_k2, lat_v2, up_k, up_v, up_k_bias, up_v_bias)
     B, Lq, Hq, D = q.shape
-    Nr, Hkv = raw_k.shape[1], raw_k.shape[2]
+    Nr, Hkv = raw_shape if raw_k is None else (raw_k.shape[1], raw_k.shape[2])
     Rk, Rv = up_k.shape[1], up_v.shape[1]
     # a second latent segment joins the first one's rows; an empty segment drops out
     if lat_k2 is not None and lat_k2.shape[1] == 0:
@@ -225,7 +227,9 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
         lat_k, lat_v, lat_k2, lat_v2 = lat_k2, lat_v2, None, None
     Nl = (0 if lat_rows is None else int(lat_rows)) if lat_k is None else lat_k.shape[1]
     split = 0
-    q, raw_k, raw_v = (_last_contiguous(x) for x in (q, raw_k, raw_v))
+    q = _last_contiguous(q)
+    if raw_k is not None:
+        raw_k, raw_v = _last_contiguous(raw_k), _last_contiguous(raw_v)
     if lat_k is not None:
         lat_k, lat_v = _latent_rows(lat_k, lat_v, Rk, Rv)
     if lat_k2 is not None:
@@ -259,7 +263,8 @@ def _latent_args(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, up_k_bias, up
         _ptr(q), *q.stride()[:3],
         _ptr(q_positions), 0 if q_positions is None else q_positions.stride(0),
         _ptr(cos), _ptr(sin), 0 if cos is None else cos.shape[0],
-        _ptr(raw_k), *raw_k.stride()[:3], _ptr(raw_v), *raw_v.stride()[:3],
+        _ptr(raw_k), *(raw_k.stride()[:3] if raw_k is not None else (0, 0, 0)),
+        _ptr(raw_v), *(raw_v.stride()[:3] if raw_v is not None else (0, 0, 0)),
         _ptr(raw_lengths), Nr,
         _ptr(lat_k), *(lat_k.stride()[:2] if lat_k is not None else (0, 0)),
         _ptr(lat_v), *(lat_v.stride()[:2] if lat_v is not None else (0, 0)),
@@ -334,7 +339,8 @@ def _stage_workspace(workspace, nbytes, stages, device):
 def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, layout, up_k, up_v, scale, *,
                         rows_total=0, up_k_bias=None, up_v_bias=None, block_diagonal=False, lat_causal=False,
                         q_positions=None, cos=None, sin=None, raw_lengths=None, raw_splits=0, lat_splits=0,
-                        out=None, lse=None, workspace=None, stages=_lib.STAGE_ALL, status=None):
+                        out=None, lse=None, workspace=None, stages=_lib.STAGE_ALL, status=None,
+                        raw_pages=None, raw_tables=None, raw_keys=None):
     """latent_decode with the beacon rows read straight out of beacon pages.
 
     pages [num_pages, layout.page_elements] bf16 in BeaconPageLayout format;
@@ -346,8 +352,14 @@ def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, la
     beacon needs raises IndexError after the call (one host synchronisation)
     unless the caller passes its own device int32 `status` word (graph
     capture, serving loops) and checks it with check_status.
+
+    raw_pages [blocks, block, 2, Hkv, D] (RawPages' pages) with raw_tables
+    [B, cols] int64 and raw_lengths [B] int32: the raw rows are read through
+    the raw block table as well (raw_k / raw_v None; raw_keys = the largest
+    raw row count, default cols * block).  Same result as RawPages.read_batch
+    into dense rows followed by this call.
     """
-    _need_device(pages, table, lat_lengths)
+    _need_device(pages, table, lat_lengths, raw_pages, raw_tables)
     _need_bf16(pages)
     if up_k.shape[1] != layout.key_rank or up_v.shape[1] != layout.value_rank:
         raise ValueError('page layout ranks differ from the up-projection ranks')
@@ -357,12 +369,30 @@ def paged_latent_decode(q, raw_k, raw_v, pages, table, lat_lengths, lat_keys, la
         raise ValueError('table must be int64 [B, pages], lat_lengths int32 [B]')
     table = table if table.stride(1) == 1 else table.contiguous()
     lat_lengths = lat_lengths.contiguous()
+    raw_fields = (None, 0, 0, 0, 0, 0, 0, None, 0, 0)
+    raw_shape = None
+    if raw_pages is not None:
+        _need_bf16(raw_pages)
+        if raw_pages.dim() != 5 or raw_pages.shape[2] != 2 or raw_pages.stride(4) != 1:
+            raise ValueError('raw pages must be [blocks, block, 2, Hkv, D] with contiguous rows')
+        if raw_tables is None or raw_tables.dtype != torch.int64 or raw_tables.dim() != 2 or raw_lengths is None:
+            raise ValueError('raw pages need int64 raw_tables [B, cols] and raw_lengths')
+        raw_tables = raw_tables if raw_tables.stride(1) == 1 else raw_tables.contiguous()
+        block = raw_pages.shape[1]
+        raw_keys = raw_tables.shape[1] * block if raw_keys is None else int(raw_keys)
+        raw_shape = (raw_keys, raw_pages.shape[3])
+        st = raw_pages.stride()
+        raw_fields = (_ptr(raw_pages), raw_pages.shape[0], block, st[0], st[1], st[2], st[3], _ptr(raw_tables),
+                      raw_tables.stride(0), raw_tables.shape[1])
+        raw_k = raw_v = None
     base, out, lse, keep = _latent_args(q, raw_k, raw_v, None, None, up_k, up_v, scale, up_k_bias, up_v_bias,
                                         block_diagonal, lat_causal, q_positions, cos, sin, raw_lengths,
-                                        lat_lengths, raw_splits, lat_splits, out, lse, True, lat_rows=lat_keys)
+                                        lat_lengths, raw_splits, lat_splits, out, lse, True, lat_rows=lat_keys,
+                                        raw_shape=raw_shape)
     status, owned = _status_word(status, pages.device)
     a = _lib.PagedLatentDecodeArgs(base, _ptr(pages), pages.shape[0], pages.stride(0), _ptr(table), table.stride(0),
-                                   table.shape[1], layout.slots, layout.sink_elements, int(rows_total), _ptr(status))
+                                   table.shape[1], layout.slots, layout.sink_elements, int(rows_total), _ptr(status),
+                                   *raw_fields)
     nbytes = lib().slimkv_paged_latent_decode_workspace(ctypes.byref(a))
     if nbytes == 0:
         check(-1)

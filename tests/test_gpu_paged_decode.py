@@ -200,3 +200,67 @@ def test_negative_entries_wrap_and_index_errors_are_reported(device, layout_args
     status.zero_()
     run(neg, status=status)
     assert int(status.item()) == 0
+
+
+def _raw_pages_of(c, device, block, seed, garbage=True):
+    """The case's dense raw rows written into RawPages-format pages [blocks,
+    block, 2, Hkv, D] at a seeded permutation, with a block table (entries
+    past a sequence's blocks hold ids outside the pool)."""
+    gen = torch.Generator().manual_seed(seed)
+    B, max_raw = c['raw_k'].shape[:2]
+    per = (max_raw + block - 1) // block
+    nblocks = B * per + 3
+    pool = torch.randn(nblocks, block, 2, HKV, D, generator=torch.Generator(device=device).manual_seed(seed),
+                       device=device).to(torch.bfloat16)
+    perm = torch.randperm(nblocks, generator=gen)
+    table = torch.randint(-(1 << 40), 1 << 40, (B, per + 1), generator=gen) if garbage \
+        else torch.zeros(B, per + 1, dtype=torch.long)
+    lengths = c['raw_lengths'].tolist()
+    for b in range(B):
+        used = (lengths[b] + block - 1) // block
+        table[b, :used] = perm[b * per:b * per + used]
+        for t in range(lengths[b]):
+            blk, off = int(table[b, t // block]), t % block
+            pool[blk, off, 0] = c['raw_k'][b, t]
+            pool[blk, off, 1] = c['raw_v'][b, t]
+    return pool, table.to(device)
+
+
+@pytest.mark.parametrize('layout_args,lengths,block', [
+    ((16, 8, 256, 256, 1024), [1000, 3, 37, 1, 777, 16, 15, 1024], 16),
+    ((480, 8, 256, 256, 1024), [513, 31, 32, 33, 1, 2000], 16),
+    ((16, 4, 256, 256, 1024), [333, 1024, 5, 64], 32),
+])
+def test_raw_rows_through_raw_pages_equal_dense_raw_rows(device, layout_args, lengths, block):
+    """The raw rows read through raw pages and the block table (no dense
+    gather) give the bits of the decode over the same rows held densely, with
+    the same split plan; raw row counts 1 to 45 cover partial blocks."""
+    from slimkv_amd import kernels
+    raw_lengths = [1 + (11 * i) % 45 for i in range(len(lengths))]
+    c = _case(device, layout_args, lengths, raw_lengths, seed=len(lengths) + block)
+    pool, table = _raw_pages_of(c, device, block, seed=block)
+    scale = D ** -0.5
+    common = dict(block_diagonal=True, raw_lengths=c['raw_lengths'], lat_splits=5, raw_splits=2)
+    want, want_lse = kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'],
+                                                 c['lengths'], c['lat_keys'], c['layout'], c['up_k'], c['up_v'],
+                                                 scale, **common)
+    got, got_lse = kernels.paged_latent_decode(c['q'], None, None, c['pages'], c['tables'], c['lengths'],
+                                               c['lat_keys'], c['layout'], c['up_k'], c['up_v'], scale,
+                                               raw_pages=pool, raw_tables=table, raw_keys=c['raw_k'].shape[1],
+                                               **common)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
+
+
+def test_raw_page_index_errors_are_reported(device):
+    """A raw block-table entry outside the pool that a raw row needs raises
+    IndexError after the call, as the reference's indexing does; the kernel
+    reads block 0 for it and every access stays in bounds."""
+    from slimkv_amd import kernels
+    c = _case(device, (16, 8, 256, 256, 1024), [64, 32], [20, 9], seed=3)
+    pool, table = _raw_pages_of(c, device, 16, seed=4, garbage=False)
+    table[1, 0] = pool.shape[0] + 5
+    with pytest.raises(IndexError):
+        kernels.paged_latent_decode(c['q'], None, None, c['pages'], c['tables'], c['lengths'], c['lat_keys'],
+                                    c['layout'], c['up_k'], c['up_v'], D ** -0.5, block_diagonal=True,
+                                    raw_lengths=c['raw_lengths'], raw_pages=pool, raw_tables=table)
