@@ -46,7 +46,7 @@ RANKS = (16, 32, 48)
 # FETCH_SIZE = half the bytes read; its 256 MiB fills WRITE_SIZE = the bytes
 # written): (2 x fetch + write) x 1024.
 SPLIT_TRAFFIC_BYTES = {32: (2 * 70_463.75 + 2_884.0) * 1024, 16: (2 * 37_631.25 + 2_884.0) * 1024,
-                       48: (2 * 103_190.0 + 3_143.90625) * 1024}
+                       48: (2 * 107_059.75 + 3_140.25) * 1024}
 SPLIT_TRAFFIC_BYTES = {r: int(v) for r, v in SPLIT_TRAFFIC_BYTES.items()}
 TRAFFIC_SOURCE = ('rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, split_kernel, scaled by the ceiling probe\'s '
                   '4 GiB stream reads and 256 MiB fills')
