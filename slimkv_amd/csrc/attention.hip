@@ -132,11 +132,11 @@ __device__ __forceinline__ u32x4 zero_unless(bool ok, u32x4 v) {
 
 // Key/value rows are read once per decode step.  Dense tiles of KS k-steps
 // read them with non-temporal loads (gfx950 `nt`) where that measured faster:
-// the rank-32 latent tiles (30.6 against 32.5 us a layer, B16 32K) and the
-// rank-48 ones (38.1 against 40.9 us).  The 128-column tiles (rank 16 per
-// head, raw rows) ran slower with them (rank 16: 18.0 against 17.4 us; the
-// paged decode's raw segment 148.2 against 146.7 us a step), and the paged
-// row policies keep plain loads.
+// the 64-column latent tiles (rank-32 layer 30.6 against 32.5 us, B16 32K)
+// and the 96-column ones (rank 48: 38.1 against 40.9 us).  The 128-column
+// tiles -- the raw rows, head_dim 128 -- ran slower with them (rank-16 layer
+// 18.0 against 17.4 us; the paged decode's raw segment 148.2 against 146.7 us
+// a step), and the paged row policies keep plain loads.
 template <int KS>
 struct StreamLoads {
     static constexpr bool value = KS == 4 || KS == 6;
