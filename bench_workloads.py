@@ -28,6 +28,16 @@ HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 _STAGE_PROLOGUE, _STAGE_ATTEND, _STAGE_ALL = 1, 2, 7      # SLIMKV_STAGE_* of include/slimkv_hip.h
 
+# HBM bytes a launch of each workload's dominant kernel moves: two rocprofv3
+# --pmc passes (FETCH_SIZE, then WRITE_SIZE, KiB a dispatch) over
+# `bench.py --workload recon|paged --steps 1 --warmup 1 --no-cpu`, scaled as the
+# latent decode's (FETCH_SIZE counts half the bytes read, WRITE_SIZE the bytes
+# written, from the ceiling probe's transfers of known size).
+RECON_TRAFFIC_BYTES = int((2 * 38_239.3 + 1_644.4) * 1024)      # recon_split_kernel<2, 1, 2>
+PAGED_TRAFFIC_BYTES = int((2 * 321_411.8 + 10_669.7) * 1024)    # split_kernel<4, 8, 1, 0, 1>
+TRAFFIC_SOURCE = ('rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this workload\'s kernel, scaled by the ceiling '
+                  'probe\'s stream reads and fills')
+
 
 def _events(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -325,7 +335,8 @@ def recon(args):
                      hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), us_per_layer=round(seconds / LAYERS * 1e6, 2),
                      bytes_per_layer=per_layer,
                      roofline={'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
-                               'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
+                               'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': RECON_TRAFFIC_BYTES,
+                               'traffic_source': TRAFFIC_SOURCE,
                                'kernel': 'recon_split_kernel (attend stage)', 'avg_us': round(attend_s * 1e6, 2),
                                'bytes_per_launch': split_bytes,
                                'mfma': {'achieved': round(mfma_tflops, 2), 'peak': MFMA_BF16_PEAK_TFLOPS,
@@ -486,7 +497,8 @@ def paged(args):
                       'beacons_total': sum(nb)},
                      hbm_frac=round(gbps / HBM_PEAK_GBPS, 4), bytes_per_step=algo,
                      roofline={'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
-                               'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': None,
+                               'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': PAGED_TRAFFIC_BYTES,
+                               'traffic_source': TRAFFIC_SOURCE,
                                'kernel': 'split_kernel<KA,8,paged,0,raw pages> (attend stage)', 'avg_us': round(attend_s * 1e6, 2),
                                'bytes_per_launch': split_bytes},
                      raw_gather_path_gbps=round(algo / raw_gather_s / 1e9, 1),

@@ -710,7 +710,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
 // Segment 0 (KA, pipelined) is the bulk segment.  The optional segment 1 (KB,
 // single register set) is short work -- the raw rows of the fused decode in
 // 32-key splits -- and is placed first in the grid so it drains while the bulk
-// workgroups stream.
+// workgroups stream (last in the grid for paged rows, see split_kernel).
 template <int KA>
 struct SplitWaves {
     static constexpr int value = KA <= 4 ? 4 : (KA <= 6 ? 3 : (KA <= 12 ? 2 : 1));
@@ -729,7 +729,18 @@ split_kernel(SplitParams prm) {
     constexpr int LB = KB > 0 ? SplitLds<(KB > 0 ? KB : 2)>::bytes : 0;
     __shared__ __attribute__((aligned(16))) char lds[LA > LB ? LA : LB];
     int w = blockIdx.x;
-    if constexpr (KB > 0) {
+    if constexpr (KB > 0 && PAGED) {
+        // Paged rows: the beacon workgroups come first, so every compact item
+        // starts at launch and the short raw workgroups fill the slots left
+        // over and those of the grid's empty items (64 sequences of U[1K,
+        // 128K] tokens: 134.6 against 145.7 us with the raw workgroups first,
+        // which held half the beacon items back until they drained).
+        if (w >= prm.seg[0].nwg) {
+            split_segment<KB, 1, 0, 0, RAWPG>(prm.seg[1], w - prm.seg[0].nwg, prm.B, prm.Lq, prm.Hq, prm.scale_log2,
+                                              lds, nullptr, &prm.rawp);
+            return;
+        }
+    } else if constexpr (KB > 0) {
         if (w < prm.seg[1].nwg) {
             split_segment<KB, 1, 0, 0, RAWPG>(prm.seg[1], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds, nullptr,
                                               &prm.rawp);
@@ -2127,9 +2138,9 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     int lat_target = cu * (lat_ks <= 2 ? 2 : 1);
     // Paged rows (compact schedule): 3.5 split items per CU.  The page reads
     // (2 KiB chunks through the table) want more workgroups in flight than the
-    // dense rows do; 64 sequences of U[1K, 128K] tokens ran a step in 143 us at
-    // 3.5 per CU, 149 us at 3, 156-165 us at 4 and 174 us filling the slots
-    // left by the raw workgroups.
+    // dense rows do; 64 sequences of U[1K, 128K] tokens ran a step in 0.151 ms
+    // at 3.5 per CU, 0.160 at 2.5, 0.164 at 3 and 0.168 at 4 (beacon
+    // workgroups first in the grid).
     int fill_target = cu * 7 / 2;
     // Keep the latent split count within the fast combine's reach (one latent
     // partial register pass, and one split per combine thread with the raw
