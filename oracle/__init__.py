@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product (`slimkv_amd/`) imports,
 calls or links anything here; only `tests/`, `__graft_entry__.smoke()` and the
-`cpu_baseline` leg of `bench.py` use it, as the checker.
+`cpu_baseline` leg of `bench.py` use it, to check results and time the host.
 
 Modules (each function cites the reference file:line it restates):
   bf16       - round-to-nearest-even bfloat16 on float arrays (bit arithmetic)
