@@ -18,9 +18,9 @@
 // when the up-projections are block diagonal a column tile only reads the
 // latent slices of the heads it holds, so each latent byte is read once.
 //
-// The combine kernel merges the split partials of both segments in fp32, lifts
-// the latent accumulator through U_V once per (b, head), folds both biases and
-// writes bf16 output plus the natural-log LSE.
+// The combine kernels merge the split partials of both segments in fp32, lift
+// the latent accumulator through U_V once per (b, head), fold both biases and
+// write bf16 output plus the natural-log LSE.
 
 #include "common.hpp"
 
@@ -1486,7 +1486,179 @@ bool combine_fast_ok(const CombineParams& cp, int T) {
            (cp.b_splits == 0 || (cp.b_w % 8 == 0 && cp.b_splits <= fast_lat_splits(cp.b_w, T)));
 }
 
+// One wave per (b, query head, query): the merge of combine_fast_kernel with
+// no barrier -- split statistics on lanes (raw splits, then latent), row
+// reductions over the wave with DPP row rotations and row swaps, split
+// weights broadcast with readlane, the latent lane groups meeting in the
+// wave's own LDS; a lane owns output columns 2 * lane and 2 * lane + 1.
+constexpr int kWaveRaw = 8;         // raw splits
+constexpr int kWaveLat = 4;         // latent partial quads per lane
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(v), CTRL, 0xf, 0xf, true));
+}
+// Over all 64 lanes: row_ror 1, 2, 4, 8 inside each 16-lane row, then the
+// row swaps.
+__device__ __forceinline__ float wave_max64(float v) {
+    v = fmaxf(v, dpp_f<0x121>(v));
+    v = fmaxf(v, dpp_f<0x122>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    return rows_max(v);
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+    v += dpp_f<0x121>(v);
+    v += dpp_f<0x122>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x128>(v);
+    return rows_sum(v);
+}
+
+template <int LW>   // latent width bound (own block), a multiple of 8
+__global__ void __launch_bounds__(64)
+combine_wave_kernel(CombineParams cp) {
+    __shared__ float4 red4[64 + LW / 4];
+    float* red = reinterpret_cast<float*>(red4);
+    const int lane = threadIdx.x;
+    const int HL = cp.Hq * cp.Lq;
+    const int pr = blockIdx.x % HL;
+    const int b = blockIdx.x / HL;
+    const int j = pr / cp.Lq;
+    const int lq = pr % cp.Lq;
+    const int h = j / (cp.Hq / cp.Hkv);
+    const int64_t row = (int64_t)b * HL + pr;
+    const int Sa = cp.a_splits, Sb = cp.b_splits, bsp = live_b_splits(cp, b);
+    const int bw = cp.b_w;
+    const int dd = 2 * lane;
+    constexpr uint32_t kPast = 0x7ffffff0u;
+
+    // -- every load at once --
+    const bool in_a = lane < Sa, in_b = lane >= Sa && lane < Sa + bsp;
+    const auto r_aml = buffer_of(cp.a_ml + row * Sa * 2, (uint32_t)Sa * 8u);
+    const auto r_bml = buffer_of(Sb ? cp.b_ml + row * Sb * 2 : nullptr, Sb ? (uint32_t)Sb * 8u : 0u);
+    const auto mla = __builtin_amdgcn_raw_buffer_load_b64(r_aml, in_a ? 8u * lane : kPast, 0, 0);
+    const auto mlb = __builtin_amdgcn_raw_buffer_load_b64(r_bml, in_b ? 8u * (lane - Sa) : kPast, 0, 0);
+    const auto r_shift = buffer_of(cp.b_shift ? cp.b_shift + row : nullptr, (Sb && cp.b_shift) ? 4u : 0u);
+    const float shift = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_shift, 0u, 0, 0)) * kLog2e;
+    const auto r_aacc = buffer_of(cp.a_acc + row * Sa * cp.a_w, (uint32_t)(Sa * cp.a_w) * 4u);
+    u32x2 ra[kWaveRaw];
+#pragma unroll
+    for (int s = 0; s < kWaveRaw; ++s)
+        ra[s] = __builtin_amdgcn_raw_buffer_load_b64(r_aacc, s < Sa ? (uint32_t)(s * cp.a_w + dd) * 4u : kPast, 0, 0);
+    const int quads = bw / 4;
+    const int ngr = quads ? 64 / quads : 1;
+    const int cq = quads ? lane % quads : 0, lg = quads ? lane / quads : 0;
+    const auto r_bacc = buffer_of(Sb ? cp.b_acc + row * Sb * bw : nullptr, (uint32_t)(Sb * bw) * 4u);
+    u32x4 lb[kWaveLat];
+#pragma unroll
+    for (int k = 0; k < kWaveLat; ++k) {
+        const int s = lg + k * ngr;
+        const bool ok = lg < ngr && s < bsp;
+        lb[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                    r_bacc, ok ? (uint32_t)(s * bw + 4 * cq) * 4u : kPast, 0, 0));
+    }
+    const uint32_t w_bytes = Sb ? (uint32_t)((int64_t)cp.Hkv * cp.D * cp.up_v_ld * 2) : 0u;
+    const auto r_wv = buffer_of(cp.up_v, w_bytes);
+    const uint32_t w0 = (uint32_t)((((int64_t)h * cp.D + dd) * cp.up_v_ld + (cp.blockdiag ? h * bw : 0)) * 2);
+    const uint32_t w1 = w0 + (uint32_t)(cp.up_v_ld * 2);
+    u32x4 wa[LW / 8], wb[LW / 8];
+#pragma unroll
+    for (int c = 0; c < LW / 8; ++c) {
+        wa[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_wv, 8 * c < bw ? w0 + 16u * c : kPast, 0, 0));
+        wb[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_wv, 8 * c < bw ? w1 + 16u * c : kPast, 0, 0));
+    }
+    const auto r_bias = buffer_of(cp.up_v_bias, (Sb && cp.up_v_bias) ? (uint32_t)(cp.Hkv * cp.D * 2) : 0u);
+    const uint32_t bias2 = __builtin_amdgcn_raw_buffer_load_b32(r_bias, (uint32_t)((h * cp.D + dd) * 2), 0, 0);
+
+    // -- split weights --
+    float mv = in_a ? __uint_as_float(mla[0]) : (in_b ? __uint_as_float(mlb[0]) : kNegInf);
+    const float lv = in_a ? __uint_as_float(mla[1]) : __uint_as_float(mlb[1]);
+    if (in_b && mv != kNegInf) mv += shift;
+    const float M = wave_max64(mv);
+    const float Mref = M == kNegInf ? 0.f : M;
+    const float w = mv != kNegInf ? fast_exp2(mv - Mref) : 0.f;
+    const float LA = wave_sum64(in_a ? lv * w : 0.f);
+    const float LB = wave_sum64(in_b ? lv * w : 0.f);
+    const float L = LA + LB;
+
+    // -- raw rows --
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < kWaveRaw; ++s) {
+        if (s >= Sa) break;
+        const float ws = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w), s));
+        o0 += ws * __uint_as_float(ra[s][0]);
+        o1 += ws * __uint_as_float(ra[s][1]);
+    }
+    // -- latent accumulator: lane groups meet in LDS, then every lane reads it --
+    if (Sb) {
+        float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < kWaveLat; ++k) {
+            const int s = lg + k * ngr;
+            const float ws = __shfl(w, Sa + s < 64 ? Sa + s : 63, 64);
+            if (lg < ngr && s < bsp) {
+                q.x += ws * __uint_as_float(lb[k].x);
+                q.y += ws * __uint_as_float(lb[k].y);
+                q.z += ws * __uint_as_float(lb[k].z);
+                q.w += ws * __uint_as_float(lb[k].w);
+            }
+        }
+        if (lg < ngr) red4[lane] = q;
+        wave_lds_fence();
+        if (lane < bw) {
+            float a = 0.f;
+            for (int g = 0; g < ngr; ++g) a += red[g * bw + lane];
+            red[256 + lane] = a;
+        }
+        wave_lds_fence();
+        float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < LW / 8; ++c) {
+            if (8 * c >= bw) break;
+            const float4 x0 = red4[64 + 2 * c], x1 = red4[65 + 2 * c];
+            const float av[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const uint32_t pa[4] = {wa[c].x, wa[c].y, wa[c].z, wa[c].w};
+            const uint32_t pb[4] = {wb[c].x, wb[c].y, wb[c].z, wb[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                l0 += lo_bf16(pa[e]) * av[2 * e] + hi_bf16(pa[e]) * av[2 * e + 1];
+                l1 += lo_bf16(pb[e]) * av[2 * e] + hi_bf16(pb[e]) * av[2 * e + 1];
+            }
+        }
+        o0 += l0 + lo_bf16(bias2) * LB;
+        o1 += l1 + hi_bf16(bias2) * LB;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *reinterpret_cast<uint32_t*>(cp.out + (int64_t)b * cp.o_sb + (int64_t)lq * cp.o_sl + (int64_t)j * cp.o_sh + dd) =
+        pack_bf16(o0 * inv, o1 * inv);
+    if (cp.lse && lane == 0)
+        cp.lse[((int64_t)b * cp.Hq + j) * cp.Lq + lq] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
+}
+
+// Whether the one-wave combine takes these partials.
+bool combine_wave_ok(const CombineParams& cp) {
+    if (cp.D != 128 || cp.a_w != 128 || cp.a_splits > kWaveRaw || cp.a_splits + cp.b_splits > 64) return false;
+    if ((reinterpret_cast<uintptr_t>(cp.out) & 3) || cp.o_sb % 2 || cp.o_sl % 2 || cp.o_sh % 2) return false;
+    if (!cp.b_splits) return true;
+    if (!cp.up_v || cp.b_w % 8 || cp.b_w > 64) return false;
+    const int ngr = 64 / (cp.b_w / 4);
+    return (cp.b_splits + ngr - 1) / ngr <= kWaveLat;
+}
+
+// The one-wave combine takes the shapes it fits (the batch-16 32K decode
+// sweep: 1.180 -> 1.138 ms; the 64-sequence paged step: 0.151 -> 0.147 ms
+// against combine_fast_kernel<128>); more splits or wider latents keep the
+// workgroup kernels.
 void launch_combine(const CombineParams& cp, int rows, hipStream_t st) {
+    if (combine_wave_ok(cp)) {
+        if (!cp.b_splits || cp.b_w <= 16) hipLaunchKernelGGL(combine_wave_kernel<16>, dim3(rows), dim3(64), 0, st, cp);
+        else if (cp.b_w <= 32) hipLaunchKernelGGL(combine_wave_kernel<32>, dim3(rows), dim3(64), 0, st, cp);
+        else if (cp.b_w <= 48) hipLaunchKernelGGL(combine_wave_kernel<48>, dim3(rows), dim3(64), 0, st, cp);
+        else hipLaunchKernelGGL(combine_wave_kernel<64>, dim3(rows), dim3(64), 0, st, cp);
+        return;
+    }
     if (combine_fast_ok(cp, 128))
         hipLaunchKernelGGL(combine_fast_kernel<128>, dim3(rows), dim3(128), 0, st, cp);
     else if (combine_fast_ok(cp, 256))
