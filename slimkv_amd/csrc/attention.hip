@@ -1499,7 +1499,8 @@ __device__ __forceinline__ float dpp_f(float v) {
     return __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(v), CTRL, 0xf, 0xf, true));
 }
 // Over all 64 lanes: row_ror 1, 2, 4, 8 inside each 16-lane row, then the
-// row swaps.
+// row swaps.  Each lane's sum associates in its own rotation order, so lanes
+// may hold sums an fp32 ulp apart (deterministic for given inputs).
 __device__ __forceinline__ float wave_max64(float v) {
     v = fmaxf(v, dpp_f<0x121>(v));
     v = fmaxf(v, dpp_f<0x122>(v));
