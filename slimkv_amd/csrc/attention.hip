@@ -88,6 +88,21 @@ struct RawPagesArg {
     int block_shift;                                 // block = 1 << block_shift tokens
 };
 
+// Query rows rotated where the split kernel reads them (the fused
+// reconstruction decode, which needs no other query preparation): q as given,
+// the RoPE tables and the query positions (null: the tables hold one row per
+// query, row b * Lq + l).  cos null: q is used as given.
+struct QRope {
+    const uint16_t* q; int64_t q_sb, q_sl, q_sh;
+    const int64_t* pos; int64_t pos_sb;
+    const float* cos; const float* sin; int64_t rope_rows;
+};
+
+__device__ __forceinline__ int64_t qrope_row(const QRope& r, int b, int l, int Lq) {
+    if (!r.pos) return (int64_t)b * Lq + l;
+    return clamp_i64(r.pos[(int64_t)b * r.pos_sb + l], 0, r.rope_rows - 1);
+}
+
 struct SplitParams {
     Seg seg[2];
     int nseg;
@@ -95,6 +110,7 @@ struct SplitParams {
     float scale_log2;
     SegRows2 two;
     RawPagesArg rawp;
+    QRope qrope;                                     // q null: seg[].q holds rotated rows
 };
 
 constexpr int kWaves = 4;
@@ -375,7 +391,7 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
 template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0, int RAWPG = 0>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int Lq, int Hq,
                                               float scale_log2, char* lds, const SegRows2* two = nullptr,
-                                              const RawPagesArg* rawp = nullptr) {
+                                              const RawPagesArg* rawp = nullptr, const QRope* qr = nullptr) {
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
     constexpr int RS = SplitLds<KS>::RS;
     const int lane = threadIdx.x & 63;
@@ -547,7 +563,24 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     // Query operand (B of the score MFMA), same k permutation as the K tile:
     // step 2c+e holds elements 32c + 8*grp + 4e + [0,4).
     u32x4 qv[KS / 2];
-    {
+    if constexpr (KS == 8) {
+        if (qr) {
+            // Rotated here from the query as given: the four pieces hold the
+            // head's 128 elements, piece c's rotate-half partner is piece c ^ 2.
+            const uint16_t* q0 = qr->q + (int64_t)b * qr->q_sb + (int64_t)lq * qr->q_sl + (int64_t)j * qr->q_sh;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) qv[c] = *reinterpret_cast<const u32x4*>(q0 + 32 * c + 8 * grp);
+            if (qr->cos) {
+                RopeRow rr;
+                const int64_t row = qrope_row(*qr, b, lq, Lq);
+                load_rope_row(rr, qr->cos + row * 128, qr->sin + row * 128, grp);
+                rope_operand(qv, rr);
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) qv[c] = zero_unless(colv, qv[c]);
+        }
+    }
+    if (!(KS == 8 && qr)) {
         const uint16_t* qrow = sg.q + (int64_t)b * sg.q_sb + (int64_t)lq * sg.q_sl + (int64_t)j * sg.q_sh;
 #pragma unroll
         for (int c = 0; c < KS / 2; ++c) {
@@ -783,6 +816,7 @@ struct ReconSeg {
     int n, hk, g, causal;
     int splits, rows_per_split, nwg;
     float* part_ml; float* part_acc;                    // partials, rv wide
+    QRope qr;                                           // q null: q above holds rotated rows
 };
 
 // One 16-key tile of latent rows in registers, with the key position of the
@@ -903,7 +937,45 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
                               : v4f{0.f, 0.f, 0.f, 0.f};
     // Rotated query of the column (B operand of the scores): d = 16t + 4grp + [0, 4).
     u32x2 qop[8];
-    {
+    if (sg.qr.q) {
+        // Rotated here from the query as given, with the reference's bf16
+        // steps (as rope_operand): element 16t + 4grp + e has its rotate-half
+        // partner at t ^ 4 in the same lane.
+        const uint16_t* qrow = sg.qr.q + (int64_t)b * sg.qr.q_sb + (int64_t)lq * sg.qr.q_sl + (int64_t)j * sg.qr.q_sh +
+                               4 * grp;
+        u32x2 x[8];
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) x[tt] = *reinterpret_cast<const u32x2*>(qrow + 16 * tt);
+        if (sg.qr.cos) {
+            const int64_t row = qrope_row(sg.qr, b, lq, Lq);
+            float4 cs[8], sn[8];
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                cs[tt] = *reinterpret_cast<const float4*>(sg.qr.cos + row * 128 + 16 * tt + 4 * grp);
+                sn[tt] = *reinterpret_cast<const float4*>(sg.qr.sin + row * 128 + 16 * tt + 4 * grp);
+            }
+            float v[8][4];
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                v[tt][0] = lo_bf16(x[tt].x); v[tt][1] = hi_bf16(x[tt].x);
+                v[tt][2] = lo_bf16(x[tt].y); v[tt][3] = hi_bf16(x[tt].y);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                const float cv[4] = {cs[tt].x, cs[tt].y, cs[tt].z, cs[tt].w};
+                const float sv[4] = {sn[tt].x, sn[tt].y, sn[tt].z, sn[tt].w};
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float partner = tt < 4 ? -v[tt ^ 4][e] : v[tt ^ 4][e];
+                    o[e] = round_bf16_hw(v[tt][e] * round_bf16_hw(cv[e])) + round_bf16_hw(partner * round_bf16_hw(sv[e]));
+                }
+                x[tt] = u32x2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) qop[tt] = u32x2{colv ? x[tt].x : 0u, colv ? x[tt].y : 0u};
+    } else {
         const uint16_t* qrow = sg.q + (int64_t)b * sg.q_sb + (int64_t)lq * sg.q_sl + (int64_t)j * sg.q_sh + 4 * grp;
 #pragma unroll
         for (int tt = 0; tt < 8; ++tt) {
@@ -1119,7 +1191,8 @@ recon_split_kernel(SplitParams prm, ReconSeg rs) {
     __shared__ __attribute__((aligned(16))) char lds[LA > LB ? LA : LB];
     int w = blockIdx.x;
     if (w < prm.seg[0].nwg) {
-        split_segment<8, 1>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds);
+        split_segment<8, 1>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds, nullptr, nullptr,
+                            prm.qrope.q ? &prm.qrope : nullptr);
         return;
     }
     w -= prm.seg[0].nwg;
@@ -2749,8 +2822,14 @@ int recon_fused_run(const slimkv_recon_decode_args* r, const ReconPlan& p, char*
     rs.part_ml = reinterpret_cast<float*>(ws + p.rml_off); rs.part_acc = reinterpret_cast<float*>(ws + p.racc_off);
     rs.wown = D; rs.nwg = p.raw.nwg;
 
+    QRope& qr = prm.qrope;
+    qr.q = static_cast<const uint16_t*>(a->q); qr.q_sb = a->q_sb; qr.q_sl = a->q_sl; qr.q_sh = a->q_sh;
+    qr.pos = a->q_positions; qr.pos_sb = a->pos_sb;
+    qr.cos = a->cos; qr.sin = a->sin; qr.rope_rows = a->rope_rows;
+
     ReconSeg bs{};
     bs.q = q_rot; bs.q_sb = rs.q_sb; bs.q_sl = rs.q_sl; bs.q_sh = rs.q_sh;
+    bs.qr = qr;
     bs.lk = static_cast<const uint16_t*>(a->lat_k); bs.lk_sb = a->lk_sb; bs.lk_sn = a->lk_sn;
     bs.lv = static_cast<const uint16_t*>(a->lat_v); bs.lv_sb = a->lv_sb; bs.lv_sn = a->lv_sn;
     bs.w = static_cast<const uint16_t*>(a->up_k); bs.bias = static_cast<const uint16_t*>(a->up_k_bias);
@@ -2833,13 +2912,14 @@ int recon_decode_run(const slimkv_recon_decode_args* r, void* workspace, size_t 
     pp.wq = 0;
     pp.B = B; pp.Lq = Lq; pp.Hq = Hq; pp.Hkv = Hkv; pp.D = D; pp.Rk = (int)a->rank_k; pp.parts = 1;
     pp.scale = (float)a->scale;
+    // The fused reconstruction decode rotates its queries where its split
+    // kernel reads them (no prologue launch; the prologue stage does nothing).
+    if (p.fused) return recon_fused_run(r, p, ws, q_rot, st, stages);
     if (stages & SLIMKV_STAGE_PROLOGUE) {
         hipLaunchKernelGGL(prologue_kernel, dim3(B * Hkv), dim3(256), 0, st, pp);
         rc = check_hip(hipGetLastError(), "prologue kernel launch");
         if (rc != SLIMKV_OK) return rc;
     }
-
-    if (p.fused) return recon_fused_run(r, p, ws, q_rot, st, stages);
 
     // 2. rebuild beacon K (optionally RoPE'd) and, unless it stays latent, V: [B, Nl, Hkv, D]
     if (has_lat && (stages & SLIMKV_STAGE_ATTEND)) {
