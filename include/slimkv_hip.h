@@ -302,8 +302,10 @@ int slimkv_prepare_rope_pairs(const float* cos, const float* sin, int64_t rows, 
 size_t slimkv_recon_decode_workspace(const slimkv_recon_decode_args* a);
 int slimkv_recon_decode(const slimkv_recon_decode_args* a, void* workspace, size_t workspace_bytes, void* stream);
 /* slimkv_recon_decode restricted to `stages` (SLIMKV_STAGE_*): the prologue
- * rotates the query; the attend stage rebuilds what the route rebuilds and
- * runs the split kernel. */
+ * rotates the query, except on the fused route (K rebuilt per tile inside the
+ * split kernel), whose split kernel rotates its query rows itself and whose
+ * prologue stage does nothing; the attend stage rebuilds what the route
+ * rebuilds and runs the split kernel. */
 int slimkv_recon_decode_stages(const slimkv_recon_decode_args* a, int stages, void* workspace,
                                size_t workspace_bytes, void* stream);
 
