@@ -270,3 +270,27 @@ def test_recon_decode_general_rope_tables_take_the_materialising_route(device):
     assert_close(got, exact, what='vs float64')
     assert_close(got, eager, what='vs bf16 eager')
     assert_lse_close(to_np(lse), lse_e)
+
+
+def test_recon_decode_fused_query_rotation_and_stages(device):
+    """The fused route rotates its queries inside the split kernel (its
+    prologue stage does nothing): a call given the query and its positions
+    equals, bit for bit, a call given the query already rotated by
+    kernels.rope_decode (bit-exact against the oracle) without tables; and
+    the three stages run as separate calls over one workspace equal one call."""
+    from slimkv_amd import _lib, kernels
+    case = latent_case(batch=4, heads=40, context=2048 + 132, tail=128, seed=91, device=device)
+    q_rot, k_rot = _rotate(case)
+    args = (k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k, case.up_v, case.scale)
+    rope = dict(q_positions=case.q_positions, cos=case.cos, sin=case.sin)
+    full = kernels.recon_decode(case.q, *args, block_diagonal=True, **rope)
+    pre = kernels.recon_decode(q_rot.transpose(1, 2).contiguous(), *args, block_diagonal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(full[0], pre[0]) and torch.equal(full[1], pre[1])
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=device)
+    out = torch.full_like(full[0], 7.0)
+    lse = torch.full_like(full[1], 7.0)
+    for stage in (_lib.STAGE_PROLOGUE, _lib.STAGE_ATTEND, _lib.STAGE_COMBINE):
+        kernels.recon_decode(case.q, *args, block_diagonal=True, out=out, lse=lse, workspace=ws, stages=stage, **rope)
+    torch.cuda.synchronize()
+    assert torch.equal(out, full[0]) and torch.equal(lse, full[1])
