@@ -186,6 +186,10 @@ def main():
         print('bench.py measures one GPU: the decode path shards by sequence with no exchange, '
               'so multi-GPU runs are not part of this build (use --gpus 1).', file=sys.stderr)
         sys.exit(2)
+    if os.environ.get('SLIMKV_HIP_LIBRARY'):
+        # an A/B override of the library: the line says so ("library"."override")
+        print(f"bench: SLIMKV_HIP_LIBRARY={os.environ['SLIMKV_HIP_LIBRARY']} overrides the in-tree library",
+              file=sys.stderr, flush=True)
     if args.workload != 'latent':
         from bench_workloads import run_workload
         print(json.dumps(run_workload(args)), flush=True)
@@ -323,6 +327,7 @@ def main():
         'replays': {'count': REPLAYS, 'median_ms': round(replay_ms, 4),
                     'median_gbps': round(sweep_bytes / (replay_ms * 1e-3) / 1e9, 1)},
         'clocks': gpu_clocks(),
+        'library': _lib.library_identity(),
     }
     if not args.no_cpu:
         rank32 = next((L for L in layers if L['rank'] == 32), layers[0])

@@ -696,12 +696,14 @@ def b1(args):
             L['q_new'] = torch.empty(1, hidden, dtype=torch.bfloat16, device=dev)
             L['o'] = torch.empty(1, hidden, dtype=torch.bfloat16, device=dev)
         token_pos = pos.view(1)
+        status = torch.zeros(1, dtype=torch.int32, device=dev)     # slot errors, checked after the timing
 
         def full_token():
             rows = kernels.query_rope_rows(cos, sin, pos)
             for L in layers:
                 q = kernels.decode_qkv(L['x'].view(1, hidden), L['w_qkv'], None, HQ, HKV, cos, sin, token_pos,
-                                       L['raw_k'], L['raw_v'], slot, plain_k=L['plain_k'], q_out=L['q_new'])
+                                       L['raw_k'], L['raw_v'], slot, plain_k=L['plain_k'], q_out=L['q_new'],
+                                       status=status)
                 kernels.latent_decode(q.view(1, 1, HQ, D), L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'],
                                       L['up_k'], L['up_v'], scale, block_diagonal=True, cos=rows[0], sin=rows[1],
                                       out=L['out'], lse=L['lse'], workspace=ws)
@@ -716,6 +718,7 @@ def b1(args):
         with torch.cuda.graph(full_graph):
             full_token()
         full_ms = _time_steps(torch, full_graph.replay, args.steps, args.warmup) * 1e3
+        kernels.check_status(status)
         per_context[ctx]['readme_scope_ms_per_token'] = round(full_ms, 4)
         del layers, ws, full_graph
         torch.cuda.empty_cache()
@@ -772,4 +775,7 @@ def b1(args):
 
 
 def run_workload(args):
-    return {'prefill': prefill, 'recon': recon, 'paged': paged, 'b1': b1, 'ceiling': ceiling}[args.workload](args)
+    from slimkv_amd._lib import library_identity
+    result = {'prefill': prefill, 'recon': recon, 'paged': paged, 'b1': b1, 'ceiling': ceiling}[args.workload](args)
+    result['library'] = library_identity()
+    return result

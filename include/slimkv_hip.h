@@ -35,6 +35,9 @@ extern "C" {
  * argument struct's `status` (device int32, optional) is set they store
  * SLIMKV_STATUS_BAD_PAGE there with an ordinary store; nothing clears it. */
 #define SLIMKV_STATUS_BAD_PAGE 1
+/* slimkv_decode_qkv: the cache slot lies outside [0, capacity); no cache row
+ * is written (the reference's index_copy_ raises IndexError). */
+#define SLIMKV_STATUS_BAD_SLOT 2
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* slimkv_last_error(void);
@@ -438,7 +441,10 @@ int slimkv_linear_rows(const slimkv_linear_rows_args* a, void* stream);
  * (slimkv/llama3/static_decode.py:148-163).  head_dim 128; x [m, K], m <= 4;
  * q [m, Hq * 128] (row stride q_sm); the caches [m, capacity, Hkv, 128] share
  * strides (c_sm, c_sn); cos/sin [rope_rows, 128] fp32; positions [m] (stride
- * pos_sm), clamped into the tables.
+ * pos_sm), clamped into the tables.  `capacity` (> 0) is the caches' slot
+ * count: a slot outside [0, capacity) writes no cache row, and when `status`
+ * (device int32, optional) is set SLIMKV_STATUS_BAD_SLOT is stored there
+ * (q is still written).
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_decode_qkv_args {
     const void* x; int64_t x_sm;
@@ -449,6 +455,8 @@ typedef struct slimkv_decode_qkv_args {
     const float* cos; const float* sin; int64_t rope_rows;
     const int64_t* positions; int64_t pos_sm;
     int64_t m, k, heads, kv_heads, head_dim;
+    int64_t capacity;
+    int32_t* status;   /* optional: SLIMKV_STATUS_BAD_SLOT on a slot outside the caches */
 } slimkv_decode_qkv_args;
 
 int slimkv_decode_qkv(const slimkv_decode_qkv_args* a, void* stream);

@@ -91,6 +91,7 @@ DecodeQKVArgs = _struct('slimkv_decode_qkv_args', [
     ('raw_k', c_ptr), ('plain_k', c_ptr), ('raw_v', c_ptr), *_i64s('c_sm', 'c_sn'),
     ('slot_index', c_ptr), ('cos', c_ptr), ('sin', c_ptr), ('rope_rows', c_i64),
     ('positions', c_ptr), ('pos_sm', c_i64), *_i64s('m', 'k', 'heads', 'kv_heads', 'head_dim'),
+    ('capacity', c_i64), ('status', c_ptr),
 ])
 
 PagedLatentDecodeArgs = _struct('slimkv_paged_latent_decode_args', [
@@ -240,20 +241,40 @@ SIGNATURES = {
     'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20
 STATUS_BAD_PAGE = 1
+STATUS_BAD_SLOT = 2
 
 
 class SlimKVError(RuntimeError):
     """A native entry point rejected its arguments or failed to launch."""
 
 
+def library_path():
+    """The library file lib() loads: the in-tree build, or the file the
+    SLIMKV_HIP_LIBRARY environment variable names (an override for A/B runs)."""
+    return Path(os.environ.get('SLIMKV_HIP_LIBRARY', LIBRARY))
+
+
+def library_identity():
+    """{'path', 'sha256', 'override'} of the library file lib() loads, for
+    measurement records: which build a figure was taken on."""
+    import hashlib
+    path = library_path()
+    digest = hashlib.sha256(path.read_bytes()).hexdigest() if path.exists() else None
+    try:
+        shown = str(path.resolve().relative_to(LIBRARY.parent.parent))
+    except ValueError:
+        shown = str(path)
+    return {'path': shown, 'sha256': digest, 'override': 'SLIMKV_HIP_LIBRARY' in os.environ}
+
+
 @lru_cache(None)
 def lib():
-    path = Path(os.environ.get('SLIMKV_HIP_LIBRARY', LIBRARY))
+    path = library_path()
     if not path.exists():
         raise ImportError(f'{path} is missing: build it with `python -m slimkv_amd.build` '
                           '(slimkv_amd has no fallback compute path)')

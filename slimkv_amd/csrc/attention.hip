@@ -1573,7 +1573,8 @@ __device__ __forceinline__ float dpp_f(float v) {
 }
 // Over all 64 lanes: row_ror 1, 2, 4, 8 inside each 16-lane row, then the
 // row swaps.  Each lane's sum associates in its own rotation order, so lanes
-// may hold sums an fp32 ulp apart (deterministic for given inputs).
+// may hold sums an fp32 ulp apart (deterministic for given inputs); callers
+// that need one value on every lane take lane 0's (wave_first).
 __device__ __forceinline__ float wave_max64(float v) {
     v = fmaxf(v, dpp_f<0x121>(v));
     v = fmaxf(v, dpp_f<0x122>(v));
@@ -1587,6 +1588,11 @@ __device__ __forceinline__ float wave_sum64(float v) {
     v += dpp_f<0x124>(v);
     v += dpp_f<0x128>(v);
     return rows_sum(v);
+}
+
+// Lane 0's value on every lane (a scalar register).
+__device__ __forceinline__ float wave_first(float v) {
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
 }
 
 template <int LW>   // latent width bound (own block), a multiple of 8
@@ -1649,11 +1655,13 @@ combine_wave_kernel(CombineParams cp) {
     float mv = in_a ? __uint_as_float(mla[0]) : (in_b ? __uint_as_float(mlb[0]) : kNegInf);
     const float lv = in_a ? __uint_as_float(mla[1]) : __uint_as_float(mlb[1]);
     if (in_b && mv != kNegInf) mv += shift;
-    const float M = wave_max64(mv);
+    // one maximum and one pair of sums for the whole row: every lane scales
+    // its two columns by the same 1 / L, lane 0 writes the LSE from that L
+    const float M = wave_first(wave_max64(mv));
     const float Mref = M == kNegInf ? 0.f : M;
     const float w = mv != kNegInf ? fast_exp2(mv - Mref) : 0.f;
-    const float LA = wave_sum64(in_a ? lv * w : 0.f);
-    const float LB = wave_sum64(in_b ? lv * w : 0.f);
+    const float LA = wave_first(wave_sum64(in_a ? lv * w : 0.f));
+    const float LB = wave_first(wave_sum64(in_b ? lv * w : 0.f));
     const float L = LA + LB;
 
     // -- raw rows --
@@ -2187,7 +2195,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 10; }
+extern "C" int slimkv_abi_version(void) { return 11; }
 
 extern "C" size_t slimkv_attention_workspace(const slimkv_attention_args* a) {
     AttnPlan plan{};

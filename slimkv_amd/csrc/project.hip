@@ -28,7 +28,7 @@ struct ProjParams {
     int64_t nq, nkv;                                   // q rows, k rows (= v rows) of the fused projection
     uint16_t* q; int64_t q_sm;
     uint16_t* raw_k; uint16_t* plain_k; uint16_t* raw_v; int64_t c_sm, c_sn;
-    const int64_t* slot;
+    const int64_t* slot; int64_t capacity; int32_t* status;
     const float* cos; const float* sin; int64_t rope_rows;
     const int64_t* pos; int64_t pos_sm;
 };
@@ -118,7 +118,12 @@ __global__ void __launch_bounds__(256) project_rows_kernel(ProjParams p) {
         }
         const bool is_k = n0 < p.nq + p.nkv;
         const int64_t r = n0 - p.nq - (is_k ? 0 : p.nkv);   // within the k (or v) rows
-        const int64_t off = m * p.c_sm + *p.slot * p.c_sn + r;  // head r / 128, element r % 128 (< 64)
+        const int64_t slot = *p.slot;
+        if (slot < 0 || slot >= p.capacity) {               // no cache row is written
+            if (p.status) *p.status = SLIMKV_STATUS_BAD_SLOT;
+            return;
+        }
+        const int64_t off = m * p.c_sm + slot * p.c_sn + r;  // head r / 128, element r % 128 (< 64)
         const float x0 = round_bf16_hw(y0), x1 = round_bf16_hw(y1);
         if (!is_k) {
             p.raw_v[off] = bf16_bits(x0);
@@ -192,6 +197,7 @@ extern "C" int slimkv_decode_qkv(const slimkv_decode_qkv_args* a, void* stream) 
     if (a->m > 1 && (a->q_sm < nq || a->c_sm < nkv || a->pos_sm < 1))
         return fail(SLIMKV_EINVAL, "output rows overlap");
     if (a->c_sn < nkv) return fail(SLIMKV_EINVAL, "cache slots overlap");
+    if (a->capacity <= 0) return fail(SLIMKV_EINVAL, "cache capacity must be positive");
     ProjParams p{};
     p.x = static_cast<const uint16_t*>(a->x); p.x_sm = a->x_sm;
     p.w = static_cast<const uint16_t*>(a->weight); p.bias = static_cast<const uint16_t*>(a->bias);
@@ -200,7 +206,7 @@ extern "C" int slimkv_decode_qkv(const slimkv_decode_qkv_args* a, void* stream) 
     p.q = static_cast<uint16_t*>(a->q); p.q_sm = a->q_sm;
     p.raw_k = static_cast<uint16_t*>(a->raw_k); p.plain_k = static_cast<uint16_t*>(a->plain_k);
     p.raw_v = static_cast<uint16_t*>(a->raw_v); p.c_sm = a->c_sm; p.c_sn = a->c_sn;
-    p.slot = a->slot_index;
+    p.slot = a->slot_index; p.capacity = a->capacity; p.status = a->status;
     p.cos = a->cos; p.sin = a->sin; p.rope_rows = a->rope_rows;
     p.pos = a->positions; p.pos_sm = a->pos_sm;
     return launch_project<true>(p, a->m, static_cast<hipStream_t>(stream));

@@ -110,6 +110,9 @@ class LatentDecodeCache:
         self.latent_index = torch.zeros(1, dtype=torch.long, device=device)
         self.raw_lengths = torch.zeros(batch, dtype=torch.int32, device=device)
         self.lat_lengths = torch.zeros(batch, dtype=torch.int32, device=device)
+        # slot errors of kernels.decode_qkv appends (prepare() already refuses
+        # a step past the capacity on the host)
+        self.status = torch.zeros(1, dtype=torch.int32, device=device)
 
     def load(self, sink_k, sink_v, raw_k, raw_v, history_k, history_v, window_k, window_v, cos=None, sin=None,
              positions=None):

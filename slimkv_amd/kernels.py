@@ -558,14 +558,41 @@ def linear_rows(x, weight, bias=None, out=None):
     return out
 
 
+def _check_qkv_shapes(x, weight, bias, heads, kv_heads, positions, q_out):
+    """Shapes slimkv_decode_qkv indexes without bounds: x [B, K] with 1 <= B <= 4,
+    a contiguous weight [(heads + 2 kv_heads) * 128, K], a bias of that many
+    elements, at least B positions, q_out [B, heads * 128]."""
+    if heads <= 0 or kv_heads <= 0 or heads % kv_heads:
+        raise ValueError('heads must be a positive multiple of kv_heads')
+    if x.dim() != 2 or not 1 <= x.shape[0] <= 4:
+        raise ValueError('x must be [B, K] with 1 <= B <= 4 rows')
+    B, K = x.shape
+    N = (heads + 2 * kv_heads) * 128
+    if weight.dim() != 2 or tuple(weight.shape) != (N, K) or not weight.is_contiguous():
+        raise ValueError(f'weight must be a contiguous [(heads + 2 kv_heads) * 128, K] = [{N}, {K}], '
+                         f'found {list(weight.shape)}')
+    if bias is not None and (bias.numel() != N or not bias.is_contiguous() or bias.dtype != BF16):
+        raise ValueError(f'bias must be a contiguous bf16 [{N}]')
+    if positions.dim() > 1 or positions.numel() < B:
+        raise ValueError(f'positions must be a 1-D tensor of at least B = {B} entries')
+    if q_out is not None and (tuple(q_out.shape) != (B, heads * 128) or q_out.stride(-1) != 1
+                              or q_out.dtype != BF16):
+        raise ValueError(f'q_out must be bf16 [{B}, {heads * 128}] with unit last stride')
+
+
 def decode_qkv(x, weight, bias, heads, kv_heads, cos, sin, positions, raw_k, raw_v, slot_index, plain_k=None,
-               q_out=None):
+               q_out=None, status=None):
     """The new token's q/k/v projection, key RoPE and raw-cache appends in one
     launch.  x [B, K] (B <= 4 rows), weight = cat([W_q, W_k, W_v]) [(Hq + 2 Hkv)
     * 128, K] (bias likewise or None), positions [B] int64, caches
     [B, capacity, Hkv, 128] (rotated K, V and optionally unrotated K) written at
-    slot = slot_index[0] (device int64).  Returns q [B, Hq * 128] unrotated."""
-    _need_device(x, weight, bias, cos, sin, positions, raw_k, raw_v, slot_index, plain_k)
+    slot = slot_index[0] (device int64).  Returns q [B, Hq * 128] unrotated.
+    A slot outside [0, capacity) writes no cache row: without a caller `status`
+    word (device int32) that raises IndexError here (one host synchronisation,
+    refused under graph capture); with one, SLIMKV_STATUS_BAD_SLOT is left in
+    it (the reference's index_copy_ raises IndexError)."""
+    _check_qkv_shapes(x, weight, bias, heads, kv_heads, positions, q_out)
+    _need_device(x, weight, bias, cos, sin, positions, raw_k, raw_v, slot_index, plain_k, q_out)
     _need_bf16(x, weight, raw_k, raw_v)
     B, K = x.shape
     if x.stride(-1) != 1:
@@ -574,18 +601,25 @@ def decode_qkv(x, weight, bias, heads, kv_heads, cos, sin, positions, raw_k, raw
     if any(c.stride() != raw_k.stride() or c.shape != raw_k.shape for c in caches) or raw_k.stride(-1) != 1 \
             or raw_k.stride(2) != 128 or raw_k.shape[2] != kv_heads or raw_k.shape[0] != B:
         raise ValueError('the caches must share shape [B, capacity, Hkv, 128] and strides')
+    if slot_index.numel() < 1:
+        raise ValueError('slot_index must hold the slot')
     if q_out is None:
         q_out = torch.empty(B, heads * 128, dtype=BF16, device=x.device)
     if cos.dtype != torch.float32 or sin.dtype != torch.float32 or not cos.is_contiguous() or \
             not sin.is_contiguous() or cos.shape != sin.shape or cos.shape[-1] != 128:
         raise ValueError('RoPE tables must be contiguous fp32 [rows, 128]')
+    if status is None and torch.cuda.is_current_stream_capturing():
+        raise ValueError('decode_qkv under graph capture needs a caller status word')
+    status, owned = _status_word(status, x.device)
     pos = positions.to(torch.int64)
     slot = slot_index.to(torch.int64)
     a = _lib.DecodeQKVArgs(_ptr(x), x.stride(0), _ptr(weight), _ptr(bias), _ptr(q_out), q_out.stride(0),
                            _ptr(raw_k), _ptr(plain_k), _ptr(raw_v), raw_k.stride(0), raw_k.stride(1), _ptr(slot),
                            _ptr(cos), _ptr(sin), cos.shape[0], _ptr(pos), pos.stride(0) if pos.dim() else 1,
-                           B, K, heads, kv_heads, 128)
+                           B, K, heads, kv_heads, 128, raw_k.shape[1], _ptr(status))
     check(lib().slimkv_decode_qkv(ctypes.byref(a), _lib.stream_handle(x.device)))
+    if owned:
+        check_status(status)
     return q_out
 
 
@@ -668,16 +702,20 @@ def _status_word(status, device):
     one that the call checks itself (one host synchronisation) when owned."""
     if status is not None:
         if status.dtype != torch.int32 or status.device != device or status.numel() < 1:
-            raise ValueError('status must be a device int32 tensor on the pages\' device')
+            raise ValueError('status must be a device int32 tensor on the tensors\' device')
         return status, False
     return torch.zeros(1, dtype=torch.int32, device=device), True
 
 
 def check_status(status):
-    """Raise IndexError when a kernel reported a block-table index error in
-    `status` (the reference's torch indexing raises IndexError for an entry
-    outside the pool, paged_cache.py:60-67).  Synchronises the host."""
-    if int(status.reshape(-1)[0].item()) != 0:
+    """Raise IndexError when a kernel reported an index error in `status`: a
+    block-table entry outside the pool (the reference's torch indexing raises
+    IndexError, paged_cache.py:60-67) or a decode cache slot outside the
+    caches (index_copy_, static_decode.py:156-163).  Synchronises the host."""
+    code = int(status.reshape(-1)[0].item())
+    if code == _lib.STATUS_BAD_SLOT:
+        raise IndexError('decode cache slot outside the cache capacity')
+    if code != 0:
         raise IndexError('block table refers to a page outside the allocation')
 
 

@@ -1,5 +1,9 @@
-"""Drop-in for the decode step of LlamaAttention.forward over a latent cache
-with the reconstruction backend, on gfx950.
+"""Drop-in for the decode step of the Llama attention classes over a latent
+cache with the reconstruction backend, on gfx950: LlamaAttention.forward
+(slimkv/llama3/modeling_llama.py:1402-1406), LlamaSdpaAttention.forward
+(:1536-1541) and LlamaFlashAttention2.forward (:1648-1653) each materialise the
+cache and run their own attention there (eager softmax, SDPA, flash_attn); the
+same `eligible` / `forward` pair serves all three.
 
 The reference (slimkv/llama3/modeling_llama.py:1384-1483) materialises the
 whole past K/V from the latents (ReconstructionCache.materialize), appends the

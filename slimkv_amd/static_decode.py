@@ -148,7 +148,8 @@ class StaticDecode:
                 # rotated and appended with its value in the same launch
                 q = kernels.decode_qkv(normalized[:, 0], fused[0], fused[1], attn.num_heads,
                                        attn.num_key_value_heads, cos, sin, positions[:, 0], cache.raw_k, cache.raw_v,
-                                       cache.raw_index, plain_k=cache.plain_k).view(B, 1, attn.num_heads, 128)
+                                       cache.raw_index, plain_k=cache.plain_k,
+                                       status=cache.status).view(B, 1, attn.num_heads, 128)
                 if size:
                     qb = attn.beacon_q_proj if 'q' in attn.config.beacon_param else attn.q_proj
                     q = torch.cat([q, qb(normalized[:, 1:]).view(B, size, attn.num_heads, 128)], dim=1)
@@ -255,6 +256,13 @@ class StaticDecode:
                                                             for x in (cache.lat_k, cache.lat_v))
         memory._window_roles = None if memory._is_full_window else memory._fast_window_roles
         memory._window_raw_indices = None if memory._is_full_window else memory._fast_window_raw_indices
+
+    def check_status(self):
+        """Raise IndexError if a captured step's cache append met a slot outside
+        the caches (synchronises the host; prepare() refuses such a step before
+        it runs, so this is a second check)."""
+        for cache in self.caches:
+            kernels.check_status(cache.status)
 
     def cache_bytes(self):
         """Logical persistent K/V bytes over all layers (memory.py:280-287)."""

@@ -1,10 +1,11 @@
 """The attention-forward drop-ins against the oracle's restatement of the
 reference forwards:
 
-* slimkv_amd.recon_decode.forward -- the decode step of LlamaAttention.forward
-  over a latent cache with the reconstruction backend
-  (slimkv/llama3/modeling_llama.py:1384-1483): materialize, append the step's
-  rows, beacon-aware RoPE, eager attention;
+* slimkv_amd.recon_decode.forward -- the decode step of LlamaAttention.forward,
+  LlamaSdpaAttention.forward and LlamaFlashAttention2.forward over a latent
+  cache with the reconstruction backend (slimkv/llama3/modeling_llama.py:
+  1384-1483, 1515-1541, 1641-1653): materialize, append the step's rows,
+  beacon-aware RoPE, attention -- reached through each class's dispatch;
 * slimkv_amd.qwen2.forward -- Qwen2FlashAttention2.forward / Qwen2Attention.forward
   (slimkv/qwen2/modeling_qwen2.py:699-779, :887-978) for prefill windows and
   decode steps, with and without unrotated beacon keys.
@@ -89,12 +90,59 @@ def _llama_module(device, skip_beacon_rope, seed):
     return att, gen
 
 
+def _eager_class(att, hidden, positions, past, output_attentions=False):
+    """The top of LlamaAttention.forward (modeling_llama.py:1399-1406) with
+    the reconstruction-decode hook ahead of the latent-decode branch."""
+    from slimkv_amd import fa2_decode, recon_decode
+    if recon_decode.eligible(att, hidden, past, output_attentions):
+        return recon_decode.forward(att, hidden, positions, past)
+    if fa2_decode.eligible(att, hidden, past, output_attentions):
+        return fa2_decode.decode(att, hidden, positions, past)
+    raise LookupError('the decode step fell through to materialize')
+
+
+def _sdpa_class(att, hidden, positions, past, output_attentions=False):
+    """The top of LlamaSdpaAttention.forward (:1515-1541): with
+    output_attentions it runs the eager class's forward; otherwise the same
+    hook before its latent-decode branch."""
+    from slimkv_amd import fa2_decode, recon_decode
+    if output_attentions:
+        return _eager_class(att, hidden, positions, past, output_attentions)
+    if recon_decode.eligible(att, hidden, past, output_attentions):
+        return recon_decode.forward(att, hidden, positions, past)
+    if fa2_decode.eligible(att, hidden, past, output_attentions):
+        return fa2_decode.decode(att, hidden, positions, past)
+    raise LookupError('the decode step fell through to materialize')
+
+
+def _fa2_class(att, hidden, positions, past, output_attentions=False):
+    """The top of LlamaFlashAttention2.forward (:1641-1653): output_attentions
+    forced off, the hook for decode steps (q_len <= 2) ahead of the
+    latent-decode branch and the join-prefill."""
+    from slimkv_amd import fa2_decode, recon_decode
+    output_attentions = False
+    if recon_decode.eligible(att, hidden, past, output_attentions):
+        return recon_decode.forward(att, hidden, positions, past)
+    if fa2_decode.eligible(att, hidden, past, output_attentions):
+        return fa2_decode.decode(att, hidden, positions, past)
+    raise LookupError('the decode step fell through to materialize')
+
+
+CLASSES = {'eager': _eager_class, 'sdpa': _sdpa_class, 'flash_attention_2': _fa2_class}
+
+
 @pytest.mark.parametrize('skip_beacon_rope', [False, True])
 @pytest.mark.parametrize('size', [0, 1])
-def test_recon_decode_forward_matches_reference_semantics(device, skip_beacon_rope, size):
+@pytest.mark.parametrize('implementation', list(CLASSES))
+def test_recon_decode_forward_matches_reference_semantics(device, skip_beacon_rope, size, implementation):
+    """The reconstruction backend's decode step through each Llama attention
+    class's dispatch (eager, SDPA, FlashAttention-2 -- the reference
+    materialises and calls its own attention in each; here every class takes
+    the same HIP forward), against the reference semantics."""
     from slimkv_amd.memory import ReconstructionCache
-    from slimkv_amd.recon_decode import eligible, forward
+    from slimkv_amd.recon_decode import eligible
     att, gen = _llama_module(device, skip_beacon_rope, seed=11 + size + 2 * skip_beacon_rope)
+    att.config._attn_implementation = implementation
     B, Hk, D, r, S, n_hist, L = 3, 2, 128, 32, 1, 300, size + 1
     roles = torch.zeros(45, dtype=torch.bool)
     roles[4::5] = True                                        # 9 window beacons among 36 raw rows
@@ -113,7 +161,7 @@ def test_recon_decode_forward_matches_reference_semantics(device, skip_beacon_ro
     hidden = (0.5 * torch.randn(B, L, 256, generator=gen, device=device)).to(torch.bfloat16)
     assert eligible(att, hidden, (pk, pv, size, indices), False)
     with torch.no_grad():
-        out, none, update = forward(att, hidden, positions, (pk, pv, size, indices))
+        out, none, update = CLASSES[implementation](att, hidden, positions, (pk, pv, size, indices))
         torch.cuda.synchronize()
         q = att.q_proj(hidden)
         k, v = att.k_proj(hidden), att.v_proj(hidden)

@@ -247,3 +247,27 @@ def test_batch1_long_context_many_splits(device, rank, queries):
     eo, el = _oracle(case, q_rot, k_rot, lat_causal=queries == 2)
     assert_close(to_np(out.transpose(1, 2)), eo)
     assert_lse_close(to_np(lse), el)
+
+
+@pytest.mark.parametrize('rank,raw_splits,lat_splits', [(32, 5, 16), (16, 8, 56), (48, 3, 16)])
+def test_one_wave_combine_matches_workgroup_combine(device, rank, raw_splits, lat_splits):
+    """The one-wave merge of the split partials and the workgroup merge, on the
+    same partials (one split plan; an output row stride of 129 elements is one
+    the one-wave merge does not take): every output within one bf16 ulp of the
+    other, the LSE within fp32 rounding, and both against the oracle."""
+    case = latent_case(batch=4, context=4096 + 132, tail=128, rank_k=rank, rank_v=rank, seed=71 + rank,
+                       device=device)
+    q_rot, k_rot = _rotated(case)
+    plan = dict(raw_splits=raw_splits, lat_splits=lat_splits)
+    wave = _run(case, k_rot, True, **plan)
+    wide = torch.zeros(4, 1, 32, 129, dtype=torch.bfloat16, device=device)
+    group = _run(case, k_rot, True, out=wide[..., :128], **plan)
+    a, b = wave[0].float(), group[0].float()
+    mag = torch.maximum(a.abs(), b.abs()).clamp_min(1e-30)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+    assert ((a - b).abs() <= ulp).all(), float((a - b).abs().max())
+    assert torch.allclose(wave[1], group[1], rtol=1e-6, atol=1e-6)
+    eo, el = _oracle(case, q_rot, k_rot)
+    for name, (out, lse) in (('one-wave', wave), ('workgroup', group)):
+        assert_close(to_np(out.transpose(1, 2)), eo, what=f'{name} merge, rank {rank}')
+        assert_lse_close(to_np(lse), el, what=f'{name} merge, rank {rank}')

@@ -117,3 +117,31 @@ def test_projection_shape_errors(device):
         kernels.linear_rows(x, w)
     with pytest.raises(Exception, match='multiple of 128'):
         kernels.linear_rows(x[:2], torch.zeros(100, 256, dtype=torch.bfloat16, device=device))
+
+
+@pytest.mark.parametrize('bad_slot', [-1, 4, 1 << 40])
+def test_decode_qkv_slot_outside_capacity(device, bad_slot):
+    """A slot outside [0, capacity) writes no cache row: IndexError without a
+    status word (the reference's index_copy_ raises), SLIMKV_STATUS_BAD_SLOT in
+    a caller's word; q is written either way and equals an in-range call's."""
+    from slimkv_amd import _lib, kernels
+    gen = torch.Generator(device=device).manual_seed(11)
+    x = torch.randn(2, 512, generator=gen, device=device).to(torch.bfloat16)
+    w = (torch.randn(6 * 128, 512, generator=gen, device=device) / 16).to(torch.bfloat16)
+    cos, sin = rope_tables(100, 128, 500000.0, device)
+    pos = torch.tensor([3, 9], device=device)
+    fill = lambda: torch.full((2, 4, 2, 128), 7.0, dtype=torch.bfloat16, device=device)
+    raw_k, raw_v, plain_k = fill(), fill(), fill()
+    slot = torch.tensor([bad_slot], device=device)
+    with pytest.raises(IndexError, match='slot'):
+        kernels.decode_qkv(x, w, None, 2, 2, cos, sin, pos, raw_k, raw_v, slot, plain_k=plain_k)
+    for cache in (raw_k, raw_v, plain_k):
+        assert (cache == 7.0).all()
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    q = kernels.decode_qkv(x, w, None, 2, 2, cos, sin, pos, raw_k, raw_v, slot, plain_k=plain_k, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == _lib.STATUS_BAD_SLOT
+    for cache in (raw_k, raw_v, plain_k):
+        assert (cache == 7.0).all()
+    good = kernels.decode_qkv(x, w, None, 2, 2, cos, sin, pos, fill(), fill(), torch.tensor([0], device=device))
+    assert torch.equal(q, good)
