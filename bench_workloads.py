@@ -152,9 +152,17 @@ def _result(metric, value, unit, args, seconds, dtype, config, **extra):
 # ----------------------------------------------------------------------------- prefill
 
 def prefill(args):
+    """The window prefill step as prefill_forward runs it over a prefill
+    history (slimkv_amd.prefill.PrefillHistory): per window the K/V rows of
+    the window are written after [sink | up(history)] in append-only buffers,
+    the window's beacon rows are down-projected and rebuilt as up(latent), the
+    prefill RoPE rotates the queries and every key but the beacons', the
+    causal attention runs over [sink | history | window], and the window's 256
+    new beacons are rebuilt onto the history.  The q/k/v projections of the
+    window (nn.Linear layers of the model) stand as given rows."""
     import torch
     from slimkv_amd import kernels
-    from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
     B, HQ, HKV, D, WIN, NB, S, r, WINDOWS = 4, 32, 8, 128, 1024, 256, 4, 32, 8
     L, R = WIN + NB, HKV * r
     dev = torch.device('cuda:0')
@@ -170,8 +178,11 @@ def prefill(args):
     latents = [torch.zeros(B, NB * WINDOWS, R, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     qs = [rnd(B, L, HQ, D) for _ in range(WINDOWS)]
     cur = [(rnd(B, L, HKV, D), rnd(B, L, HKV, D)) for _ in range(WINDOWS)]
-    sinks = rnd(B, S, HKV, D), rnd(B, S, HKV, D)
-    beacon_rows = torch.arange(4, L, 5, device=dev)             # one beacon after every 4 raw tokens
+    roles = torch.zeros(L, dtype=torch.long, device=dev)
+    roles[4::5] = 1                                             # one beacon after every 4 raw tokens
+    beacon_rows = roles.nonzero().flatten()
+    cos, sin = rope_tables(n_max, D, 500000.0, dev)
+    positions = torch.arange(n_max, device=dev)[None].expand(B, -1)
     out = torch.empty(B, L, HQ, D, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, HQ, L, dtype=torch.float32, device=dev)
     scale = D ** -0.5
@@ -181,23 +192,27 @@ def prefill(args):
 
     def window(w, timed=None):
         n = keys(w)
-        base = 0 if w == 0 else S + NB * w
-        if w:
-            work_k[:, :S].copy_(sinks[0])
-            work_v[:, :S].copy_(sinks[1])
-            for j, dst in ((0, work_k), (1, work_v)):
-                kernels.reconstruct(latents[j][:, :NB * w], up[j], kv_heads=HKV, out=dst[:, S:S + NB * w],
-                                    block_diagonal=True)
+        base = 0 if w == 0 else S + NB * w           # the window follows [sink | history]
         work_k[:, base:base + L].copy_(cur[w][0])
         work_v[:, base:base + L].copy_(cur[w][1])
-        for j in range(2):
-            kernels.down_project(cur[w][j].view(B, L, HKV * D), down[j], beacon_rows, blocks=HKV,
-                                 out=latents[j][:, NB * w:NB * (w + 1)])
+        for j, dst in ((0, work_k), (1, work_v)):
+            lat = latents[j][:, NB * w:NB * (w + 1)]
+            kernels.down_project(cur[w][j].view(B, L, HKV * D), down[j], beacon_rows, blocks=HKV, out=lat)
+            kernels.reconstruct(lat, up[j], kv_heads=HKV, out=dst[:, base:base + L], dst_rows=beacon_rows,
+                                block_diagonal=True)
+        q_rot, k_rot = kernels.prefill_rope(qs[w].transpose(1, 2), work_k[:, :n].transpose(1, 2), cos, sin,
+                                            positions[:, :n], roles, S if w else 0)
         if timed:
             timed[0].record()
-        kernels.prefill_attention(qs[w], work_k[:, :n], work_v[:, :n], scale, True, out=out, lse=lse)
+        kernels.prefill_attention(q_rot.transpose(1, 2), k_rot.transpose(1, 2), work_v[:, :n], scale, True,
+                                  out=out, lse=lse)
         if timed:
             timed[1].record()
+        # the window's new beacons onto the history (after the sink of window 0)
+        hist = S + NB * w
+        for j, dst in ((0, work_k), (1, work_v)):
+            kernels.reconstruct(latents[j][:, NB * w:NB * (w + 1)], up[j], kv_heads=HKV,
+                                out=dst[:, hist:hist + NB], block_diagonal=True)
 
     def step():
         for w in range(WINDOWS):
@@ -222,7 +237,9 @@ def prefill(args):
                      'TFLOP/s', args, seconds, 'bf16',
                      {'workload': 'window prefill, 8192-token prompt, t4, per-head rank 32', 'batch': B,
                       'window': WIN, 'beacons_per_window': NB, 'windows': WINDOWS, 'q_heads': HQ, 'kv_heads': HKV,
-                      'head_dim': D, 'sinks': S},
+                      'head_dim': D, 'sinks': S,
+                      'step': 'window K/V writes, beacon down-projection and rebuild, prefill RoPE, attention, '
+                              'the 256 new beacons rebuilt onto an append-only history'},
                      roofline={'bound': 'mfma', 'achieved': round(achieved, 1), 'peak': MFMA_BF16_PEAK_TFLOPS,
                                'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                                'traffic': None, 'kernel': 'prefill_kernel', 'kernel_ms': round(kernel_s * 1e3, 3)},

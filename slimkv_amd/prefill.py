@@ -12,7 +12,13 @@ _apply_rotary_with_beacon (:1108-1216, prefill-metadata case):
    reconstruction kernel scattered straight into the window's K/V rows.
 2. The cache update carries those latents, packed as the reference packs them.
 3. The key/value workspace [sink | up(history) | window | current] is built by
-   ReconstructionCache.materialize (reconstruction kernel for the latent parts).
+   ReconstructionCache.materialize (reconstruction kernel for the latent parts),
+   or -- for a stream of prefill windows with a PrefillHistory attached --
+   read from append-only storage that already holds [sink | up(history)]: the
+   window is written after it, and once the window is attended only its new
+   beacons are rebuilt onto the history (the reference rebuilds the whole
+   history every window, modeling_llama.py:1677-1681, from a latent history it
+   concatenates anew, slimkv/llama3/memory.py:255-267).
 4. bf16-exact RoPE that leaves beacon K unrotated (prefill RoPE kernel).
 5. Causal attention (MFMA flash-attention kernel), then o_proj_with_beacon.
 
@@ -105,15 +111,89 @@ def _pack(attention, latent):
                           rank // attention.num_key_value_heads).transpose(1, 2).contiguous()
 
 
-def prefill_forward(attention, hidden_states, position_ids, past_key_value):
+class PrefillHistory:
+    """Append-only full-dimensional K/V of one layer for a stream of prefill
+    windows: rows [0, sink + history) hold [sink | up(history beacons)] in the
+    order the memory keeps them, and each window is written right after them.
+
+    It replaces the per-window rebuild of the whole history: the memory hands
+    every window the sink and the latents of all earlier windows' beacons
+    (ReconstructionCache), and ReconstructionCache.materialize up-projects all
+    of them again (modeling_llama.py:1677-1681).  Here a window costs one
+    reconstruction of its own new beacons.  The store follows the memory's
+    update rules (slimkv/llama3/memory.py:233-278): the first window's first
+    `sink` rows become the sink, and every window's beacon latents are
+    appended to the history.  `capacity` bounds sink + history + window rows;
+    BHSD buffers [batch, kv_heads, capacity, head_dim]."""
+
+    def __init__(self, batch, kv_heads, head_dim, capacity, device, dtype=torch.bfloat16):
+        self.k = torch.empty(batch, kv_heads, capacity, head_dim, dtype=dtype, device=device)
+        self.v = torch.empty_like(self.k)
+        self.sink = 0
+        self.history = 0
+
+    def reset(self):
+        self.sink = self.history = 0
+
+    def follows(self, past_key, past_value):
+        """Whether the store holds exactly the memory's sink and history for
+        this window (and the memory has no open window rows).  An empty past
+        restarts the stream."""
+        lengths = [0 if x is None else x.shape[2] for x in (past_key.sink, past_key.history)]
+        if past_key.raw is not None or past_key.window is not None or past_value.raw is not None or \
+                past_value.window is not None:
+            return False
+        if lengths == [0, 0]:
+            self.reset()
+            return True
+        return lengths == [self.sink, self.history]
+
+    def window(self, current_k, current_v):
+        """Write the window's K/V (BHSD [B, Hk, L, D]) after the held rows and
+        return the key/value sets [sink | up(history) | window] as views."""
+        base, L = self.sink + self.history, current_k.shape[2]
+        if base + L > self.k.shape[2] or current_k.shape[0] != self.k.shape[0]:
+            raise ValueError('prefill history capacity exceeded')
+        self.k[:, :, base:base + L].copy_(current_k)
+        self.v[:, :, base:base + L].copy_(current_v)
+        return self.k[:, :, :base + L], self.v[:, :, :base + L]
+
+    def append(self, attention, key_latent, value_latent, sink_size):
+        """After the window is attended: the first window's leading rows stay
+        as the sink, and the window's new beacons -- up(latents), the rows the
+        memory appends to its history -- are rebuilt onto the history, over
+        the window's own rows."""
+        if self.history == 0 and self.sink == 0:
+            self.sink = sink_size
+        n = 0 if key_latent is None else key_latent.shape[1]
+        if n:
+            if value_latent is None or value_latent.shape[1] != n:
+                raise ValueError('prefill history needs key and value latents of the same rows')
+            heads = attention.num_key_value_heads
+            base = self.sink + self.history
+            for lat, up, dst in ((key_latent, attention.beacon_k_up_proj, self.k),
+                                 (value_latent, attention.beacon_v_up_proj, self.v)):
+                kernels.reconstruct(lat, up.weight, up.bias, kv_heads=heads,
+                                    out=dst[:, :, base:base + n].transpose(1, 2),
+                                    block_diagonal=is_block_diagonal(up.weight, heads))
+            self.history += n
+
+
+def prefill_forward(attention, hidden_states, position_ids, past_key_value, history=None):
     """(attn_output [B, L, hidden], None, cache update) for a prefill window
-    over a ReconstructionCache (modeling_llama.py:1632-1750, join_prefill)."""
+    over a ReconstructionCache (modeling_llama.py:1632-1750, join_prefill).
+    `history` (or the module's `_slimkv_prefill_history`): a PrefillHistory
+    kept across the stream's windows; it must follow the memory (an empty
+    past restarts it), else ValueError."""
     past_key, past_value, beacon_size, beacon_indices = past_key_value
     if not isinstance(past_key, ReconstructionCache):
         raise ValueError('prefill_forward expects a latent (ReconstructionCache) past')
     B, L, _ = hidden_states.shape
     Hq, Hk, D = attention.num_heads, attention.num_key_value_heads, attention.head_dim
     metadata = getattr(attention, '_prefill_metadata', None)
+    store = history if history is not None else getattr(attention, '_slimkv_prefill_history', None)
+    if store is not None and not store.follows(past_key, past_value):
+        raise ValueError('the prefill history store does not hold the memory\'s sink and history')
     q, k, v, key_latent, value_latent = project_with_beacon(attention, hidden_states, beacon_size, beacon_indices,
                                                             metadata)
     current_k, current_v = k.transpose(1, 2), v.transpose(1, 2)           # BHSD views
@@ -123,8 +203,11 @@ def prefill_forward(attention, hidden_states, position_ids, past_key_value):
                                            _pack(attention, key_latent), _pack(attention, value_latent))
         if metadata is not None:
             update.raw_indices = metadata.raw_indices
-    key_states = past_key.materialize(attention, current_k)
-    value_states = past_value.materialize(attention, current_v)
+    if store is not None:
+        key_states, value_states = store.window(current_k, current_v)
+    else:
+        key_states = past_key.materialize(attention, current_k)
+        value_states = past_value.materialize(attention, current_v)
     query_states = q.view(B, L, Hq, D).transpose(1, 2)
     if metadata is None:
         raise ValueError('prefill_forward needs the prefill metadata (prefill_ops.prepare_metadata)')
@@ -137,4 +220,6 @@ def prefill_forward(attention, hidden_states, position_ids, past_key_value):
     out, _ = kernels.prefill_attention(q_rot.transpose(1, 2), k_rot.transpose(1, 2), value_states.transpose(1, 2),
                                        scale, causal=True)
     out = out.reshape(B, L, Hq * D)
+    if store is not None:
+        store.append(attention, key_latent, value_latent, getattr(attention.config, 'beacon_sink_size', 0))
     return attention.o_proj_with_beacon(out, beacon_size, beacon_indices), None, update

@@ -1,17 +1,22 @@
 """Drop-in for the attention core of slimkv/qwen2/modeling_qwen2.py on gfx950.
 
 forward
-    Qwen2FlashAttention2.forward and the eager Qwen2Attention.forward
-    (slimkv/qwen2/modeling_qwen2.py:887-978, :699-779) with their Python
-    signature: the module's own projections (qkv_proj_with_beacon) and output
+    Qwen2FlashAttention2.forward (slimkv/qwen2/modeling_qwen2.py:887-978)
+    with its Python signature, for batches without padding: the reference's
+    memory drops the mask for flash_attention_2 when no token is padded
+    (slimkv/memory.py:618-622) and this forward takes exactly that call.  The
+    eager Qwen2Attention.forward (:699-779) always receives the memory's 4-D
+    mask (slimkv/memory.py:626-633), which this forward refuses (ValueError),
+    so it is not a drop-in there.  The module's own projections
+    (qkv_proj_with_beacon) and output
     projection (o_proj_with_beacon) as they are; the beacon-aware RoPE of
     _apply_rotary_with_beacon (:602-635) in the bf16-exact prefill RoPE kernel;
     causal GQA attention over [past ; current] in the split-K decode kernel
     (one or two query rows) or the MFMA prefill kernel (longer windows).
 flash_attention_forward
     Qwen2FlashAttention2._flash_attention_forward (:980-1040) for batches
-    without padding (the model passes no mask then, :1299-1301 of the model
-    forward): bottom-right causal attention, BSHD in and out.
+    without padding (no mask, as above): bottom-right causal attention, BSHD
+    in and out.
 
 The past K/V stay pre-RoPE as the reference keeps them (the returned cache
 holds the current step's keys before RoPE), so every step rotates the whole

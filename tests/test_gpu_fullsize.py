@@ -155,13 +155,18 @@ def _llama8b_module(device, seed):
 
 
 def test_c3_prefill_window_chain(device):
+    """The chain through prefill_forward with the append-only PrefillHistory
+    (each window rebuilds only its new beacons) against the oracle; every
+    window's output and latents also bit-identical to the same window run
+    through ReconstructionCache.materialize (the whole history rebuilt)."""
     from slimkv_amd.memory import ReconstructionCache
-    from slimkv_amd.prefill import prefill_forward
+    from slimkv_amd.prefill import PrefillHistory, prefill_forward
     from slimkv_amd.prefill_ops import PrefillMetadata
     B, L, H, Hk, D, R, S, NB, WINDOWS = 4, 1280, 32, 8, 128, 256, 4, 256, 8
     heads = (5, 30)                                           # sampled query heads (KV heads 1 and 7)
     check = (0, 3, 7)
     att, gen = _llama8b_module(device, 77)
+    store = PrefillHistory(B, Hk, D, S + NB * WINDOWS + L, device)
     roles = torch.zeros(L, dtype=torch.long, device=device)
     roles[4::5] = 1                                           # a beacon after every 4 raw tokens
     brows = (roles != 0).nonzero().flatten().cpu().numpy()
@@ -177,8 +182,13 @@ def test_c3_prefill_window_chain(device):
         att._prefill_metadata = PrefillMetadata((roles == 0).nonzero().flatten(), (roles != 0).nonzero().flatten(),
                                                 roles, positions, False)
         with torch.no_grad():
-            out, _, update = prefill_forward(att, hidden, positions, (pk, pv, NB, roles))
+            out, _, update = prefill_forward(att, hidden, positions, (pk, pv, NB, roles), history=store)
+            full, _, full_update = prefill_forward(att, hidden, positions, (pk, pv, NB, roles))
             torch.cuda.synchronize()
+            assert torch.equal(out, full), f'window {w}: append-only history output differs from the full rebuild'
+            assert torch.equal(update.key_latents, full_update.key_latents)
+            assert torch.equal(update.value_latents, full_update.value_latents)
+            assert (store.sink, store.history) == (S, NB * (w + 1))
             if w in check:
                 q_mod = torch.where((roles == 0)[:, None], att.q_proj(hidden), att.beacon_q_proj(hidden))
                 kf, vf = att.k_proj(hidden), att.v_proj(hidden)
