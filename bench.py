@@ -13,8 +13,9 @@ layer rotates at the same positions) and passes them to each layer.  The
 32-layer sweep is captured once in a HIP graph and replayed.
 
 value  = algorithmic bytes of the sweep / sweep time (GB/s), inputs resident in HBM.
-roofline = the split-K attention kernel alone: its algorithmic bytes per launch
-           / its average duration measured with HIP events on the launch stream.
+roofline = the split-K attention kernel alone (it makes its own query operands):
+           its algorithmic bytes per launch / its average duration measured with
+           HIP events on the launch stream.
 cpu_baseline = the reference eager fp32 path restated in torch, one full-shape
            rank-32 layer repeated for ~10-30 s on the host cores.
 """
@@ -62,6 +63,11 @@ def layer_bytes(rk, rv):
 def split_kernel_bytes(rk, rv):
     """Bytes the split-K kernel must read: latent rows, raw rows and q once."""
     return B * (BEACONS * HKV * (rk + rv) * 2 + RAW * HKV * D * 2 * 2 + HQ * D * 2)
+
+
+def fused_kernel_bytes(rk, rv):
+    """The split kernel that makes its own query operands also reads U_K once."""
+    return split_kernel_bytes(rk, rv) + HKV * D * rk * 2
 
 
 REPLAYS = 50
@@ -250,46 +256,58 @@ def main():
     print(f'bench: sweep {ms_per_step:.3f} ms, {gbps:.1f} GB/s', file=sys.stderr, flush=True)
     replay_ms = replay_median_ms(torch, step, REPLAYS)
 
-    # Split-K kernel alone, through the library's staged entry point: every
-    # layer's prologue stage runs once into a workspace of its own, then the
-    # attend stages (the split kernel, full work over the layer's own latent and
-    # raw rows and its own query operands) of one rank's layers -- each with
-    # its own buffers, so the cache holds none of them -- are captured back to
-    # back in one graph and timed with HIP events over PROFILE_REPLAYS replays:
-    # the per-launch average includes the hand-off between launches, as the
-    # kernel trace does, and no per-launch event cost.
+    # The split kernel alone, as the sweep runs it: with per-head bases and no
+    # K bias a call of the prologue and attend stages is one launch of the
+    # split kernel that makes its own query operands (query RoPE, absorption
+    # into U_K).  One rank's layers -- each with its own buffers, so the cache
+    # holds none of them -- are captured back to back in one graph and timed
+    # with HIP events over PROFILE_REPLAYS replays: the per-launch average
+    # includes the hand-off between launches, as the kernel trace does, and no
+    # per-launch event cost.  Beside it the attend stage alone over query
+    # operands a prologue stage wrote beforehand (the three-launch form).
     from slimkv_amd._lib import STAGE_ATTEND, STAGE_PROLOGUE
-    stage_ws = [torch.empty(ws_bytes, dtype=torch.uint8, device=device) for _ in layers]
     rows = kernels.query_rope_rows(cos, sin, step_pos)
-    for L, w in zip(layers, stage_ws):
-        run_layer(kernels, L, rows, scale, w, stages=STAGE_PROLOGUE)
-    torch.cuda.synchronize()
-    durations = {}
-    for r in sorted(set(ranks)):
-        group = [(L, w) for L, w in zip(layers, stage_ws) if L['rank'] == r]
 
-        def split_sweep():
-            for L, w in group:
-                run_layer(kernels, L, rows, scale, w, stages=STAGE_ATTEND)
-        split_sweep()
+    def timed_graph(body):
+        body()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            split_sweep()
+            body()
         torch.cuda.current_stream().wait_stream(side)
-        split_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(split_graph):
-            split_sweep()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            body()
         for _ in range(3):
-            split_graph.replay()
+            g.replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         a.record()
         for _ in range(PROFILE_REPLAYS):
-            split_graph.replay()
+            g.replay()
         b.record()
         torch.cuda.synchronize()
-        durations[r] = [a.elapsed_time(b) * 1e-3 / (PROFILE_REPLAYS * len(group))]
+        return a.elapsed_time(b) * 1e-3 / PROFILE_REPLAYS
+
+    durations, staged = {}, {}
+    for r in sorted(set(ranks)):
+        group = [L for L in layers if L['rank'] == r]
+
+        def fused_sweep():
+            for L in group:
+                run_layer(kernels, L, rows, scale, workspace, stages=STAGE_PROLOGUE | STAGE_ATTEND)
+        durations[r] = [timed_graph(fused_sweep) / len(group)]
+    stage_ws = [torch.empty(ws_bytes, dtype=torch.uint8, device=device) for _ in layers]
+    for L, w in zip(layers, stage_ws):
+        run_layer(kernels, L, rows, scale, w, stages=STAGE_PROLOGUE)
+    torch.cuda.synchronize()
+    for r in sorted(set(ranks)):
+        group = [(L, w) for L, w in zip(layers, stage_ws) if L['rank'] == r]
+
+        def attend_sweep():
+            for L, w in group:
+                run_layer(kernels, L, rows, scale, w, stages=STAGE_ATTEND)
+        staged[r] = timed_graph(attend_sweep) / len(group)
     del stage_ws
     # The read rate a plain grid-stride stream reaches on this GPU (the
     # slimkv_probe_stream_read ceiling probe), to read the split kernel's rate
@@ -299,18 +317,19 @@ def main():
     dom = 32 if 32 in durations else max(durations, key=lambda r: len(durations[r]))
     dur = durations[dom]
     dur_avg = sum(dur) / len(dur)
-    achieved = split_kernel_bytes(dom, dom) / dur_avg / 1e9
+    achieved = fused_kernel_bytes(dom, dom) / dur_avg / 1e9
     all_split = sum(sum(v) / len(v) * ranks.count(r) for r, v in durations.items())
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                 'frac': round(achieved / HBM_PEAK_GBPS, 4),
                 'traffic': SPLIT_TRAFFIC_BYTES.get(dom), 'traffic_source': TRAFFIC_SOURCE,
-                'kernel': f'split_kernel (rank-{dom} layers)',
+                'kernel': f'split_kernel, query operands made in the kernel (rank-{dom} layers)',
                 'avg_us': round(dur_avg * 1e6, 2),
                 'split_kernel_sweep_frac': round(all_split / (elapsed / args.steps), 3),
                 'ceiling': {'plain_gbps': ceiling['plain'], 'nt_gbps': ceiling['nt'],
                             'frac_of_plain': round(achieved / ceiling['plain'], 4),
                             'source': 'slimkv_probe_stream_read over 4 GiB, best configuration, same run'},
-                'avg_us_by_rank': {str(r): round(sum(v) / len(v) * 1e6, 2) for r, v in sorted(durations.items())}}
+                'avg_us_by_rank': {str(r): round(sum(v) / len(v) * 1e6, 2) for r, v in sorted(durations.items())},
+                'attend_stage_us_by_rank': {str(r): round(v * 1e6, 2) for r, v in sorted(staged.items())}}
 
     result = {
         'metric': METRIC, 'value': round(gbps, 1), 'unit': 'GB/s', 'n_gpus': 1, 'steps': args.steps,

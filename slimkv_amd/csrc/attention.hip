@@ -103,6 +103,15 @@ __device__ __forceinline__ int64_t qrope_row(const QRope& r, int b, int l, int L
     return clamp_i64(r.pos[(int64_t)b * r.pos_sb + l], 0, r.rope_rows - 1);
 }
 
+// Latent query operands made inside the split kernel (the fused decode with
+// per-KV-head bases): each latent wave rotates its query rows from
+// SplitParams::qrope and absorbs them into its heads' U_K on the MFMA, and the
+// raw waves rotate theirs, so no prologue launch precedes the split kernel.
+struct QAbsorb {
+    const uint16_t* ut;                              // per-head U_K^T [Hkv][wq][128], null: Seg::q holds operands
+    int wq;                                          // per-head K rank
+};
+
 struct SplitParams {
     Seg seg[2];
     int nseg;
@@ -111,6 +120,7 @@ struct SplitParams {
     SegRows2 two;
     RawPagesArg rawp;
     QRope qrope;                                     // q null: seg[].q holds rotated rows
+    QAbsorb absorb;
 };
 
 constexpr int kWaves = 4;
@@ -382,16 +392,142 @@ __device__ __forceinline__ void load_tile_pair(TileRegs<KS>& t, const TilePair& 
     }
 }
 
+// Fused query operands (FQ instances): the RoPE table rows of a wave's query
+// positions pass through the wave's own LDS (its V-tile buffer, idle until the
+// first tile is consumed), so a lane holds one 16-byte piece of them instead
+// of the 64 table values its rotation reads.  Lane l loads elements
+// 4 (l % 32) + [0, 4) of the cos (l < 32) or sin (l >= 32) row of query slot
+// lq' < Lq <= 2; the wave's LDS holds row lq' at [256 lq', 256 lq' + 256)
+// floats, cos then sin.
+struct RopeStage {
+    u32x4 v[2];                                      // table bits (ext vector: kept in registers)
+};
+
+// Both slots are loaded and stored whatever Lq is (slot 1 repeats slot 0 when
+// Lq is 1), and without tables (a query given rotated) the loads read the
+// query's first 16 bytes, unused: a load under a run-time condition would be
+// kept in scratch memory.
+__device__ __forceinline__ void rope_stage_load(RopeStage& st, const QRope& qr, int b, int Lq, int lane) {
+    const bool tables = qr.cos != nullptr;
+    const float* tab = !tables ? reinterpret_cast<const float*>(qr.q) : ((lane >> 5) ? qr.sin : qr.cos);
+    const int e = tables ? 4 * (lane & 31) : 0;
+#pragma unroll
+    for (int l = 0; l < 2; ++l) {
+        const int64_t row = tables ? qrope_row(qr, b, l < Lq ? l : 0, Lq) : 0;
+        st.v[l] = *reinterpret_cast<const u32x4*>(tab + row * 128 + e);
+    }
+}
+
+__device__ __forceinline__ void rope_stage_store(const RopeStage& st, float* rows, int lane) {
+#pragma unroll
+    for (int l = 0; l < 2; ++l)
+        *reinterpret_cast<u32x4*>(rows + 256 * l + 128 * (lane >> 5) + 4 * (lane & 31)) = st.v[l];
+}
+
+// rope_operand with the table row read from LDS (cos at row[0, 128), sin at
+// row[128, 256)): the same values and the same bf16 operation order, one
+// rotate-half pair of pieces (c, c + 2) at a time so that a lane holds 32 of
+// the table values at once instead of 64.
+__device__ __forceinline__ void rope_operand_lds(u32x4 (&x)[4], const float* row, int grp) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        float v[2][8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[h][2 * e] = bf16_to_f32(x[c + 2 * h][e] & 0xffffu);
+                v[h][2 * e + 1] = bf16_to_f32(x[c + 2 * h][e] >> 16);
+            }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int d0 = 32 * (c + 2 * h) + 8 * grp;
+            const float4 c0 = *reinterpret_cast<const float4*>(row + d0);
+            const float4 c1 = *reinterpret_cast<const float4*>(row + d0 + 4);
+            const float4 s0 = *reinterpret_cast<const float4*>(row + 128 + d0);
+            const float4 s1 = *reinterpret_cast<const float4*>(row + 128 + d0 + 4);
+            const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                float o[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float partner = h == 0 ? -v[1][i + u] : v[0][i + u];
+                    o[u] = round_bf16_hw(v[h][i + u] * round_bf16_hw(cv[i + u])) +
+                           round_bf16_hw(partner * round_bf16_hw(sv[i + u]));
+                }
+                w[i / 2] = pack_bf16(o[0], o[1]);
+            }
+            x[c + 2 * h] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+    }
+}
+
+// The absorption of a latent wave's rotated query rows into its heads' U_K
+// (what the prologue writes to the workspace, bit for bit, made in place):
+// chunk c of the operand (tile columns 32c + [0, 32)) comes from two MFMA
+// blocks t, and block t's row 4g + e is tile column 32c + 8g + 4t + e, so lane
+// (col, grp) receives exactly the eight columns 32c + 8grp + [0, 8) it feeds
+// the score MFMA.  A row's head and latent dimension follow from its tile
+// column (per-head blocks of blk_k columns from the wave's first block); rows
+// past the span read row 0 of the first block and meet a zero select.  Each
+// U_K^T row is read as the prologue reads it (k-steps of 32 in order), so each
+// output element is the same MFMA dot product.  The rows are loaded first
+// (absorb_load) and used once the query is rotated (absorb_apply), so that
+// the caller can issue other loads in between.
+template <int KS>
+struct AbsorbRows {
+    u32x4 a[KS / 2][2][4];
+};
+
+template <int KS>
+__device__ __forceinline__ void absorb_load(AbsorbRows<KS>& u, const QAbsorb& qa, int col, int grp, int first_blk,
+                                            int blk_k, int span_k) {
+#pragma unroll
+    for (int c = 0; c < KS / 2; ++c)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int xcol = 32 * c + 8 * (col >> 2) + 4 * t + (col & 3);
+            const bool in = xcol < span_k;
+            const int head = first_blk + (in ? xcol / blk_k : 0);
+            const int dim = in ? xcol % blk_k : 0;
+            const uint16_t* urow = qa.ut + ((int64_t)head * qa.wq + dim) * 128 + 8 * grp;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) u.a[c][t][kk] = *reinterpret_cast<const u32x4*>(urow + 32 * kk);
+        }
+}
+
+template <int KS>
+__device__ __forceinline__ void absorb_apply(u32x4 (&qv)[KS / 2], const AbsorbRows<KS>& u, const u32x4 (&x)[4],
+                                             int col, int span_k) {
+#pragma unroll
+    for (int c = 0; c < KS / 2; ++c) {
+        v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const bool in = 32 * c + 8 * (col >> 2) + 4 * t + (col & 3) < span_k;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) acc[t] = mfma32(zero_unless(in, u.a[c][t][kk]), x[kk], acc[t]);
+        }
+        qv[c] = u32x4{pack_bf16(acc[0][0], acc[0][1]), pack_bf16(acc[0][2], acc[0][3]),
+                      pack_bf16(acc[1][0], acc[1][1]), pack_bf16(acc[1][2], acc[1][3])};
+    }
+}
+
 // A workgroup owns (batch b, group of 4 tile slots, key split s); a slot is a
 // (KV head, column tile) pair and each wave takes one slot.  The four waves
 // therefore stream the same keys' rows at the same time (whole DRAM pages),
 // never exchange data, and write their own partials.
 // PAGED: 0 dense rows, 1 rows through per-lane page ids, 2 rows through the
 // tile's two pages (pages of at least 16 rows).
-template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0, int RAWPG = 0>
+template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0, int RAWPG = 0, int FQ = 0>
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int Lq, int Hq,
                                               float scale_log2, char* lds, const SegRows2* two = nullptr,
-                                              const RawPagesArg* rawp = nullptr, const QRope* qr = nullptr) {
+                                              const RawPagesArg* rawp = nullptr, const QRope* qr = nullptr,
+                                              const QAbsorb* qa = nullptr) {
+    static_assert(!FQ || KS <= 8, "fused query operands are built for tiles up to 128 columns");
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
     constexpr int RS = SplitLds<KS>::RS;
     const int lane = threadIdx.x & 63;
@@ -549,6 +685,20 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     };
     using PageIds = std::conditional_t<PAGED == 2, TilePair, TilePages<KS>>;
     PageIds pcur, poth;
+    uint16_t* vbuf = reinterpret_cast<uint16_t*>(lds) + wave * 2 * 16 * RS;
+    // FQ: the query rows and their RoPE table rows go out first, so that
+    // waiting for them does not wait for the first tile (loads complete in
+    // issue order); the first tile follows at once and is in flight while the
+    // rotation runs.  qa null: the raw segment.
+    const bool fq_rot = FQ && qr->cos;
+    RopeStage rst;
+    u32x4 fx[4];
+    if constexpr (FQ) {
+        rope_stage_load(rst, *qr, b, Lq, lane);
+        const uint16_t* q0 = qr->q + (int64_t)b * qr->q_sb + (int64_t)lq * qr->q_sl + (int64_t)j * qr->q_sh + 8 * grp;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) fx[c] = *reinterpret_cast<const u32x4*>(q0 + 32 * c);
+    }
     // First tile in flight before the query operand is fetched.
     TileRegs<KS> cur;
     if constexpr (PAGED) {
@@ -562,9 +712,48 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
 
     // Query operand (B of the score MFMA), same k permutation as the K tile:
     // step 2c+e holds elements 32c + 8*grp + 4e + [0,4).
+    // A query given as is (QRope::q set) is rotated here; a null QRope::q, or
+    // no QRope, means the segment's q holds prepared operands.  The pointers
+    // are never selected at run time (that would put the kernel arguments in
+    // scratch memory), only the fields they point at are tested.
+    const bool rot = !FQ && qr && qr->q;
+    const bool absorb = rot && qa && qa->ut;
     u32x4 qv[KS / 2];
-    if constexpr (KS == 8) {
-        if (qr) {
+    if constexpr (FQ) {
+        float* rows = reinterpret_cast<float*>(vbuf);
+        rope_stage_store(rst, rows, lane);
+        if (fq_rot) {
+            wave_lds_fence();
+#pragma unroll
+            for (int c = 0; c < 4; ++c) fx[c] = zero_unless(colv, fx[c]);
+            rope_operand_lds(fx, rows + 256 * lq, grp);
+            wave_lds_fence();
+        }
+        if (qa) {
+            // U_K^T rows once the query is rotated (few registers are live
+            // then); the absorption waits for them and, loads completing in
+            // issue order, for the first tile.  The second tile goes out after
+            // the absorption: issued before it, the second tile or the U_K^T
+            // rows left too few registers for the other (spills) or made the
+            // absorption wait for both tiles (C1 ranks 16/32/48: 18.7 / 27.1 /
+            // 41.7 us a launch this way; 18.9 / 28.1 / 43.2 with the second
+            // tile before the U_K^T rows; 23-26 / 34-37 / 57 with the rows
+            // first, spilling).
+            AbsorbRows<KS> u;
+            absorb_load<KS>(u, *qa, col, grp, first_blk, sg.blk_k, span_k);
+            absorb_apply<KS>(qv, u, fx, col, span_k);
+#pragma unroll
+            for (int c = 0; c < KS / 2; ++c) {
+                const int kk = 32 * c + 8 * grp;
+                const bool in = colv && kk >= own_k_lo && kk + 8 <= own_k_lo + own_k_w && kk + 8 <= span_k;
+                qv[c] = zero_unless(in, qv[c]);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < KS / 2; ++c) qv[c] = zero_unless(colv, fx[c]);
+        }
+    } else if constexpr (KS == 8) {
+        if (rot && !absorb) {
             // Rotated here from the query as given: the four pieces hold the
             // head's 128 elements, piece c's rotate-half partner is piece c ^ 2.
             const uint16_t* q0 = qr->q + (int64_t)b * qr->q_sb + (int64_t)lq * qr->q_sl + (int64_t)j * qr->q_sh;
@@ -580,7 +769,9 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
             for (int c = 0; c < 4; ++c) qv[c] = zero_unless(colv, qv[c]);
         }
     }
-    if (!(KS == 8 && qr)) {
+    if (FQ) {
+        // the operand is made above
+    } else if (!(KS == 8 && rot)) {
         const uint16_t* qrow = sg.q + (int64_t)b * sg.q_sb + (int64_t)lq * sg.q_sl + (int64_t)j * sg.q_sh;
 #pragma unroll
         for (int c = 0; c < KS / 2; ++c) {
@@ -595,8 +786,6 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     v4f acc[VT];
 #pragma unroll
     for (int i = 0; i < VT; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    uint16_t* vbuf = reinterpret_cast<uint16_t*>(lds) + wave * 2 * 16 * RS;
 
     // One 16-key tile: V to LDS, scores, online softmax, P^T V^T.  The tile's
     // rows past the sequence were read from a clamped row: their scores are
@@ -755,7 +944,9 @@ struct SplitDepth {
     static constexpr int value = 2;
 };
 
-template <int KA, int KB, int PAGED = 0, int SEG2 = 0, int RAWPG = 0>
+// FQ: the query operands are made here (QRope and QAbsorb of SplitParams),
+// no prologue launch precedes the kernel.
+template <int KA, int KB, int PAGED = 0, int SEG2 = 0, int RAWPG = 0, int FQ = 0>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(SplitWaves<KA>::value)))
 split_kernel(SplitParams prm) {
     constexpr int LA = SplitLds<KA>::bytes;
@@ -769,20 +960,21 @@ split_kernel(SplitParams prm) {
         // 128K] tokens: 134.6 against 145.7 us with the raw workgroups first,
         // which held half the beacon items back until they drained).
         if (w >= prm.seg[0].nwg) {
-            split_segment<KB, 1, 0, 0, RAWPG>(prm.seg[1], w - prm.seg[0].nwg, prm.B, prm.Lq, prm.Hq, prm.scale_log2,
-                                              lds, nullptr, &prm.rawp);
+            split_segment<KB, 1, 0, 0, RAWPG, FQ>(prm.seg[1], w - prm.seg[0].nwg, prm.B, prm.Lq, prm.Hq,
+                                                  prm.scale_log2, lds, nullptr, &prm.rawp, FQ ? &prm.qrope : nullptr);
             return;
         }
     } else if constexpr (KB > 0) {
         if (w < prm.seg[1].nwg) {
-            split_segment<KB, 1, 0, 0, RAWPG>(prm.seg[1], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds, nullptr,
-                                              &prm.rawp);
+            split_segment<KB, 1, 0, 0, RAWPG, FQ>(prm.seg[1], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds, nullptr,
+                                                  &prm.rawp, FQ ? &prm.qrope : nullptr);
             return;
         }
         w -= prm.seg[1].nwg;
     }
-    split_segment<KA, SplitDepth<KA>::value, PAGED, SEG2>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds,
-                                                          &prm.two);
+    split_segment<KA, SplitDepth<KA>::value, PAGED, SEG2, 0, FQ>(prm.seg[0], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2,
+                                                                 lds, &prm.two, nullptr, FQ ? &prm.qrope : nullptr,
+                                                                 FQ ? &prm.absorb : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -2005,6 +2197,31 @@ hipError_t launch_split_any(int ka, int kb, const SplitParams& prm, int grid, hi
     return seg2 ? dispatch_split_seg2(ka, prm, grid, st) : dispatch_split(ka, kb, prm, grid, st);
 }
 
+// Instances that make their query operands (FQ): latent tiles up to 128
+// columns beside the head_dim-128 raw rows -- dense rows in one or two
+// segments, and rows through pages of at least 16 slots with the raw rows
+// dense or through raw pages.
+template <int PAGED, int SEG2, int RAWPG>
+hipError_t launch_split_fq(int ka, const SplitParams& prm, int grid, hipStream_t st) {
+    switch (ka) {
+        case 2: hipLaunchKernelGGL((split_kernel<2, 8, PAGED, SEG2, RAWPG, 1>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 4: hipLaunchKernelGGL((split_kernel<4, 8, PAGED, SEG2, RAWPG, 1>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 6: hipLaunchKernelGGL((split_kernel<6, 8, PAGED, SEG2, RAWPG, 1>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        case 8: hipLaunchKernelGGL((split_kernel<8, 8, PAGED, SEG2, RAWPG, 1>), dim3(grid), dim3(kThreads), 0, st, prm); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+bool split_fq_ok(int ka, bool paged, int slots) {
+    return (ka == 2 || ka == 4 || ka == 6 || ka == 8) && (!paged || slots >= 16);
+}
+
+hipError_t launch_split_fused(int ka, const SplitParams& prm, int grid, hipStream_t st, bool paged, bool seg2) {
+    if (paged) return prm.rawp.table ? launch_split_fq<2, 0, 1>(ka, prm, grid, st) : launch_split_fq<2, 0, 0>(ka, prm, grid, st);
+    return seg2 ? launch_split_fq<0, 1, 0>(ka, prm, grid, st) : launch_split_fq<0, 0, 0>(ka, prm, grid, st);
+}
+
 int round_even_tile(int width) {
     // MFMA k-steps of 16 needed for `width`, rounded to the instantiated set.
     const int ks = (width + 15) / 16;
@@ -2508,7 +2725,13 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     const bool mfma_prologue = has_lat && bd && pp.ut && pp.wq % 16 == 0 && nct >= 1 && nct <= 3 &&
                                g * Lq <= 16 && ptr_aligned16(pp.ut) && ptr_aligned16(a->q) &&
                                (!a->up_k_bias || ptr_aligned16(a->up_k_bias));
-    if (!(stages & SLIMKV_STAGE_PROLOGUE)) {
+    // With per-head bases and no K bias, a call that runs the prologue and the
+    // attend stage together makes the query operands inside the split kernel
+    // (its raw waves rotate their rows, its latent waves rotate and absorb
+    // theirs): two launches a layer instead of three, the same bits.
+    const bool fused = mfma_prologue && !a->up_k_bias && (stages & SLIMKV_STAGE_PROLOGUE) &&
+                       (stages & SLIMKV_STAGE_ATTEND) && split_fq_ok(p.lat.ks, pg != nullptr, pg ? (int)pg->slots : 0);
+    if (fused || !(stages & SLIMKV_STAGE_PROLOGUE)) {
         // the query operands of an earlier prologue stage are in the workspace
     } else if (mfma_prologue) {
         if (nct == 1) hipLaunchKernelGGL(prologue_mfma_kernel<1>, dim3(B * Hkv), dim3(64), 0, st, pp);
@@ -2524,6 +2747,10 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     prm.B = B; prm.Lq = Lq; prm.Hq = Hq;
     prm.scale_log2 = (float)(a->scale * 1.4426950408889634);
     prm.nseg = has_lat ? 2 : 1;
+    if (fused) {
+        prm.qrope = QRope{pp.q, pp.q_sb, pp.q_sl, pp.q_sh, pp.pos, pp.pos_sb, pp.cos, pp.sin, pp.rope_rows};
+        prm.absorb = QAbsorb{pp.ut, pp.wq};
+    }
     // Latent rows (the bulk, pipelined) are segment 0; the short raw segment is
     // segment 1, whose workgroups split_kernel places first in the grid.
     Seg& r = prm.seg[has_lat ? 1 : 0];
@@ -2586,7 +2813,9 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     if (paged && ka > 8) return fail(SLIMKV_EUNSUP, "paged decode handles latent tiles up to 128 wide");
     const int grid = prm.seg[0].nwg + (has_lat ? prm.seg[1].nwg : 0);
     if (stages & SLIMKV_STAGE_ATTEND) {
-        rc = check_hip(launch_split_any(ka, kb, prm, grid, st, paged, has_lat && a->lat_k2 != nullptr),
+        const bool seg2 = has_lat && a->lat_k2 != nullptr;
+        rc = check_hip(fused ? launch_split_fused(ka, prm, grid, st, paged, seg2)
+                             : launch_split_any(ka, kb, prm, grid, st, paged, seg2),
                        "split kernel launch");
         if (rc != SLIMKV_OK) return rc;
     }

@@ -271,3 +271,61 @@ def test_one_wave_combine_matches_workgroup_combine(device, rank, raw_splits, la
     for name, (out, lse) in (('one-wave', wave), ('workgroup', group)):
         assert_close(to_np(out.transpose(1, 2)), eo, what=f'{name} merge, rank {rank}')
         assert_lse_close(to_np(lse), el, what=f'{name} merge, rank {rank}')
+
+
+def _fused_and_staged(call, nbytes, device):
+    """(one call: the split kernel makes the query operands, the prologue
+    stage and the attend + combine stages as two calls over one workspace:
+    the prologue kernel writes them)."""
+    from slimkv_amd import _lib
+    one = call(stages=_lib.STAGE_ALL, workspace=None)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    call(stages=_lib.STAGE_PROLOGUE, workspace=ws)
+    two = call(stages=_lib.STAGE_ATTEND | _lib.STAGE_COMBINE, workspace=ws)
+    torch.cuda.synchronize()
+    return one, two
+
+
+@pytest.mark.parametrize('rank,queries,segments', [(32, 1, 1), (16, 1, 1), (48, 1, 1), (32, 2, 1), (32, 1, 2),
+                                                   (48, 2, 2), (16, 2, 1)])
+def test_operands_made_in_the_split_kernel_equal_the_prologue(device, rank, queries, segments):
+    """With per-head bases and no K bias a full call makes the query operands
+    inside the split kernel (no prologue launch): bit-identical to the
+    prologue's operands consumed by the attend stage, over ragged lengths that
+    leave splits of 0 to 6 tiles, the two-query insertion step and latent rows
+    in two segments; and against the oracle."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=6, context=1600 + 132, tail=128, rank_k=rank, rank_v=rank, seed=91 + rank + queries,
+                       device=device)
+    if queries == 2:
+        gen = torch.Generator(device=device).manual_seed(92)
+        case.q = torch.randn(6, 2, 32, 128, generator=gen, device=device).to(torch.bfloat16)
+        case.q_positions = torch.tensor([[1732, 1733]] * 6, device=device)
+        case.cos, case.sin = rope_tables(1734, 128, 500000.0, device)
+    q_rot, k_rot = _rotated(case)
+    n = case.lat_k.shape[1]
+    lat_len = torch.tensor([n, 1, 17, 40, 100, n - 3], dtype=torch.int32, device=device)
+    lat = dict(lat_k=case.lat_k, lat_v=case.lat_v)
+    if segments == 2:
+        cut = n - 37
+        lat = dict(lat_k=case.lat_k[:, :cut], lat_v=case.lat_v[:, :cut], lat_k2=case.lat_k[:, cut:],
+                   lat_v2=case.lat_v[:, cut:])
+    common = dict(block_diagonal=True, lat_causal=queries == 2, q_positions=case.q_positions, cos=case.cos,
+                  sin=case.sin, lat_lengths=lat_len, lat_splits=24)
+
+    def call(stages, workspace):
+        return kernels.latent_decode(case.q, k_rot.transpose(1, 2), case.raw_v, lat['lat_k'], lat['lat_v'],
+                                     case.up_k, case.up_v, case.scale, lat_k2=lat.get('lat_k2'),
+                                     lat_v2=lat.get('lat_v2'), stages=stages, workspace=workspace, **common)
+    nbytes = kernels.latent_decode_workspace_bytes(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v,
+                                                   case.up_k, case.up_v, case.scale, **common)
+    one, two = _fused_and_staged(call, nbytes, device)
+    assert torch.equal(one[0], two[0]) and torch.equal(one[1], two[1])
+    for b in range(6):
+        m = int(lat_len[b])
+        eo, el = oa.latent_layer(to_np(q_rot[b:b + 1]), to_np(k_rot[b:b + 1]),
+                                 to_np(case.raw_v[b:b + 1].transpose(1, 2)), to_np(case.lat_k[b:b + 1, :m])[:, None],
+                                 to_np(case.lat_v[b:b + 1, :m])[:, None], to_np(case.up_k), to_np(case.up_v),
+                                 case.scale, case.kv_heads, lat_causal=queries == 2)
+        assert_close(to_np(one[0][b:b + 1].transpose(1, 2)), eo, what=f'sequence {b} ({m} beacons)')
+        assert_lse_close(to_np(one[1][b:b + 1]), el)
