@@ -244,6 +244,18 @@ def prefill(args):
                                'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                                'traffic': None, 'kernel': 'prefill_kernel', 'kernel_ms': round(kernel_s * 1e3, 3)},
                      attention_tflop=round(sum(flops) / 1e12, 4), replays=replays, clocks=clocks)
+    # LDS reads of prefill_kernel: each of a workgroup's four waves reads the
+    # whole 64-key K tile and V^T tile (2 x 64 x 128 x 2 B) per key tile it
+    # attends, so a workgroup reads 128 KB a tile; tiles per workgroup follow
+    # the causal visibility of its 128 query rows.
+    lds = lds_probe(torch, dev)
+    qblocks = (L + 127) // 128
+    tiles = sum(sum(-(-min(keys(w), (i + 1) * 128 + keys(w) - L) // 64) for i in range(qblocks)) for w in range(WINDOWS))
+    lds_bytes = tiles * B * HQ * 4 * 2 * 64 * D * 2
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    best_cu = max(lds['gbps_per_cu'].values())
+    result['lds'] = dict(lds, kernel_bytes=lds_bytes, kernel_gbps_per_cu=round(lds_bytes / kernel_s / 1e9 / cu, 1),
+                         bound_ms_at_probe_rate=round(lds_bytes / (best_cu * 1e9 * cu) * 1e3, 3))
     if not args.no_cpu:
         result['cpu_baseline'] = _prefill_cpu(torch, qs[1], work_k, work_v, keys(1), scale, pairs[1] * 4 * D * HQ * B)
     return result
@@ -586,13 +598,13 @@ def ceiling_probe(torch, dev, gib=4, reps=10):
         chunk.fill_(1)
     cu = torch.cuda.get_device_properties(dev).multi_processor_count
     sink = torch.empty(cu * 64 * 64, dtype=torch.int32, device=dev)
-    lib = _lib.lib()
+    lib = _lib.probe_lib()
     stream = _lib.stream_handle(dev)
     rates = {}
     for nt in (0, 1):
         for waves, depth in CEILING_CONFIGS:
             def launch():
-                _lib.check(lib.slimkv_probe_stream_read(ctypes.c_void_p(buf.data_ptr()), nbytes,
+                _lib.probe_check(lib.slimkv_probe_stream_read(ctypes.c_void_p(buf.data_ptr()), nbytes,
                                                         ctypes.c_void_p(sink.data_ptr()), sink.numel(), waves,
                                                         depth, nt, stream))
             for _ in range(3):
@@ -609,10 +621,42 @@ def ceiling_probe(torch, dev, gib=4, reps=10):
     return rates, best
 
 
+def lds_probe(torch, dev, iters=256, reps=5):
+    """LDS read rate of a CU (slimkv_probe_lds_read): 8- and 16-byte reads, one
+    and two 256-thread workgroups a CU.  {config: GB/s a CU} and, at the shader
+    clock the driver reports, bytes a clock a CU."""
+    import ctypes
+    from slimkv_amd import _lib
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(cu * 2 * 256, dtype=torch.int32, device=dev)
+    lib, stream = _lib.probe_lib(), _lib.stream_handle(dev)
+    rates = {}
+    for width in (8, 16):
+        for wgs in (1, 2):
+            def launch():
+                _lib.probe_check(lib.slimkv_probe_lds_read(ctypes.c_void_p(sink.data_ptr()), sink.numel(), wgs,
+                                                           iters, width, stream))
+            launch()
+            a, b = _events(torch)
+            a.record()
+            for _ in range(reps):
+                launch()
+            b.record()
+            torch.cuda.synchronize()
+            nbytes = cu * wgs * 256 * iters * 16 * width
+            rates[f'b{8 * width}_wg{wgs}'] = round(nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9 / cu, 1)
+    clocks = _replays_clocks() or {}
+    mhz = float(clocks['sclk'].rstrip('Mhz')) if clocks.get('sclk', '').rstrip('Mhz').isdigit() else None
+    per_clk = {k: round(v * 1e9 / (mhz * 1e6), 1) for k, v in rates.items()} if mhz else None
+    return {'gbps_per_cu': rates, 'bytes_per_clock_per_cu': per_clk, 'sclk_mhz': mhz,
+            'source': 'slimkv_probe_lds_read (libslimkv_probe.so), conflict-free consecutive reads'}
+
+
 def ceiling(args):
     """The HBM read ceiling of this GPU: a grid-stride stream of 16-byte loads
     (slimkv_probe_stream_read) over 4 GiB, the best of several resident-wave /
-    loads-in-flight configurations, plain and non-temporal."""
+    loads-in-flight configurations, plain and non-temporal; and the LDS read
+    rate of a CU (slimkv_probe_lds_read)."""
     import torch
     dev = torch.device('cuda:0')
     t0 = time.perf_counter()
@@ -622,7 +666,8 @@ def ceiling(args):
                    'u8', {'workload': 'stream read of a 4 GiB buffer, 16-byte loads',
                           'configs': [list(c) for c in CEILING_CONFIGS]},
                    hbm_frac=round(best['plain'] / HBM_PEAK_GBPS, 4), nt_gbps=best['nt'],
-                   nt_frac=round(best['nt'] / HBM_PEAK_GBPS, 4), rates=rates, clocks=_replays_clocks())
+                   nt_frac=round(best['nt'] / HBM_PEAK_GBPS, 4), rates=rates, lds=lds_probe(torch, dev),
+                   clocks=_replays_clocks())
 
 
 def _replays_clocks():

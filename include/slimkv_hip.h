@@ -594,18 +594,8 @@ typedef struct slimkv_raw_pages_args {
 
 int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream);
 
-/* ------------------------------------------------------------------------
- * HBM read-bandwidth ceiling probe (measurement only; no counterpart in the
- * reference).  Reads `bytes` of `src` once with 16-byte loads, `depth` (1, 2,
- * 4 or 8) in flight per thread, grid-stride over the whole buffer, with
- * `waves_per_cu` (multiple of 4, 4..64) resident waves per CU, plain or
- * non-temporal loads; folds the data into `sink`, which must hold
- * CUs * waves_per_cu * 64 words (checked).  Times taken around it
- * give the read rate a stream of this GPU reaches, the ceiling the HBM-bound
- * kernels are compared with beside the 8 TB/s peak.
- * ---------------------------------------------------------------------- */
-int slimkv_probe_stream_read(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_words,
-                             int32_t waves_per_cu, int32_t depth, int32_t non_temporal, void* stream);
+/* The measurement probes (HBM and LDS read ceilings) are in
+ * libslimkv_probe.so, declared in slimkv_probe.h. */
 
 #ifdef __cplusplus
 }

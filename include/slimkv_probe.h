@@ -1,0 +1,36 @@
+/* Measurement probes of libslimkv_probe.so: hardware ceilings that measured
+ * kernel rates are read against.  Not part of the serving library
+ * (libslimkv_hip.so) and without counterpart in the reference.  Return 0, or
+ * a negative code with slimkv_probe_last_error() describing it. */
+#ifndef SLIMKV_PROBE_H
+#define SLIMKV_PROBE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* slimkv_probe_last_error(void);
+
+/* HBM read rate: a grid-stride stream of 16-byte loads over `bytes` of src
+ * (16-byte aligned), `depth` (1, 2, 4, 8) loads in flight a thread,
+ * waves_per_cu (multiple of 4 in [4, 64]) resident waves a CU, plain or
+ * non-temporal loads; one folded word a thread to sink (at least
+ * grid * 256 words, grid = CUs * waves_per_cu / 4). */
+int slimkv_probe_stream_read(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_words,
+                             int32_t waves_per_cu, int32_t depth, int32_t non_temporal, void* stream);
+
+/* LDS read rate of a CU: workgroups_per_cu (1 or 2) workgroups of 256
+ * threads a CU, each with 64 KB of LDS, read it `iters` x 16 times a lane,
+ * `width` (8 or 16) bytes a read, conflict free; one word a thread to sink
+ * (at least CUs * workgroups_per_cu * 256 words).  Bytes read =
+ * CUs * workgroups_per_cu * 256 * iters * 16 * width. */
+int slimkv_probe_lds_read(uint32_t* sink, int64_t sink_words, int32_t workgroups_per_cu, int32_t iters,
+                          int32_t width, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

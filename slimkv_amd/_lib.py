@@ -238,7 +238,6 @@ SIGNATURES = {
                                                     ctypes.c_size_t, c_ptr]),
     'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
-    'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
 }
 
 ABI_VERSION = 11
@@ -270,6 +269,34 @@ def library_identity():
     except ValueError:
         shown = str(path)
     return {'path': shown, 'sha256': digest, 'override': 'SLIMKV_HIP_LIBRARY' in os.environ}
+
+
+PROBE_LIBRARY = LIBRARY.with_name('libslimkv_probe.so')
+
+PROBE_SIGNATURES = {
+    'slimkv_probe_last_error': (ctypes.c_char_p, []),
+    'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
+    'slimkv_probe_lds_read': (ctypes.c_int, [c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
+}
+
+
+@lru_cache(None)
+def probe_lib():
+    """The measurement probes (include/slimkv_probe.h), a library of their own
+    beside the serving one."""
+    if not PROBE_LIBRARY.exists():
+        raise ImportError(f'{PROBE_LIBRARY} is missing: build it with `python -m slimkv_amd.build`')
+    handle = ctypes.CDLL(str(PROBE_LIBRARY))
+    for name, (restype, argtypes) in PROBE_SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return handle
+
+
+def probe_check(code):
+    if code != 0:
+        raise SlimKVError(f'probe error {code}: {probe_lib().slimkv_probe_last_error().decode(errors="replace")}')
 
 
 @lru_cache(None)

@@ -14,7 +14,10 @@ PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / 'csrc'
 LIBRARY = PACKAGE / 'libslimkv_hip.so'
 SOURCES = ['attention.hip', 'rope.hip', 'recon.hip', 'paged.hip', 'prefill.hip', 'down.hip', 'project.hip',
-           'eager.hip', 'probe.hip']
+           'eager.hip']
+# measurement probes: a library of their own (include/slimkv_probe.h)
+PROBE_LIBRARY = PACKAGE / 'libslimkv_probe.so'
+PROBE_SOURCES = ['probe.hip']
 
 FLAGS = [
     '--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared',
@@ -36,9 +39,15 @@ def sources():
 
 
 def build(verbose=False, extra=()):
-    """Compile every HIP source into one shared library; always recompiles."""
-    tmp = LIBRARY.with_suffix('.so.tmp')
-    cmd = [hipcc(), *FLAGS, *extra, '-o', str(tmp), *map(str, sources())]
+    """Compile the serving library and the probe library; always recompiles."""
+    _build_one(LIBRARY, sources(), verbose, extra)
+    _build_one(PROBE_LIBRARY, [CSRC / name for name in PROBE_SOURCES], verbose, extra)
+    return LIBRARY
+
+
+def _build_one(library, srcs, verbose, extra):
+    tmp = library.with_suffix('.so.tmp')
+    cmd = [hipcc(), *FLAGS, *extra, '-o', str(tmp), *map(str, srcs)]
     if verbose:
         print(' '.join(cmd), flush=True)
     result = subprocess.run(cmd, cwd=str(CSRC), capture_output=True, text=True)
@@ -48,8 +57,8 @@ def build(verbose=False, extra=()):
         raise RuntimeError(f'hipcc failed ({result.returncode}):\n{stderr}')
     if verbose and stderr.strip():
         print(stderr, file=sys.stderr)
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, library)
+    return library
 
 
 if __name__ == '__main__':

@@ -1,13 +1,53 @@
-// HBM read-bandwidth ceiling probe (a measurement kernel with no counterpart
-// in the reference).  Every thread streams 16-byte loads of a buffer, `depth`
-// of them in flight, over a grid-stride walk of the whole buffer (all waves
-// sweep one address window together, the friendliest pattern for the DRAM
-// pages), and writes one folded word so no load is dropped.  Plain or
-// non-temporal loads; the grid is `waves_per_cu` resident waves per CU.
+// Measurement probes, built as libslimkv_probe.so beside the serving library
+// (no counterpart in the reference; nothing on the attention path calls
+// them).  Each reports a hardware ceiling the kernels' measured rates are read
+// against:
+//
+// * slimkv_probe_stream_read: the HBM read rate.  Every thread streams
+//   16-byte loads of a buffer, `depth` of them in flight, over a grid-stride
+//   walk of the whole buffer (all waves sweep one address window together,
+//   the friendliest pattern for the DRAM pages), and writes one folded word so
+//   no load is dropped.  Plain or non-temporal loads; the grid is
+//   `waves_per_cu` resident waves per CU.
+// * slimkv_probe_lds_read: the LDS read rate of a CU.  Workgroups of four
+//   waves fill 64 KB of LDS, then every lane reads `width` bytes a read
+//   (ds_read_b64 / ds_read_b128) at consecutive addresses -- a wave reads a
+//   contiguous 512 B or 1 KB, bank-conflict free, as the prefill kernel's
+//   operand reads are laid out -- `iters` passes of 16 reads, and folds the
+//   words into one per lane.  Bytes read = grid threads x iters x 16 x width.
 
-#include "common.hpp"
+#include <hip/hip_runtime.h>
+#include <stdint.h>
 
-namespace slimkv {
+#include <string>
+
+#include "../../include/slimkv_probe.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+thread_local std::string g_probe_error;
+
+int probe_fail(const char* msg) {
+    g_probe_error = msg;
+    return -1;
+}
+
+int probe_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return 0;
+    g_probe_error = std::string(what) + ": " + hipGetErrorString(e);
+    return -4;
+}
+
+int cu_count() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                hipSuccess)
+        return 0;
+    return cus;
+}
 
 template <int DEPTH, bool NT>
 __global__ void __launch_bounds__(256) stream_read_kernel(const u32x4* __restrict__ src, int64_t n16,
@@ -36,18 +76,49 @@ hipError_t launch_stream_read(const u32x4* src, int64_t n16, uint32_t* sink, int
     return hipGetLastError();
 }
 
-}  // namespace slimkv
+constexpr int kLdsWords = 16384;                       // 64 KB of 32-bit words
 
-using namespace slimkv;
+// Every read address stays inside the 64 KB buffer (the index is masked).
+template <int WIDTH>
+__global__ void __launch_bounds__(256) lds_read_kernel(int iters, uint32_t* __restrict__ sink) {
+    __shared__ __attribute__((aligned(16))) uint32_t buf[kLdsWords];
+    for (int i = threadIdx.x; i < kLdsWords; i += blockDim.x) buf[i] = i * 2654435761u;
+    __syncthreads();
+    constexpr int W = WIDTH / 4;                       // words a read
+    constexpr int kReads = kLdsWords / W;              // reads a pass of the buffer holds
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t acc = 0;
+    int r = (wave * 16 * 64 + lane) % kReads;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int idx = ((r + 64 * u) % kReads) * W;
+            if constexpr (WIDTH == 16) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(buf + idx);
+                acc ^= v.x ^ v.y ^ v.z ^ v.w;
+            } else {
+                const u32x2 v = *reinterpret_cast<const u32x2*>(buf + idx);
+                acc ^= v.x ^ v.y;
+            }
+        }
+        r = (r + 64 * 16) % kReads;
+    }
+    sink[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" const char* slimkv_probe_last_error(void) { return g_probe_error.c_str(); }
 
 extern "C" int slimkv_probe_stream_read(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_words,
                                         int32_t waves_per_cu, int32_t depth, int32_t non_temporal, void* stream) {
     if (!src || !sink || bytes < 16 || (bytes & 15) || (reinterpret_cast<uintptr_t>(src) & 15))
-        return fail(SLIMKV_EINVAL, "probe needs a 16-byte aligned buffer of a multiple of 16 bytes");
+        return probe_fail("probe needs a 16-byte aligned buffer of a multiple of 16 bytes");
     if (waves_per_cu < 4 || waves_per_cu % 4 || waves_per_cu > 64)
-        return fail(SLIMKV_EINVAL, "waves_per_cu must be a multiple of 4 in [4, 64]");
-    const int grid = device_cu_count() * waves_per_cu / 4;
-    if (sink_words < (int64_t)grid * 256) return fail(SLIMKV_EINVAL, "sink too small (grid * 256 words)");
+        return probe_fail("waves_per_cu must be a multiple of 4 in [4, 64]");
+    const int grid = cu_count() * waves_per_cu / 4;
+    if (grid <= 0) return probe_fail("no device");
+    if (sink_words < (int64_t)grid * 256) return probe_fail("sink too small (grid * 256 words)");
     const int64_t n16 = bytes / 16;
     const u32x4* s = static_cast<const u32x4*>(src);
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -58,7 +129,20 @@ extern "C" int slimkv_probe_stream_read(const void* src, int64_t bytes, uint32_t
         case 2: e = launch_stream_read<2>(s, n16, sink, grid, nt, st); break;
         case 4: e = launch_stream_read<4>(s, n16, sink, grid, nt, st); break;
         case 8: e = launch_stream_read<8>(s, n16, sink, grid, nt, st); break;
-        default: return fail(SLIMKV_EINVAL, "depth must be 1, 2, 4 or 8");
+        default: return probe_fail("depth must be 1, 2, 4 or 8");
     }
-    return check_hip(e, "stream read probe launch");
+    return probe_hip(e, "stream read probe launch");
+}
+
+extern "C" int slimkv_probe_lds_read(uint32_t* sink, int64_t sink_words, int32_t workgroups_per_cu, int32_t iters,
+                                     int32_t width, void* stream) {
+    if (!sink || workgroups_per_cu < 1 || workgroups_per_cu > 2 || iters < 1 || (width != 8 && width != 16))
+        return probe_fail("lds probe: 1 or 2 workgroups per CU, iters >= 1, width 8 or 16");
+    const int grid = cu_count() * workgroups_per_cu;
+    if (grid <= 0) return probe_fail("no device");
+    if (sink_words < (int64_t)grid * 256) return probe_fail("sink too small (grid * 256 words)");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (width == 16) hipLaunchKernelGGL(lds_read_kernel<16>, dim3(grid), dim3(256), 0, st, iters, sink);
+    else hipLaunchKernelGGL(lds_read_kernel<8>, dim3(grid), dim3(256), 0, st, iters, sink);
+    return probe_hip(hipGetLastError(), "lds read probe launch");
 }

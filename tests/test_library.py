@@ -9,12 +9,13 @@ import pytest
 ROOT = Path(__file__).resolve().parents[1]
 
 
-def declared_symbols():
-    names = set()
-    for header in (ROOT / 'include').glob('*.h'):
-        text = re.sub(r'/\*.*?\*/', '', header.read_text(), flags=re.S)
-        names.update(re.findall(r'\b(slimkv_[a-z0-9_]+)\s*\(', text))
-    return sorted(names)
+def declared_symbols(header='slimkv_hip.h'):
+    text = re.sub(r'/\*.*?\*/', '', (ROOT / 'include' / header).read_text(), flags=re.S)
+    return sorted(set(re.findall(r'\b(slimkv_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_every_header_is_checked():
+    assert sorted(p.name for p in (ROOT / 'include').glob('*.h')) == ['slimkv_hip.h', 'slimkv_probe.h']
 
 
 def test_header_declares_entry_points():
@@ -28,6 +29,17 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(handle, name), name
         assert name in _lib.SIGNATURES, f'{name} has no ctypes signature'
+
+
+def test_probe_library_exports_its_symbols_and_the_serving_library_none():
+    """The measurement probes live in libslimkv_probe.so only."""
+    from slimkv_amd import _lib
+    probes = declared_symbols('slimkv_probe.h')
+    assert probes == sorted(_lib.PROBE_SIGNATURES)
+    handle = _lib.probe_lib()
+    for name in probes:
+        assert hasattr(handle, name), name
+        assert not hasattr(_lib.lib(), name), f'{name} is exported by the serving library'
 
 
 def STRUCTS(_lib):
