@@ -40,14 +40,15 @@ RAW = SINKS + TAIL + 1              # sinks + tail + current token
 RANKS = (16, 32, 48)
 
 
-# HBM bytes per launch of the split kernel of a rank-r layer, from two rocprofv3
-# --pmc passes (FETCH_SIZE, then WRITE_SIZE; KiB a dispatch) over
+# HBM bytes per launch of the split kernel (query operands made in the
+# kernel) of a rank-r layer, from two rocprofv3 --pmc passes (FETCH_SIZE, then
+# WRITE_SIZE; KiB a dispatch) over
 # `bench.py --layers 5 --steps 2 --warmup 1 --no-cpu --no-graph`, scaled by the
 # same counters on the run's ceiling probe (its 4 GiB stream reads read
 # FETCH_SIZE = half the bytes read; its 256 MiB fills WRITE_SIZE = the bytes
 # written): (2 x fetch + write) x 1024.
-SPLIT_TRAFFIC_BYTES = {32: (2 * 70_463.75 + 2_884.0) * 1024, 16: (2 * 37_631.25 + 2_884.0) * 1024,
-                       48: (2 * 107_059.75 + 3_140.25) * 1024}
+SPLIT_TRAFFIC_BYTES = {32: (2 * 70_840.53 + 2_628.01) * 1024, 16: (2 * 37_944.51 + 2_628.01) * 1024,
+                       48: (2 * 107_667.30 + 3_140.01) * 1024}
 SPLIT_TRAFFIC_BYTES = {r: int(v) for r, v in SPLIT_TRAFFIC_BYTES.items()}
 TRAFFIC_SOURCE = ('rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, split_kernel, scaled by the ceiling probe\'s '
                   '4 GiB stream reads and 256 MiB fills')
