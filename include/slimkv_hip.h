@@ -564,6 +564,7 @@ typedef struct slimkv_beacon_pages_args {
     int64_t slots, key_rank, value_rank, sink_elements;
     int32_t to_pages;
     int32_t* status;   /* optional: SLIMKV_STATUS_BAD_PAGE on an index error */
+    const int64_t* starts;   /* optional [batch]: request b's rows start at start + starts[b] */
 } slimkv_beacon_pages_args;
 
 int slimkv_beacon_pages(const slimkv_beacon_pages_args* a, void* stream);
@@ -590,6 +591,7 @@ typedef struct slimkv_raw_pages_args {
     int64_t batch, start, count, block_size, kv_heads, head_dim;
     int32_t to_pages;
     int32_t* status;   /* optional: SLIMKV_STATUS_BAD_PAGE on an index error */
+    const int64_t* starts;   /* optional [batch]: request b's positions start at start + starts[b] */
 } slimkv_raw_pages_args;
 
 int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream);

@@ -187,7 +187,7 @@ BeaconPagesArgs = _struct('slimkv_beacon_pages_args', [
     ('lengths', c_ptr),
     *_i64s('batch', 'start', 'count', 'slots', 'key_rank', 'value_rank', 'sink_elements'),
     ('to_pages', c_i32),
-    ('status', c_ptr),
+    ('status', c_ptr), ('starts', c_ptr),
 ])
 
 RawPagesArgs = _struct('slimkv_raw_pages_args', [
@@ -198,7 +198,7 @@ RawPagesArgs = _struct('slimkv_raw_pages_args', [
     ('lengths', c_ptr),
     *_i64s('batch', 'start', 'count', 'block_size', 'kv_heads', 'head_dim'),
     ('to_pages', c_i32),
-    ('status', c_ptr),
+    ('status', c_ptr), ('starts', c_ptr),
 ])
 
 # name -> (restype, argtypes)
@@ -240,7 +240,7 @@ SIGNATURES = {
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20

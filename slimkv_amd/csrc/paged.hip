@@ -7,6 +7,8 @@
 // Raw pages (paged_cache.py:102-127): [blocks, block_size, 2, Hkv, D]; token t
 // lives in block table[t / block_size] at row t % block_size.  Table entries
 // follow torch's indexing rules; an index error moves nothing and is reported.
+// An optional per-request `starts` offsets each request's first row (a batch
+// of requests at different positions, such as one decode step's appends).
 //
 // These copies are HBM-bound byte moves: one thread moves one 16-byte piece
 // (VEC = 8 bf16) whenever every row start and width allows it, else one
@@ -36,10 +38,10 @@ beacon_pages_kernel(slimkv_beacon_pages_args a) {
     if (gid >= a.count * per_row) return;
     const int64_t r = gid / per_row;
     const int64_t c = (gid % per_row) * VEC;           // column inside [K | V]
-    const int64_t logical = a.start + r;
+    const int64_t logical = a.start + (a.starts ? a.starts[b] : 0) + r;
     if (a.lengths && logical >= a.lengths[b]) return;
-    const int64_t col = logical / a.slots;
-    const int64_t page = col < a.t_cols ? table_page(a.table[b * a.t_sb + col], a.num_pages) : -1;
+    const int64_t col = logical >= 0 ? logical / a.slots : -1;     // a negative position is an index error
+    const int64_t page = col >= 0 && col < a.t_cols ? table_page(a.table[b * a.t_sb + col], a.num_pages) : -1;
     if (page < 0) {
         report_bad_page(a.status);
         return;
@@ -60,10 +62,10 @@ __global__ void __launch_bounds__(256)
 raw_pages_kernel(slimkv_raw_pages_args a) {
     const int64_t b = blockIdx.y;
     const int64_t r = blockIdx.x;
-    const int64_t t = a.start + r;
+    const int64_t t = a.start + (a.starts ? a.starts[b] : 0) + r;
     if (a.lengths && t >= a.lengths[b]) return;
-    const int64_t col = t / a.block_size;
-    const int64_t block = col < a.t_cols ? table_page(a.table[b * a.t_sb + col], a.num_blocks) : -1;
+    const int64_t col = t >= 0 ? t / a.block_size : -1;             // a negative position is an index error
+    const int64_t block = col >= 0 && col < a.t_cols ? table_page(a.table[b * a.t_sb + col], a.num_blocks) : -1;
     if (block < 0) {
         if (threadIdx.x == 0) report_bad_page(a.status);
         return;

@@ -738,14 +738,25 @@ def _lengths(lengths, batch, device):
     return lengths
 
 
+def _starts(starts, batch, device):
+    if starts is None:
+        return None
+    starts = starts.to(device=device, dtype=torch.int64).contiguous()
+    if starts.shape != (batch,):
+        raise ValueError('starts must be [batch]')
+    return starts
+
+
 def beacon_pages(pages, table, dense_k, dense_v, *, slots, key_rank, value_rank, sink_elements, start, count,
-                 to_pages, lengths=None, status=None):
+                 to_pages, lengths=None, status=None, starts=None):
     """Copy beacon latents between pages [num_pages, >=page_elements] and dense
     rows dense_k [B, count, key_rank], dense_v [B, count, value_rank]
     (slimkv/vllm_plugin/paged_cache.py:60-87).  table: [B, T] or [T] int64,
     entries under torch's indexing rules.  A row whose entry lies outside the
     pool moves nothing; without a caller `status` word that raises IndexError
-    here (one host synchronisation), with one it is left in `status`."""
+    here (one host synchronisation), with one it is left in `status`.
+    `starts` (device int64 [B], optional): request b's dense row r is beacon
+    start + starts[b] + r (rows at or past lengths[b] are skipped)."""
     _need_device(pages, dense_k, dense_v)
     _need_bf16(pages, dense_k, dense_v)
     if pages.dim() != 2 or pages.stride(1) != 1:
@@ -756,6 +767,7 @@ def beacon_pages(pages, table, dense_k, dense_v, *, slots, key_rank, value_rank,
         if t.dim() != 3 or t.shape != (B, count, w) or t.stride(2) != 1:
             raise ValueError(f'dense latents must be [{B}, {count}, {w}] with contiguous rows')
     lengths = _lengths(lengths, B, pages.device)
+    starts = _starts(starts, B, pages.device)
     status, owned = _status_word(status, pages.device)
     a = _lib.BeaconPagesArgs(
         pages=_ptr(pages), num_pages=pages.shape[0], page_stride=pages.stride(0),
@@ -763,16 +775,18 @@ def beacon_pages(pages, table, dense_k, dense_v, *, slots, key_rank, value_rank,
         dense_k=_ptr(dense_k), dk_sb=dense_k.stride(0), dk_sn=dense_k.stride(1),
         dense_v=_ptr(dense_v), dv_sb=dense_v.stride(0), dv_sn=dense_v.stride(1),
         lengths=_ptr(lengths), batch=B, start=start, count=count, slots=slots, key_rank=key_rank,
-        value_rank=value_rank, sink_elements=sink_elements, to_pages=int(bool(to_pages)), status=_ptr(status))
+        value_rank=value_rank, sink_elements=sink_elements, to_pages=int(bool(to_pages)), status=_ptr(status),
+        starts=_ptr(starts))
     check(lib().slimkv_beacon_pages(ctypes.byref(a), _lib.stream_handle(pages.device)))
     if owned:
         check_status(status)
 
 
-def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths=None, status=None):
+def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths=None, status=None, starts=None):
     """Copy raw K/V between pages [blocks, block_size, 2, Hkv, D] and dense
     dense_k/dense_v [B, Hkv, count, D] (slimkv/vllm_plugin/paged_cache.py:102-127).
-    Table entries and `status` as beacon_pages."""
+    Table entries, `status` and `starts` (request b's dense row r is position
+    start + starts[b] + r) as beacon_pages."""
     _need_device(pages, dense_k, dense_v)
     _need_bf16(pages, dense_k, dense_v)
     if pages.dim() != 5 or pages.shape[2] != 2 or pages.stride(4) != 1:
@@ -784,6 +798,7 @@ def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths
         if t.dim() != 4 or t.shape != (B, H, count, D) or t.stride(3) != 1:
             raise ValueError(f'dense K/V must be [{B}, {H}, {count}, {D}] with contiguous rows')
     lengths = _lengths(lengths, B, pages.device)
+    starts = _starts(starts, B, pages.device)
     status, owned = _status_word(status, pages.device)
     a = _lib.RawPagesArgs(
         pages=_ptr(pages), num_blocks=pages.shape[0], p_sblk=pages.stride(0), p_stok=pages.stride(1),
@@ -792,7 +807,7 @@ def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths
         dense_k=_ptr(dense_k), dk_sb=dense_k.stride(0), dk_sh=dense_k.stride(1), dk_sn=dense_k.stride(2),
         dense_v=_ptr(dense_v), dv_sb=dense_v.stride(0), dv_sh=dense_v.stride(1), dv_sn=dense_v.stride(2),
         lengths=_ptr(lengths), batch=B, start=start, count=count, block_size=block_size, kv_heads=H,
-        head_dim=D, to_pages=int(bool(to_pages)), status=_ptr(status))
+        head_dim=D, to_pages=int(bool(to_pages)), status=_ptr(status), starts=_ptr(starts))
     check(lib().slimkv_raw_pages(ctypes.byref(a), _lib.stream_handle(pages.device)))
     if owned:
         check_status(status)
