@@ -153,13 +153,16 @@ def _result(metric, value, unit, args, seconds, dtype, config, **extra):
 
 def prefill(args):
     """The window prefill step as prefill_forward runs it over a prefill
-    history (slimkv_amd.prefill.PrefillHistory): per window the K/V rows of
-    the window are written after [sink | up(history)] in append-only buffers,
-    the window's beacon rows are down-projected and rebuilt as up(latent), the
-    prefill RoPE rotates the queries and every key but the beacons', the
-    causal attention runs over [sink | history | window], and the window's 256
-    new beacons are rebuilt onto the history.  The q/k/v projections of the
-    window (nn.Linear layers of the model) stand as given rows."""
+    history (slimkv_amd.prefill.PrefillHistory): per window the window's
+    beacon rows are down-projected and rebuilt as up(latent) in the
+    projection's K/V rows, the V rows are written after [sink | up(history)]
+    in the append-only store, the prefill RoPE rotates the window's keys
+    (beacon keys copied unrotated) into the store after the held keys, the
+    causal attention rotates its queries as it loads them and runs over
+    [sink | history | window], and the window's 256 new beacons are rebuilt
+    onto the history.  The q/k/v
+    projections of the window (nn.Linear layers of the model) stand as given
+    rows, copied into the projection's output buffer each window."""
     import torch
     from slimkv_amd import kernels
     from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
@@ -173,8 +176,9 @@ def prefill(args):
     down = [block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).t().contiguous().to(dev, torch.bfloat16)
             for _ in range(2)]                                  # per-head K_full[128] -> r bases [R, Hkv*D]
     n_max = S + NB * (WINDOWS - 1) + L
-    work_k = torch.zeros(B, n_max, HKV, D, dtype=torch.bfloat16, device=dev)
+    work_k = torch.zeros(B, n_max, HKV, D, dtype=torch.bfloat16, device=dev)   # rotated keys as attended
     work_v = torch.zeros_like(work_k)
+    proj_k = torch.zeros(B, L, HKV, D, dtype=torch.bfloat16, device=dev)      # the window's K projection
     latents = [torch.zeros(B, NB * WINDOWS, R, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     qs = [rnd(B, L, HQ, D) for _ in range(WINDOWS)]
     cur = [(rnd(B, L, HKV, D), rnd(B, L, HKV, D)) for _ in range(WINDOWS)]
@@ -193,19 +197,18 @@ def prefill(args):
     def window(w, timed=None):
         n = keys(w)
         base = 0 if w == 0 else S + NB * w           # the window follows [sink | history]
-        work_k[:, base:base + L].copy_(cur[w][0])
+        proj_k.copy_(cur[w][0])
         work_v[:, base:base + L].copy_(cur[w][1])
-        for j, dst in ((0, work_k), (1, work_v)):
+        for j, dst in ((0, proj_k), (1, work_v[:, base:base + L])):
             lat = latents[j][:, NB * w:NB * (w + 1)]
             kernels.down_project(cur[w][j].view(B, L, HKV * D), down[j], beacon_rows, blocks=HKV, out=lat)
-            kernels.reconstruct(lat, up[j], kv_heads=HKV, out=dst[:, base:base + L], dst_rows=beacon_rows,
-                                block_diagonal=True)
-        q_rot, k_rot = kernels.prefill_rope(qs[w].transpose(1, 2), work_k[:, :n].transpose(1, 2), cos, sin,
-                                            positions[:, :n], roles, S if w else 0)
+            kernels.reconstruct(lat, up[j], kv_heads=HKV, out=dst, dst_rows=beacon_rows, block_diagonal=True)
+        kernels.rope_keys(proj_k.transpose(1, 2), cos, sin, positions[:, base:n], roles, 0,
+                          out_k=work_k[:, base:n].transpose(1, 2))
         if timed:
             timed[0].record()
-        kernels.prefill_attention(q_rot.transpose(1, 2), k_rot.transpose(1, 2), work_v[:, :n], scale, True,
-                                  out=out, lse=lse)
+        kernels.prefill_attention(qs[w], work_k[:, :n], work_v[:, :n], scale, True, out=out, lse=lse,
+                                  q_positions=positions[:, base:n], cos=cos, sin=sin)
         if timed:
             timed[1].record()
         # the window's new beacons onto the history (after the sink of window 0)
@@ -238,8 +241,9 @@ def prefill(args):
                      {'workload': 'window prefill, 8192-token prompt, t4, per-head rank 32', 'batch': B,
                       'window': WIN, 'beacons_per_window': NB, 'windows': WINDOWS, 'q_heads': HQ, 'kv_heads': HKV,
                       'head_dim': D, 'sinks': S,
-                      'step': 'window K/V writes, beacon down-projection and rebuild, prefill RoPE, attention, '
-                              'the 256 new beacons rebuilt onto an append-only history'},
+                      'step': 'window K/V writes, beacon down-projection and rebuild, prefill RoPE of the window '
+                              'keys into the kept key set, attention (query RoPE inside), the 256 new beacons '
+                              'rebuilt onto an append-only history'},
                      roofline={'bound': 'mfma', 'achieved': round(achieved, 1), 'peak': MFMA_BF16_PEAK_TFLOPS,
                                'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                                'traffic': None, 'kernel': 'prefill_kernel', 'kernel_ms': round(kernel_s * 1e3, 3)},

@@ -341,7 +341,9 @@ int slimkv_rope_decode(const slimkv_rope_decode_args* a, void* stream);
  * and prefill_rope_kernel (slimkv/llama3/prefill_kernels.py:7-53).
  * Query slot s uses positions[b*pos_sb + Nk - Lq + s]; key slot s uses
  * positions[b*pos_sb + s] unless it is a beacon: s in [sink, Nk-role_len) or
- * roles[s - (Nk-role_len)] in {1, 2}, which is copied unchanged.
+ * roles[s - (Nk-role_len)] in {1, 2}, which is copied unchanged.  queries = 0
+ * (q and out_q may then be NULL) rotates the keys alone, for callers whose
+ * attention rotates its queries itself (slimkv_prefill_attention).
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_prefill_rope_args {
     const void* q; int64_t q_sb, q_sh, q_ss;
@@ -473,6 +475,14 @@ int slimkv_decode_qkv(const slimkv_decode_qkv_args* a, void* stream);
  * that sees no key gets output 0 and LSE -inf.  Strides are multiples of 8
  * elements, tensors 16-byte aligned, k_sn and v_sn in [128, 2^23) (SLIMKV_EUNSUP
  * otherwise), scale > 0.
+ * Optional query RoPE (rope_pairs non-NULL): each query row is rotated as it
+ * is loaded, at q_positions[b * qpos_sb + i] clamped into [0, rope_rows)
+ * (qpos_sb 0: the same positions for every batch entry), with the
+ * reference's bf16 steps (the prefill RoPE of _apply_rotary_with_beacon,
+ * modeling_llama.py:1108-1216): rope_pairs [rope_rows, 128] from
+ * slimkv_prepare_rope_pairs of the cos/sin tables, rope_repeats = 1 when every
+ * row is its first half twice.  The same bits as rotating q with
+ * slimkv_prefill_rope first.
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_prefill_attention_args {
     const void* q; int64_t q_sb, q_sl, q_sh;
@@ -484,6 +494,9 @@ typedef struct slimkv_prefill_attention_args {
     int64_t batch, queries, heads, kv_heads, keys, head_dim;
     double scale;
     int32_t causal;
+    const uint32_t* rope_pairs; int64_t rope_rows;   /* optional query RoPE */
+    int32_t rope_repeats;
+    const int64_t* q_positions; int64_t qpos_sb;
 } slimkv_prefill_attention_args;
 
 int slimkv_prefill_attention(const slimkv_prefill_attention_args* a, void* stream);

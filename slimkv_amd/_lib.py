@@ -161,6 +161,9 @@ PrefillAttentionArgs = _struct('slimkv_prefill_attention_args', [
     *_i64s('batch', 'queries', 'heads', 'kv_heads', 'keys', 'head_dim'),
     ('scale', c_f64),
     ('causal', c_i32),
+    ('rope_pairs', c_ptr), ('rope_rows', c_i64),
+    ('rope_repeats', c_i32),
+    ('q_positions', c_ptr), ('qpos_sb', c_i64),
 ])
 
 DownProjectArgs = _struct('slimkv_down_project_args', [
@@ -240,7 +243,7 @@ SIGNATURES = {
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20

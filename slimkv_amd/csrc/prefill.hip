@@ -54,9 +54,57 @@ struct PrefillParams {
     int B, Lq, Hq, Hk, Nk, causal;
     int qblocks;
     float scale_log2;
+    const uint32_t* pairs; int64_t rope_rows; int repeats;    // query RoPE when pairs != nullptr
+    const int64_t* q_pos; int64_t qpos_sb;
 };
 
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16(lo, hi); }
+
+// Query RoPE in the operand registers: lane pieces kk and kk + 2 hold d and
+// d + 64 (d = 32 kk + 8 grp + e), rotate_half's partners.  The reference's bf16
+// steps, element by element: bf16(bf16(x * bf16(c)) + bf16(r * bf16(s))) with
+// r = -x[d + 64] below the half and x[d - 64] above it; (bf16 c | bf16 s)
+// pairs from the table prepared once (slimkv_prepare_rope_pairs), the upper
+// half read from the lower one where every row repeats its first half.
+struct QPairs {
+    u32x4 p[4][2];          // pairs of piece kk: d = 32 kk + 8 grp .. + 7
+};
+
+__device__ __forceinline__ void load_q_pairs(QPairs& t, const uint32_t* row, int grp, int repeats) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const int d = 32 * kk + 8 * grp;
+        const int c = (kk >= 2 && repeats) ? d - 64 : d;
+        t.p[kk][0] = *reinterpret_cast<const u32x4*>(row + c);
+        t.p[kk][1] = *reinterpret_cast<const u32x4*>(row + c + 4);
+    }
+}
+
+__device__ __forceinline__ void rope_q_operand(u32x4 (&x)[4], const QPairs& t) {
+    u32x4 y[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const u32x4& own = x[kk];
+        const u32x4& partner = x[kk ^ 2];
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float sum[2];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const uint32_t cs = t.p[kk][e >> 1][2 * (e & 1) + hb];
+                const float v = hb ? hi_bf16(own[e]) : lo_bf16(own[e]);
+                float r = hb ? hi_bf16(partner[e]) : lo_bf16(partner[e]);
+                if (kk < 2) r = -r;
+                sum[hb] = round_bf16_hw(v * lo_bf16(cs)) + round_bf16_hw(r * hi_bf16(cs));
+            }
+            o[e] = pack_bf16(sum[0], sum[1]);
+        }
+        y[kk] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) x[kk] = y[kk];
+}
 
 // V^T keeps, per 32-key step, the keys a lane group reads together side by
 // side: key 16h + 4g + j of the step sits at 8g + 4h + j, so the eight keys of
@@ -159,6 +207,16 @@ prefill_kernel(PrefillParams p) {
     if (p.causal) k_end = min(n, min(qb * kQRows + kQRows, p.Lq) + shift);
     const int ntiles = k_end > 0 ? (k_end + kKeys - 1) / kKeys : 0;
 
+    // Query RoPE: the rows' positions first, their table pairs once the
+    // first K/V tile's loads are issued, the rotation before the tile loop.
+    int64_t qpos[2] = {0, 0};
+    if (p.pairs) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            qpos[nt] = clamp_i64(p.q_pos[(int64_t)b * p.qpos_sb + min(q0 + 16 * nt + col, p.Lq - 1)], 0,
+                                 p.rope_rows - 1);
+    }
+
     // Q operand: rows q0 + 16 nt + col, d = 32 ks + 8 grp .. +7
     u32x4 qr[2][4];
     {
@@ -188,12 +246,22 @@ prefill_kernel(PrefillParams p) {
     const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
     const TileOffsets toff = tile_offsets(p.k_sn, p.v_sn);
     TileRegs tr;
-    if (ntiles > 0) {
-        load_tile(tr, kb, vb, p.k_sn, p.v_sn, 0, n, toff);
+    if (ntiles > 0) load_tile(tr, kb, vb, p.k_sn, p.v_sn, 0, n, toff);
+    if (p.pairs) {
+        QPairs qp[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) load_q_pairs(qp[nt], p.pairs + qpos[nt] * kD, grp, p.repeats);
+        if (ntiles > 0) {
+            store_tile(tr, ks_buf[0], vts_buf[0]);
+            if (ntiles > 1) load_tile(tr, kb, vb, p.k_sn, p.v_sn, kKeys, n, toff);
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) rope_q_operand(qr[nt], qp[nt]);
+    } else if (ntiles > 0) {
         store_tile(tr, ks_buf[0], vts_buf[0]);
         if (ntiles > 1) load_tile(tr, kb, vb, p.k_sn, p.v_sn, kKeys, n, toff);
-        __syncthreads();
     }
+    if (ntiles > 0) __syncthreads();
     // the wave's earliest query sees keys up to q0 + shift
     const int wave_last = p.causal ? q0 + shift : n - 1;
 
@@ -346,6 +414,14 @@ extern "C" int slimkv_prefill_attention(const slimkv_prefill_attention_args* a, 
     p.Nk = (int)a->keys; p.causal = a->causal ? 1 : 0;
     p.qblocks = (p.Lq + kQRows - 1) / kQRows;
     p.scale_log2 = (float)(a->scale * 1.4426950408889634);
+    if (a->rope_pairs) {
+        // positions [batch, >= queries] with row stride qpos_sb (0: one row for every batch entry)
+        if (!a->q_positions || a->rope_rows <= 0 || a->qpos_sb < 0 || (a->qpos_sb > 0 && a->qpos_sb < a->queries))
+            return fail(SLIMKV_EINVAL, "query RoPE needs rope pairs, rope_rows > 0 and [batch, >= queries] positions");
+        if (!al16(a->rope_pairs)) return fail(SLIMKV_EINVAL, "RoPE pairs must be 16-byte aligned");
+        p.pairs = a->rope_pairs; p.rope_rows = a->rope_rows; p.repeats = a->rope_repeats ? 1 : 0;
+        p.q_pos = a->q_positions; p.qpos_sb = a->qpos_sb;
+    }
     const int64_t groups = (int64_t)p.qblocks * p.B * p.Hk;
     const int64_t grid = (groups + kXcds - 1) / kXcds * kXcds * (p.Hq / p.Hk);
     if (grid > 0x7fffffff) return fail(SLIMKV_EINVAL, "prefill grid too large");

@@ -206,9 +206,10 @@ extern "C" int slimkv_rope_decode(const slimkv_rope_decode_args* a, void* stream
 }
 
 extern "C" int slimkv_prefill_rope(const slimkv_prefill_rope_args* a, void* stream) {
-    if (!a || !a->q || !a->k || !a->out_q || !a->out_k || !a->cos || !a->sin || !a->positions || !a->roles)
+    if (!a || (a->queries && (!a->q || !a->out_q)) || !a->k || !a->out_k || !a->cos || !a->sin || !a->positions ||
+        !a->roles)
         return fail(SLIMKV_EINVAL, "null pointer");
-    if (a->dim <= 0 || a->dim % 16 || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->queries <= 0 ||
+    if (a->dim <= 0 || a->dim % 16 || a->batch <= 0 || a->heads <= 0 || a->kv_heads <= 0 || a->queries < 0 ||
         a->keys < a->queries || a->role_len < 0 || a->role_len > a->keys || a->rope_rows <= 0 || a->sink < 0)
         return fail(SLIMKV_EINVAL, "invalid prefill RoPE sizes");
     const int64_t strides[] = {a->q_sb, a->q_sh, a->q_ss, a->k_sb, a->k_sh, a->k_ss,
@@ -222,6 +223,7 @@ extern "C" int slimkv_prefill_rope(const slimkv_prefill_rope_args* a, void* stre
     p.q_rows = a->batch * a->heads * a->queries;
     p.k_rows = a->batch * a->kv_heads * a->keys;
     const int64_t items = (p.q_rows + p.k_rows) * (a->dim / 8);
+    if (items == 0) return SLIMKV_OK;
     const int64_t blocks = (items + 255) / 256;
     hipLaunchKernelGGL(prefill_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
     return check_hip(hipGetLastError(), "prefill rope kernel launch");

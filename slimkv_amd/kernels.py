@@ -74,13 +74,18 @@ def attention_forward(q, k, v, scale, causal=False, splits=0, seqlens=None, out=
     return out, lse
 
 
-def prefill_attention(q, k, v, scale, causal=True, seqlens_k=None, out=None, lse=None):
+def prefill_attention(q, k, v, scale, causal=True, seqlens_k=None, out=None, lse=None, *, q_positions=None,
+                      cos=None, sin=None):
     """Causal (bottom-right) GQA prefill attention, head_dim 128 (MFMA flash
-    attention).  q [B,Lq,Hq,128], k/v [B,N,Hk,128] BSHD bf16.
+    attention).  q [B,Lq,Hq,128], k/v [B,N,Hk,128] BSHD bf16.  With fp32
+    RoPE tables cos/sin [rows, 128] and q_positions [B, >= Lq] the kernel
+    rotates each query row as it loads it (the bits of prefill_rope's query
+    rotation), reading (bf16 cos | bf16 sin) pairs prepared once per table
+    (prepare_rope_pairs, cached on the table); k is taken as given.
 
     Returns (out [B,Lq,Hq,128] bf16, lse [B,Hq,Lq] fp32).
     """
-    _need_device(q, k, v, seqlens_k)
+    _need_device(q, k, v, seqlens_k, q_positions, cos, sin)
     _need_bf16(q, k, v)
     q, k, v = (_last_contiguous(x) for x in (q, k, v))
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -96,10 +101,23 @@ def prefill_attention(q, k, v, scale, causal=True, seqlens_k=None, out=None, lse
     if seqlens_k is not None:
         if seqlens_k.dtype != torch.int32 or not seqlens_k.is_contiguous() or seqlens_k.numel() != B:
             raise ValueError('One int32 key length per sequence required')
+    rope, pairs = (None, 0, 0, None, 0), None
+    if cos is not None:
+        if sin is None or q_positions is None:
+            raise ValueError('query RoPE needs cos, sin and q_positions')
+        if cos.dim() != 2 or cos.shape[1] != D:
+            raise ValueError('RoPE tables must be fp32 [rows, head_dim]')
+        pairs, repeats = prepare_rope_pairs(cos, sin)
+        q_positions = q_positions.to(torch.int64)
+        if q_positions.stride(-1) != 1:
+            q_positions = q_positions.contiguous()
+        if q_positions.dim() != 2 or q_positions.shape[0] != B or q_positions.shape[1] < Lq:
+            raise ValueError('q_positions must be [B, >= Lq]')
+        rope = (_ptr(pairs), pairs.shape[0], int(repeats), _ptr(q_positions), q_positions.stride(0))
     a = _lib.PrefillAttentionArgs(
         _ptr(q), *q.stride()[:3], _ptr(k), *k.stride()[:3], _ptr(v), *v.stride()[:3],
         _ptr(out), *out.stride()[:3], _ptr(lse), _ptr(seqlens_k),
-        B, Lq, Hq, Hk, N, D, float(scale), int(bool(causal)))
+        B, Lq, Hq, Hk, N, D, float(scale), int(bool(causal)), *rope)
     check(lib().slimkv_prefill_attention(ctypes.byref(a), _lib.stream_handle(q.device)))
     return out, lse
 
@@ -623,11 +641,17 @@ def decode_qkv(x, weight, bias, heads, kv_heads, cos, sin, positions, raw_k, raw
     return q_out
 
 
-def prefill_rope(q, k, cos, sin, positions, roles, sink):
-    """q [B,Hq,Lq,D], k [B,Hk,Nk,D]; outputs keep the input strides (empty_like)."""
-    _need_device(q, k, cos, sin, positions, roles)
-    _need_bf16(q, k)
-    oq, ok = torch.empty_like(q), torch.empty_like(k)
+def prefill_rope(q, k, cos, sin, positions, roles, sink, out_q=None, out_k=None):
+    """q [B,Hq,Lq,D], k [B,Hk,Nk,D]; outputs keep the input strides
+    (empty_like) unless the caller passes them (out_q / out_k of the inputs'
+    shapes, rows 16-byte aligned, not overlapping the inputs: a row's
+    rotate-half partner is read by another thread)."""
+    _need_device(q, k, cos, sin, positions, roles, out_q, out_k)
+    _need_bf16(q, k, out_q, out_k)
+    oq = torch.empty_like(q) if out_q is None else out_q
+    ok = torch.empty_like(k) if out_k is None else out_k
+    if oq.shape != q.shape or ok.shape != k.shape or oq.stride(-1) != 1 or ok.stride(-1) != 1:
+        raise ValueError('RoPE outputs must have the shapes of q and k with contiguous rows')
     pos = positions if positions.stride(-1) == 1 else positions.contiguous()
     roles = roles.to(device=q.device, dtype=torch.int64).contiguous()
     a = _lib.PrefillRopeArgs(
@@ -638,6 +662,28 @@ def prefill_rope(q, k, cos, sin, positions, roles, sink):
         q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3], int(sink))
     check(lib().slimkv_prefill_rope(ctypes.byref(a), _lib.stream_handle(q.device)))
     return oq, ok
+
+
+def rope_keys(k, cos, sin, positions, roles, sink, out_k=None):
+    """The key half of prefill_rope: k [B,Hk,Nk,D] rotated (beacon keys
+    copied unchanged) into out_k (default empty_like); for an attention that
+    rotates its own queries (prefill_attention with q_positions)."""
+    _need_device(k, cos, sin, positions, roles, out_k)
+    _need_bf16(k, out_k)
+    ok = torch.empty_like(k) if out_k is None else out_k
+    if ok.shape != k.shape or ok.stride(-1) != 1:
+        raise ValueError('the RoPE output must have the shape of k with contiguous rows')
+    pos = positions if positions.stride(-1) == 1 else positions.contiguous()
+    roles = roles.to(device=k.device, dtype=torch.int64).contiguous()
+    B, Hk, Nk, D = k.shape
+    a = _lib.PrefillRopeArgs(
+        None, 0, 0, 0, _ptr(k), *k.stride()[:3],
+        None, 0, 0, 0, _ptr(ok), *ok.stride()[:3],
+        _ptr(cos), _ptr(sin), cos.shape[0], _ptr(pos), pos.stride(0),
+        _ptr(roles), roles.numel(),
+        B, Hk, Hk, 0, Nk, D, int(sink))
+    check(lib().slimkv_prefill_rope(ctypes.byref(a), _lib.stream_handle(k.device)))
+    return ok
 
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}

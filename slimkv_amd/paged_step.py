@@ -192,9 +192,8 @@ def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_ta
     raw_k[rows, t['new_row']] = new_k[:, 0]
     raw_v[rows, t['new_row']] = new_v[:, 0]
     cos, sin = _tables(attention.rotary_emb, device)
-    unrotated_q = q.new_zeros(B, 1, 1, dim)                    # prefill_rope rotates keys and queries
-    _, raw_k_rot = kernels.prefill_rope(unrotated_q, raw_k.transpose(1, 2), cos, sin, t['raw_positions'],
-                                        torch.zeros(group.max_raw, dtype=torch.long, device=device), 0)
+    raw_k_rot = kernels.rope_keys(raw_k.transpose(1, 2), cos, sin, t['raw_positions'],
+                                  torch.zeros(group.max_raw, dtype=torch.long, device=device), 0)
 
     # 4. the fused latent decode, beacon rows through their pages
     bd = is_block_diagonal(uk.weight, kv_heads) and is_block_diagonal(uv.weight, kv_heads)

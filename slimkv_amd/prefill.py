@@ -19,7 +19,10 @@ _apply_rotary_with_beacon (:1108-1216, prefill-metadata case):
    beacons are rebuilt onto the history (the reference rebuilds the whole
    history every window, modeling_llama.py:1677-1681, from a latent history it
    concatenates anew, slimkv/llama3/memory.py:255-267).
-4. bf16-exact RoPE that leaves beacon K unrotated (prefill RoPE kernel).
+4. bf16-exact RoPE that leaves beacon K unrotated: the keys by the prefill
+   RoPE kernel, the queries inside the attention kernel as it loads them
+   (the same bits as rotating them first, without writing them out and
+   reading them back).
 5. Causal attention (MFMA flash-attention kernel), then o_proj_with_beacon.
 
 The module's own q/k/v/o projections are called as they are (model layers);
@@ -30,7 +33,6 @@ import torch
 from . import kernels
 from .latent_decode import uses_latent_decode
 from .memory import ReconstructionCache, ReconstructionCacheUpdate, is_block_diagonal
-from .prefill_ops import fused_prefill_rope
 
 
 def _rows_where(current, role):
@@ -112,19 +114,26 @@ def _pack(attention, latent):
 
 
 class PrefillHistory:
-    """Append-only full-dimensional K/V of one layer for a stream of prefill
-    windows: rows [0, sink + history) hold [sink | up(history beacons)] in the
-    order the memory keeps them, and each window is written right after them.
+    """Append-only attention K/V of one layer for a stream of prefill windows:
+    rows [0, sink + history) hold [sink | up(history beacons)] in the order
+    the memory keeps them, keys as the attention reads them, and each window
+    is written right after them.
 
-    It replaces the per-window rebuild of the whole history: the memory hands
-    every window the sink and the latents of all earlier windows' beacons
-    (ReconstructionCache), and ReconstructionCache.materialize up-projects all
-    of them again (modeling_llama.py:1677-1681).  Here a window costs one
-    reconstruction of its own new beacons.  The store follows the memory's
-    update rules (slimkv/llama3/memory.py:233-278): the first window's first
-    `sink` rows become the sink, and every window's beacon latents are
-    appended to the history.  `capacity` bounds sink + history + window rows;
-    BHSD buffers [batch, kv_heads, capacity, head_dim]."""
+    It replaces the per-window rebuild and rotation of the whole key set: the
+    memory hands every window the sink and the latents of all earlier
+    windows' beacons (ReconstructionCache), ReconstructionCache.materialize
+    up-projects all of them again (modeling_llama.py:1677-1681) and the
+    prefill RoPE then runs over every key (:1685-1690).  Here a window costs
+    the rotation of its own rows and one reconstruction of its new beacons:
+    history keys are beacon keys, which the prefill RoPE leaves unrotated
+    (beacon_skip_rope_for_beacon_k), and the sink keeps the rotation it got
+    in the first window, at positions 0 .. sink - 1, which full-coverage
+    prefill positions (arange over the memory and the window,
+    slimkv/memory.py:616) give it in every window.  The store follows the
+    memory's update rules (slimkv/llama3/memory.py:233-278): the first
+    window's first `sink` rows become the sink, and every window's beacon
+    latents are appended to the history.  `capacity` bounds sink + history +
+    window rows; BHSD buffers [batch, kv_heads, capacity, head_dim]."""
 
     def __init__(self, batch, kv_heads, head_dim, capacity, device, dtype=torch.bfloat16):
         self.k = torch.empty(batch, kv_heads, capacity, head_dim, dtype=dtype, device=device)
@@ -148,15 +157,18 @@ class PrefillHistory:
             return True
         return lengths == [self.sink, self.history]
 
-    def window(self, current_k, current_v):
-        """Write the window's K/V (BHSD [B, Hk, L, D]) after the held rows and
-        return the key/value sets [sink | up(history) | window] as views."""
-        base, L = self.sink + self.history, current_k.shape[2]
-        if base + L > self.k.shape[2] or current_k.shape[0] != self.k.shape[0]:
+    def reserve(self, batch, length):
+        """(base, key rows, value rows) of a window of `length` rows written
+        after the held ones: BHSD views [B, Hk, length, D] at row `base`."""
+        base = self.sink + self.history
+        if base + length > self.k.shape[2] or batch != self.k.shape[0]:
             raise ValueError('prefill history capacity exceeded')
-        self.k[:, :, base:base + L].copy_(current_k)
-        self.v[:, :, base:base + L].copy_(current_v)
-        return self.k[:, :, :base + L], self.v[:, :, :base + L]
+        return base, self.k[:, :, base:base + length], self.v[:, :, base:base + length]
+
+    def sets(self, length):
+        """The key and value sets [sink | history | window] as views."""
+        end = self.sink + self.history + length
+        return self.k[:, :, :end], self.v[:, :, :end]
 
     def append(self, attention, key_latent, value_latent, sink_size):
         """After the window is attended: the first window's leading rows stay
@@ -177,6 +189,22 @@ class PrefillHistory:
                                     out=dst[:, :, base:base + n].transpose(1, 2),
                                     block_diagonal=is_block_diagonal(up.weight, heads))
             self.history += n
+
+
+def _rope_tables(rope, query, keys, metadata, n):
+    """fp32 (cos, sin) of the module's rotary table for the prefill RoPE of
+    [B, n] keys; ValueError where the kernels do not apply (the conditions of
+    fused_prefill_rope, prefill_ops.py:48-73)."""
+    B = query.shape[0]
+    if (not query.is_cuda or query.dtype != torch.bfloat16 or keys.dtype != query.dtype or query.shape[-1] % 16
+            or type(rope).__name__ not in ('RotaryEmbedding', 'LinearScalingRotaryEmbedding', 'Llama3RotaryEmbedding')
+            or metadata.positions.shape != (B, n) or n > rope.max_seq_len_cached
+            or metadata.roles.numel() > keys.shape[2] or query.stride(-1) != 1 or keys.stride(-1) != 1):
+        raise ValueError('prefill RoPE needs bf16 device tensors and a standard rotary table')
+    cos, sin = rope.cos_cached, rope.sin_cached
+    if cos.device != query.device or cos.dtype != torch.float32:
+        cos, sin = cos.to(query.device, torch.float32), sin.to(query.device, torch.float32)
+    return cos, sin
 
 
 def prefill_forward(attention, hidden_states, position_ids, past_key_value, history=None):
@@ -203,22 +231,28 @@ def prefill_forward(attention, hidden_states, position_ids, past_key_value, hist
                                            _pack(attention, key_latent), _pack(attention, value_latent))
         if metadata is not None:
             update.raw_indices = metadata.raw_indices
+    query = q.view(B, L, Hq, D)                                           # BSHD
+    if metadata is None:
+        raise ValueError('prefill_forward needs the prefill metadata (prefill_ops.prepare_metadata)')
+    positions, roles = metadata.positions, metadata.roles
+    # The queries are rotated inside the attention kernel as it loads them;
+    # the keys by the prefill RoPE (beacon keys copied unrotated).
     if store is not None:
-        key_states, value_states = store.window(current_k, current_v)
+        base, key_rows, value_rows = store.reserve(B, L)
+        cos, sin = _rope_tables(attention.rotary_emb, query, current_k, metadata, base + L)
+        if roles.numel() != L:
+            raise ValueError('the prefill history rotates the window\'s keys: roles must cover the window')
+        value_rows.copy_(current_v)
+        kernels.rope_keys(current_k, cos, sin, positions[:, base:], roles, 0, out_k=key_rows)
+        k_rot, value_states = store.sets(L)
     else:
         key_states = past_key.materialize(attention, current_k)
         value_states = past_value.materialize(attention, current_v)
-    query_states = q.view(B, L, Hq, D).transpose(1, 2)
-    if metadata is None:
-        raise ValueError('prefill_forward needs the prefill metadata (prefill_ops.prepare_metadata)')
-    rotated = fused_prefill_rope(query_states, key_states, attention.rotary_emb, metadata,
-                                 attention.config.beacon_sink_size)
-    if rotated is None:
-        raise ValueError('prefill RoPE needs bf16 device tensors and a standard rotary table')
-    q_rot, k_rot = rotated
+        cos, sin = _rope_tables(attention.rotary_emb, query, key_states, metadata, key_states.shape[2])
+        k_rot = kernels.rope_keys(key_states, cos, sin, positions, roles, attention.config.beacon_sink_size)
     scale = getattr(attention, 'softmax_scale', None) or D ** -0.5
-    out, _ = kernels.prefill_attention(q_rot.transpose(1, 2), k_rot.transpose(1, 2), value_states.transpose(1, 2),
-                                       scale, causal=True)
+    out, _ = kernels.prefill_attention(query, k_rot.transpose(1, 2), value_states.transpose(1, 2), scale,
+                                       causal=True, q_positions=positions[:, -L:], cos=cos, sin=sin)
     out = out.reshape(B, L, Hq * D)
     if store is not None:
         store.append(attention, key_latent, value_latent, getattr(attention.config, 'beacon_sink_size', 0))

@@ -102,16 +102,19 @@ def test_extension_module_signature():
 def test_prefill_history_follows_the_memory():
     """PrefillHistory bookkeeping on the host: an empty past restarts the
     stream, a past whose sink/history lengths differ from the store's (or that
-    holds open window rows) is refused, the window is written after the held
-    rows and the capacity is enforced."""
+    holds open window rows) is refused, the window's rows are reserved after
+    the held rows and the capacity is enforced."""
     from slimkv_amd.memory import ReconstructionCache
     from slimkv_amd.prefill import PrefillHistory
     store = PrefillHistory(2, 2, 128, 40, 'cpu')
     empty = ReconstructionCache(None, None, None, None, None, 2, 128, 'k')
     assert store.follows(empty, empty)
     cur = torch.randn(2, 2, 16, 128).to(torch.bfloat16)
-    k, v = store.window(cur, -cur)
-    assert k.shape == (2, 2, 16, 128) and torch.equal(k, cur) and torch.equal(v, -cur)
+    base, kr, vr = store.reserve(2, 16)
+    kr.copy_(cur)
+    vr.copy_(-cur)
+    k, v = store.sets(16)
+    assert base == 0 and k.shape == (2, 2, 16, 128) and torch.equal(k, cur) and torch.equal(v, -cur)
     att = SimpleNamespace(num_key_value_heads=2)
     store.append(att, None, None, sink_size=4)            # no beacons: only the sink is kept
     assert (store.sink, store.history) == (4, 0)
@@ -121,10 +124,14 @@ def test_prefill_history_follows_the_memory():
     assert not store.follows(past, past)                 # the store holds no history yet
     store.history = 8
     assert store.follows(past, past)
-    k, _ = store.window(cur, cur)
-    assert k.shape[2] == 4 + 8 + 16 and torch.equal(k[:, :, 12:], cur)
+    base, kr, _ = store.reserve(2, 16)
+    kr.copy_(cur)
+    k, _ = store.sets(16)
+    assert base == 12 and k.shape[2] == 4 + 8 + 16 and torch.equal(k[:, :, 12:], cur)
     with_window = ReconstructionCache(sink, hist, torch.zeros(2, 2, 3, 128), None, None, 2, 128, 'k')
     assert not store.follows(with_window, with_window)
     with pytest.raises(ValueError, match='capacity'):
-        store.window(torch.zeros(2, 2, 29, 128), torch.zeros(2, 2, 29, 128))
+        store.reserve(2, 29)
+    with pytest.raises(ValueError, match='capacity'):
+        store.reserve(3, 16)
     assert store.follows(empty, empty) and (store.sink, store.history) == (0, 0)

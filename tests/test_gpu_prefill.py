@@ -89,6 +89,35 @@ def test_per_sequence_key_lengths(device):
     _run(device, 4, 64, 300, 8, 2, True, seed=2, seqlens=[300, 64, 1, 0])
 
 
+@pytest.mark.parametrize('B,Lq,N,Hq,Hk,sink', [(2, 200, 330, 8, 2, 4), (1, 64, 64, 4, 1, 0)])
+def test_query_rope_inside_attention_is_bit_identical(device, B, Lq, N, Hq, Hk, sink):
+    """Queries rotated as the attention kernel loads them (q_positions, cos,
+    sin) give the bits of prefill_rope's rotated queries fed to the same
+    kernel; rope_keys gives prefill_rope's keys; the queries' positions are
+    the last Lq of [B, N] (here shuffled per batch entry, so each row reads
+    its own position), beacon roles in the window."""
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import rope_tables
+    gen = torch.Generator(device=device).manual_seed(7)
+    q = torch.randn(B, Lq, Hq, 128, generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn(B, N, Hk, 128, generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn(B, N, Hk, 128, generator=gen, device=device).to(torch.bfloat16)
+    cos, sin = rope_tables(4096, 128, 500000.0, device)
+    positions = torch.stack([torch.randperm(4000, generator=torch.Generator().manual_seed(b))[:N]
+                             for b in range(B)]).to(device)
+    roles = torch.zeros(Lq, dtype=torch.long, device=device)
+    roles[4::5] = 1
+    q_rot, k_rot = kernels.prefill_rope(q.transpose(1, 2), k.transpose(1, 2), cos, sin, positions, roles, sink)
+    k_only = kernels.rope_keys(k.transpose(1, 2), cos, sin, positions, roles, sink)
+    want, want_lse = kernels.prefill_attention(q_rot.transpose(1, 2), k_rot.transpose(1, 2), v, 0.0883883)
+    got, got_lse = kernels.prefill_attention(q, k_only.transpose(1, 2), v, 0.0883883, q_positions=positions[:, -Lq:],
+                                             cos=cos, sin=sin)
+    torch.cuda.synchronize()
+    assert torch.equal(k_only.view(torch.int16), k_rot.view(torch.int16))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(got_lse, want_lse)
+
+
 def test_rejects_other_head_dims(device):
     from slimkv_amd import kernels
     x = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16, device=device)
