@@ -139,6 +139,88 @@ prefill_rope_kernel(PrefillRopeParams p) {
     }
 }
 
+// head_dim 128: 16 lanes a row (8 features a lane, one 16-byte load), the
+// rotate-half partner (features d +- 64) taken from lane l ^ 8 of the same
+// 16-lane row by a DPP rotation instead of a second load, 32-bit index math,
+// and kRopeRows rows a lane group with all their loads issued before any use.
+constexpr int kRopeRows = 4;
+
+__device__ __forceinline__ uint32_t ror8(uint32_t v) {        // row_ror:8 inside each 16-lane row
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, true);
+}
+
+__global__ void __launch_bounds__(256)
+prefill_rope_rows_kernel(PrefillRopeParams p) {
+    const slimkv_prefill_rope_args& a = p.a;
+    const uint32_t lane16 = threadIdx.x & 15;
+    const uint32_t group = (blockIdx.x * 256u + threadIdx.x) >> 4;
+    const uint32_t Q = (uint32_t)p.q_rows, total = (uint32_t)(p.q_rows + p.k_rows);
+    const uint32_t queries = (uint32_t)a.queries, keys = (uint32_t)a.keys;
+    const uint32_t heads = (uint32_t)a.heads, kv_heads = (uint32_t)a.kv_heads;
+    const int dd = (int)lane16 * 8;
+    const int64_t prefix = a.keys - a.role_len;
+    const uint16_t* src[kRopeRows];
+    uint16_t* dst[kRopeRows];
+    int64_t pos[kRopeRows];
+    bool live[kRopeRows], beacon[kRopeRows];
+    u32x4 x[kRopeRows];
+#pragma unroll
+    for (int i = 0; i < kRopeRows; ++i) {
+        const uint32_t r = group * kRopeRows + i;
+        live[i] = r < total;
+        const uint32_t rr = live[i] ? r : total - 1;          // dead rows read a live one, store nothing
+        if (rr < Q) {
+            const uint32_t s = rr % queries, t = rr / queries, hh = t % heads, b = t / heads;
+            src[i] = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_sb + (int64_t)hh * a.q_sh + (int64_t)s * a.q_ss;
+            dst[i] = static_cast<uint16_t*>(a.out_q) + (int64_t)b * a.oq_sb + (int64_t)hh * a.oq_sh + (int64_t)s * a.oq_ss;
+            pos[i] = a.positions[(int64_t)b * a.pos_sb + a.keys - a.queries + s];
+            beacon[i] = false;
+        } else {
+            const uint32_t kr = rr - Q;
+            const uint32_t s = kr % keys, t = kr / keys, hh = t % kv_heads, b = t / kv_heads;
+            src[i] = static_cast<const uint16_t*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hh * a.k_sh + (int64_t)s * a.k_ss;
+            dst[i] = static_cast<uint16_t*>(a.out_k) + (int64_t)b * a.ok_sb + (int64_t)hh * a.ok_sh + (int64_t)s * a.ok_ss;
+            pos[i] = a.positions[(int64_t)b * a.pos_sb + s];
+            const bool in_window = (int64_t)s >= prefix;
+            const int64_t role = in_window ? a.roles[(int64_t)s - prefix] : 0;
+            beacon[i] = in_window ? (role == 1 || role == 2) : ((int64_t)s >= a.sink);
+        }
+        x[i] = *reinterpret_cast<const u32x4*>(src[i] + dd);
+    }
+    float4 cv[kRopeRows][2], sv[kRopeRows][2];
+#pragma unroll
+    for (int i = 0; i < kRopeRows; ++i) {
+        const int64_t row = clamp_i64(pos[i], 0, a.rope_rows - 1) * a.dim + dd;
+        cv[i][0] = *reinterpret_cast<const float4*>(a.cos + row);
+        cv[i][1] = *reinterpret_cast<const float4*>(a.cos + row + 4);
+        sv[i][0] = *reinterpret_cast<const float4*>(a.sin + row);
+        sv[i][1] = *reinterpret_cast<const float4*>(a.sin + row + 4);
+    }
+#pragma unroll
+    for (int i = 0; i < kRopeRows; ++i) {
+        const uint32_t pr[4] = {ror8(x[i].x), ror8(x[i].y), ror8(x[i].z), ror8(x[i].w)};
+        const uint32_t xs[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+        const float c8[8] = {cv[i][0].x, cv[i][0].y, cv[i][0].z, cv[i][0].w, cv[i][1].x, cv[i][1].y, cv[i][1].z, cv[i][1].w};
+        const float s8[8] = {sv[i][0].x, sv[i][0].y, sv[i][0].z, sv[i][0].w, sv[i][1].x, sv[i][1].y, sv[i][1].z, sv[i][1].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float sum[2];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const float v = hb ? hi_bf16(xs[e]) : lo_bf16(xs[e]);
+                float pt = hb ? hi_bf16(pr[e]) : lo_bf16(pr[e]);
+                if (lane16 < 8) pt = -pt;
+                sum[hb] = round_bf16_hw(v * round_bf16_hw(c8[2 * e + hb])) +
+                          round_bf16_hw(pt * round_bf16_hw(s8[2 * e + hb]));
+            }
+            o[e] = pack_bf16(sum[0], sum[1]);
+        }
+        const u32x4 out = beacon[i] ? x[i] : u32x4{o[0], o[1], o[2], o[3]};
+        if (live[i]) *reinterpret_cast<u32x4*>(dst[i] + dd) = out;
+    }
+}
+
 __global__ void __launch_bounds__(256)
 merge_kernel(slimkv_merge_args a) {
     const int per_row = (int)(a.dim / 8);
@@ -224,6 +306,13 @@ extern "C" int slimkv_prefill_rope(const slimkv_prefill_rope_args* a, void* stre
     p.k_rows = a->batch * a->kv_heads * a->keys;
     const int64_t items = (p.q_rows + p.k_rows) * (a->dim / 8);
     if (items == 0) return SLIMKV_OK;
+    if (a->dim == 128 && p.q_rows + p.k_rows < ((int64_t)1 << 31) - kRopeRows * 4096 && a->queries < (1 << 30) &&
+        a->keys < (1 << 30) && pal16(a->cos) && pal16(a->sin)) {
+        const int64_t groups = (p.q_rows + p.k_rows + kRopeRows - 1) / kRopeRows;
+        hipLaunchKernelGGL(prefill_rope_rows_kernel, dim3((unsigned)((groups * 16 + 255) / 256)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), p);
+        return check_hip(hipGetLastError(), "prefill rope kernel launch");
+    }
     const int64_t blocks = (items + 255) / 256;
     hipLaunchKernelGGL(prefill_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
     return check_hip(hipGetLastError(), "prefill rope kernel launch");
