@@ -54,6 +54,31 @@ def _time_steps(torch, step, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
+def _timed_graph(torch, body, replays=20):
+    """Seconds per run of `body` captured as one HIP graph and replayed back to
+    back (HIP events around the replays): the kernels' own time at warm
+    clocks, with no host launch gaps."""
+    body()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        body()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    for _ in range(3):
+        g.replay()
+    a, b = _events(torch)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3 / replays
+
+
 def _replays(torch, step, count=50):
     """Median of `count` single steps bracketed by HIP events, and the clocks."""
     from bench import gpu_clocks, replay_median_ms
@@ -194,7 +219,13 @@ def prefill(args):
     def keys(w):
         return L if w == 0 else S + NB * w + L
 
-    def window(w, timed=None):
+    def attend(w):
+        n = keys(w)
+        base = 0 if w == 0 else S + NB * w
+        kernels.prefill_attention(qs[w], work_k[:, :n], work_v[:, :n], scale, True, out=out, lse=lse,
+                                  q_positions=positions[:, base:n], cos=cos, sin=sin)
+
+    def window(w):
         n = keys(w)
         base = 0 if w == 0 else S + NB * w           # the window follows [sink | history]
         proj_k.copy_(cur[w][0])
@@ -205,12 +236,7 @@ def prefill(args):
             kernels.reconstruct(lat, up[j], kv_heads=HKV, out=dst, dst_rows=beacon_rows, block_diagonal=True)
         kernels.rope_keys(proj_k.transpose(1, 2), cos, sin, positions[:, base:n], roles, 0,
                           out_k=work_k[:, base:n].transpose(1, 2))
-        if timed:
-            timed[0].record()
-        kernels.prefill_attention(qs[w], work_k[:, :n], work_v[:, :n], scale, True, out=out, lse=lse,
-                                  q_positions=positions[:, base:n], cos=cos, sin=sin)
-        if timed:
-            timed[1].record()
+        attend(w)
         # the window's new beacons onto the history (after the sink of window 0)
         hist = S + NB * w
         for j, dst in ((0, work_k), (1, work_v)):
@@ -225,16 +251,9 @@ def prefill(args):
     replays, clocks = _replays(torch, step)
     pairs = [sum(min(keys(w), i + keys(w) - L + 1) for i in range(L)) for w in range(WINDOWS)]
     flops = [p * 4 * D * HQ * B for p in pairs]
-    # attention kernel alone, events on the launch stream
-    evs = [_events(torch) for _ in range(WINDOWS)]
-    kernel_s = []
-    for _ in range(3):
-        torch.cuda._sleep(50_000_000)
-        for w in range(WINDOWS):
-            window(w, evs[w])
-        torch.cuda.synchronize()
-        kernel_s.append(sum(a.elapsed_time(b) for a, b in evs) * 1e-3)
-    kernel_s = sorted(kernel_s)[1]
+    # the eight attention launches of a step alone, replayed back to back as
+    # one graph (their cost does not depend on the values the buffers hold)
+    kernel_s = _timed_graph(torch, lambda: [attend(w) for w in range(WINDOWS)])
     achieved = sum(flops) / kernel_s / 1e12
     result = _result('prefill attention TFLOP/s, 8 windows of 1024+256, b4, 32/8 heads', sum(flops) / seconds / 1e12,
                      'TFLOP/s', args, seconds, 'bf16',
