@@ -253,7 +253,18 @@ def prefill(args):
     flops = [p * 4 * D * HQ * B for p in pairs]
     # the eight attention launches of a step alone, replayed back to back as
     # one graph (their cost does not depend on the values the buffers hold)
-    kernel_s = _timed_graph(torch, lambda: [attend(w) for w in range(WINDOWS)])
+    attention_only = lambda: [attend(w) for w in range(WINDOWS)]
+    if args.no_graph:                                 # counter runs: eager launches, events around them
+        attention_only()
+        a, b = _events(torch)
+        torch.cuda.synchronize()
+        a.record()
+        attention_only()
+        b.record()
+        torch.cuda.synchronize()
+        kernel_s = a.elapsed_time(b) * 1e-3
+    else:
+        kernel_s = _timed_graph(torch, attention_only)
     achieved = sum(flops) / kernel_s / 1e12
     result = _result('prefill attention TFLOP/s, 8 windows of 1024+256, b4, 32/8 heads', sum(flops) / seconds / 1e12,
                      'TFLOP/s', args, seconds, 'bf16',
