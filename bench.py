@@ -183,9 +183,10 @@ def main():
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-graph', action='store_true', help='time eager launches instead of graph replay')
-    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged', 'b1', 'ceiling'),
+    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged', 'paged_step', 'b1', 'ceiling'),
                     help='latent: the headline decode sweep; prefill / recon / paged: the window prefill, '
-                         'reconstruction decode and paged-cache decode workloads; b1: batch-1 ms per token '
+                         'reconstruction decode and paged-cache decode workloads; paged_step: one attention '
+                         'layer of a batched vLLM decode step over the pages; b1: batch-1 ms per token '
                          'at the contexts the reference publishes; ceiling: the HBM read rate a plain '
                          'stream reaches on this GPU')
     args = ap.parse_args()

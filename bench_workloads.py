@@ -870,8 +870,149 @@ def b1(args):
                    clocks=clocks)
 
 
+# ----------------------------------------------------------------------------- batched paged decode step
+
+STEP_SHAPE = dict(NREQ=64, HIDDEN=4096, HQ=32, HKV=8, D=128, RATIO=8, WINDOW=1024, SINK=1, r=32)
+
+
+class _RotaryTables:
+    """Rotary module stand-in with the name the decode paths recognise."""
+    def __init__(self, cos, sin):
+        self.cos_cached, self.sin_cached = cos, sin
+        self.max_seq_len_cached = cos.shape[0]
+
+
+def paged_step(args):
+    """One decode step of one Llama-3.1-8B attention layer (32/8 heads, t8,
+    per-head rank 32, window 1024, one sink) for 64 vLLM requests whose
+    contexts are drawn from [1024, 131072]: slimkv_amd.paged_step's
+    paged_decode_layer over the requests' beacon pages (BeaconPageLayout(16, 8,
+    256, 256, 1024)) and raw pages, the module's q/k/v/o and beacon
+    projections included (random-init nn.Linear layers of the layer's
+    shapes).  The step plan (plan_paged_step) is made once per decode step
+    for all layers and is not timed.  Beside it the same layer runs once per
+    request (groups of one), the shape of the reference's per-request loop
+    (SlimKVLlamaForCausalLM._paged_forward, vllm_plugin/model.py:114-142)."""
+    import random
+    from types import SimpleNamespace
+    import torch
+    from slimkv_amd import kernels
+    from slimkv_amd.paged_cache import BeaconPageLayout
+    from slimkv_amd.paged_step import paged_decode_layer, plan_paged_step
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
+    c = STEP_SHAPE
+    NREQ, HID, HQ, HKV, D, RATIO, W, SINK, r = (c[k] for k in ('NREQ', 'HIDDEN', 'HQ', 'HKV', 'D', 'RATIO', 'WINDOW',
+                                                               'SINK', 'r'))
+    R = HKV * r
+    dev = torch.device('cuda:0')
+    rng = random.Random(args.seed)
+    processed = [rng.randint(1024, 131072) for _ in range(NREQ)]
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    cpu = torch.Generator().manual_seed(args.seed + 1)
+
+    def linear(i, o, weight=None):
+        lin = torch.nn.Linear(i, o, bias=False, device=dev, dtype=torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.copy_(weight if weight is not None else torch.randn(o, i, generator=gen, device=dev) / i ** 0.5)
+        return lin
+
+    cos, sin = rope_tables(max(processed) + 4096, D, 500000.0, dev)
+    up = [block_diagonal([orthonormal_columns(D, r, cpu) for _ in range(HKV)]).to(dev, torch.bfloat16)
+          for _ in range(2)]
+    att = SimpleNamespace(
+        config=SimpleNamespace(beacon_param=['q', 'k', 'v'], beacon_skip_rope_for_beacon_k=True),
+        num_heads=HQ, num_key_value_heads=HKV, head_dim=D, hidden_size=HID,
+        q_proj=linear(HID, HQ * D), k_proj=linear(HID, HKV * D), v_proj=linear(HID, HKV * D),
+        beacon_q_proj=linear(HID, HQ * D), beacon_k_down_proj=linear(HID, R), beacon_v_down_proj=linear(HID, R),
+        beacon_k_up_proj=linear(R, HKV * D, up[0]), beacon_v_up_proj=linear(R, HKV * D, up[1]),
+        o_proj=linear(HQ * D, HID), rotary_emb=_RotaryTables(cos, sin))
+    att._use_shared_kv_down_proj = lambda: False
+    att.o_proj_with_beacon = lambda output, size, roles: att.o_proj(output)
+
+    # beacon pages: each request's beacons (and the step's new one) on a permuted pool
+    layout = BeaconPageLayout(16, RATIO, R, R, HKV * D)
+    need = [(p // RATIO + 1 + layout.slots - 1) // layout.slots for p in processed]
+    pool_pages = sum(need) + 64
+    pool = torch.empty(pool_pages, layout.page_elements, dtype=torch.bfloat16, device=dev)
+    for i in range(0, pool_pages, 50_000):
+        pool[i:i + 50_000].normal_(generator=gen)
+    perm = torch.randperm(pool_pages, generator=cpu)
+    btables = torch.zeros(NREQ, max(need), dtype=torch.long)
+    off = 0
+    for i, n in enumerate(need):
+        btables[i, :n] = perm[off:off + n]
+        off += n
+    # raw pages: blocks of the open window and the step's token; earlier
+    # positions map to block 0, which the step neither reads nor writes
+    cols = max((p + 1) // 16 + 1 for p in processed)
+    win_blocks = [list(range((p - p % W) // 16, p // 16 + 1)) for p in processed]
+    raw_blocks = 1 + sum(len(x) for x in win_blocks)
+    raw_pool = torch.randn(raw_blocks, 16, 2, HKV, D, generator=gen, device=dev).to(torch.bfloat16)
+    rtables = torch.zeros(NREQ, cols, dtype=torch.long)
+    nxt = 1
+    for i, blocks in enumerate(win_blocks):
+        for blk in blocks:
+            rtables[i, blk] = nxt
+            nxt += 1
+    btables, rtables = btables.to(dev), rtables.to(dev)
+    groups = plan_paged_step(processed, W, RATIO, SINK, dev)
+    hidden = {g.size: (0.5 * torch.randn(len(g.index), 1 + g.size, HID, generator=gen, device=dev)).to(torch.bfloat16)
+              for g in groups}
+    tables = {g.size: (rtables[g.tensors['index']], btables[g.tensors['index']]) for g in groups}
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def layer():
+        with torch.no_grad():
+            for g in groups:
+                rt, bt = tables[g.size]
+                paged_decode_layer(att, hidden[g.size], g, raw_pool, pool, rt, bt, 16, status=status)
+
+    # the same layer one request at a time (groups of one)
+    row_of = {i: (g.size, row) for g in groups for row, i in enumerate(g.index)}
+    singles = []
+    for i, p in enumerate(processed):
+        (g1,) = plan_paged_step([p], W, RATIO, SINK, dev)
+        size, row = row_of[i]
+        singles.append((g1, hidden[size][row:row + 1], rtables[i:i + 1], btables[i:i + 1]))
+
+    def per_request():
+        with torch.no_grad():
+            for g1, h1, rt, bt in singles:
+                paged_decode_layer(att, h1, g1, raw_pool, pool, rt, bt, 16, status=status)
+
+    seconds = _time_steps(torch, layer, args.steps, args.warmup)
+    replays, clocks = _replays(torch, layer)
+    graph_s = _timed_graph(torch, layer)          # the layer's GPU time without host launch gaps
+    loop_s = _time_steps(torch, per_request, max(3, args.steps // 4), 1)
+    kernels.check_status(status)
+    weights = sum(x.weight.numel() for x in (att.q_proj, att.k_proj, att.v_proj, att.o_proj, att.beacon_k_up_proj,
+                                             att.beacon_v_up_proj)) * 2
+    inserting = [g for g in groups if g.size]
+    if inserting:
+        weights += sum(x.weight.numel() for x in (att.beacon_q_proj, att.beacon_k_down_proj,
+                                                  att.beacon_v_down_proj)) * 2
+    beacon_bytes = sum(g.rows_total for g in groups) * 2 * R * 2
+    raw_bytes = sum((SINK + rc) * HKV * D * 2 * 2 for g in groups for rc in g.raw_counts)
+    step_bytes = weights + beacon_bytes + raw_bytes
+    tokens_per_s = NREQ / (32 * seconds)
+    return _result('batched paged decode step, one Llama-3.1-8B attention layer, 64 requests ctx U[1K,128K] t8',
+                   step_bytes / seconds / 1e9, 'GB/s', args, seconds, 'bf16',
+                   {'workload': 'vLLM decode step of 64 paged requests through paged_decode_layer (projections, '
+                                'page appends, raw gather and RoPE, paged latent decode, flush writes)',
+                    'requests': NREQ, 'window': W, 'ratio': RATIO, 'sink': SINK, 'per_head_rank': r,
+                    'groups': {str(g.size): len(g.index) for g in groups}, 'beacon_pool_pages': pool_pages},
+                   hbm_frac=round(step_bytes / seconds / 1e9 / HBM_PEAK_GBPS, 4), bytes_per_step=step_bytes,
+                   bytes_note='algorithmic: layer weights once, beacon latents and raw window rows of every request',
+                   attention_layers_tokens_per_s=round(tokens_per_s, 1),
+                   graph_replay_ms=round(graph_s * 1e3, 4),
+                   graph_replay_gbps=round(step_bytes / graph_s / 1e9, 1),
+                   per_request_loop_ms=round(loop_s * 1e3, 4),
+                   batched_speedup=round(loop_s / seconds, 2), replays=replays, clocks=clocks)
+
+
 def run_workload(args):
     from slimkv_amd._lib import library_identity
-    result = {'prefill': prefill, 'recon': recon, 'paged': paged, 'b1': b1, 'ceiling': ceiling}[args.workload](args)
+    result = {'prefill': prefill, 'recon': recon, 'paged': paged, 'paged_step': paged_step, 'b1': b1,
+              'ceiling': ceiling}[args.workload](args)
     result['library'] = library_identity()
     return result

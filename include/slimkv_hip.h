@@ -609,6 +609,48 @@ typedef struct slimkv_raw_pages_args {
 
 int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Raw rows of one decode step over vLLM pages, and flush_memory's raw and
+ * sink writes, in one launch for a batch of requests.  No single counterpart
+ * in the reference, which rebuilds each request's memory on its own
+ * (restore_memory, slimkv/vllm_plugin/paged_model.py:7-52: RawPages.read and
+ * BeaconPages.read_sink, paged_cache.py:102-127, 89-99), rotates the raw keys
+ * in fa2_decode.decode (slimkv/llama3/fa2_decode.py:107-142) and writes back
+ * in flush_memory (paged_model.py:55-84).
+ * For request b the dense raw set [sink | window rows | new token] goes to
+ * out_k / out_v [B, rows, Hkv, 128] (head stride 128): the sink (sink = 1) from
+ * the first 2 * Hkv * 128 elements of the root beacon page beacon_table[b, 0]
+ * (K, then V), window row j from the raw pages at position window_start[b] + j
+ * (j < raw_count[b]), the new token from new_k / new_v [B, Hkv, 128]; K rotated
+ * at positions[b, r] with the reference's bf16 steps (fp32 cos/sin tables
+ * [rope_rows, 128]), V copied.  Rows past sink + raw_count[b] + 1 are not
+ * written.  With `flush` set, afterwards: the new token's K/V (unrotated) into
+ * the raw page at position window_start[b] + raw_count[b] when that is below
+ * raw_write_end[b], and the root page's sink replaced by the new token where
+ * sink_update[b] (one byte per request) is non-zero.  Table entries follow
+ * torch's indexing; an entry outside the pool moves nothing for its row and
+ * stores SLIMKV_STATUS_BAD_PAGE in the optional status word.
+ * ---------------------------------------------------------------------- */
+typedef struct slimkv_paged_step_rows_args {
+    void* raw_pages; int64_t num_blocks, p_sblk, p_stok, p_skind, p_sh;
+    const int64_t* raw_table; int64_t rt_sb, rt_cols, block_size;
+    void* beacon_pages; int64_t num_pages, page_stride;
+    const int64_t* beacon_table; int64_t bt_sb;
+    const void* new_k; int64_t nk_sb;
+    const void* new_v; int64_t nv_sb;
+    const int64_t* window_start; const int32_t* raw_count;
+    const int64_t* positions; int64_t pos_sb;
+    const float* cos; const float* sin; int64_t rope_rows;
+    void* out_k; int64_t ok_sb, ok_sn;
+    void* out_v; int64_t ov_sb, ov_sn;
+    int64_t batch, rows, kv_heads, head_dim, sink;
+    int32_t flush;
+    const int32_t* raw_write_end; const uint8_t* sink_update;
+    int32_t* status;
+} slimkv_paged_step_rows_args;
+
+int slimkv_paged_step_rows(const slimkv_paged_step_rows_args* a, void* stream);
+
 /* The measurement probes (HBM and LDS read ceilings) are in
  * libslimkv_probe.so, declared in slimkv_probe.h. */
 

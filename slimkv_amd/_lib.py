@@ -204,6 +204,24 @@ RawPagesArgs = _struct('slimkv_raw_pages_args', [
     ('status', c_ptr), ('starts', c_ptr),
 ])
 
+PagedStepRowsArgs = _struct('slimkv_paged_step_rows_args', [
+    ('raw_pages', c_ptr), *_i64s('num_blocks', 'p_sblk', 'p_stok', 'p_skind', 'p_sh'),
+    ('raw_table', c_ptr), *_i64s('rt_sb', 'rt_cols', 'block_size'),
+    ('beacon_pages', c_ptr), *_i64s('num_pages', 'page_stride'),
+    ('beacon_table', c_ptr), ('bt_sb', c_i64),
+    ('new_k', c_ptr), ('nk_sb', c_i64),
+    ('new_v', c_ptr), ('nv_sb', c_i64),
+    ('window_start', c_ptr), ('raw_count', c_ptr),
+    ('positions', c_ptr), ('pos_sb', c_i64),
+    ('cos', c_ptr), ('sin', c_ptr), ('rope_rows', c_i64),
+    ('out_k', c_ptr), *_i64s('ok_sb', 'ok_sn'),
+    ('out_v', c_ptr), *_i64s('ov_sb', 'ov_sn'),
+    *_i64s('batch', 'rows', 'kv_heads', 'head_dim', 'sink'),
+    ('flush', c_i32),
+    ('raw_write_end', c_ptr), ('sink_update', c_ptr),
+    ('status', c_ptr),
+])
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     'slimkv_last_error': (ctypes.c_char_p, []),
@@ -241,9 +259,10 @@ SIGNATURES = {
                                                     ctypes.c_size_t, c_ptr]),
     'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
     'slimkv_raw_pages': (ctypes.c_int, [ctypes.POINTER(RawPagesArgs), c_ptr]),
+    'slimkv_paged_step_rows': (ctypes.c_int, [ctypes.POINTER(PagedStepRowsArgs), c_ptr]),
 }
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20

@@ -97,6 +97,112 @@ dim3 io_grid(int64_t items, int64_t batch) {
     return dim3((unsigned)((items + 255) / 256), (unsigned)batch);
 }
 
+// Rows of a decode step (slimkv_paged_step_rows): 16 lanes a (request, row,
+// KV head), 8 features a lane; the rotate-half partner (d +- 64) from lane
+// l ^ 8 of the same 16-lane row by a DPP rotation.  Every lane loads from a
+// valid address (dead lanes re-read a live row) so the rotation sees whole
+// rows; only live lanes store.
+__device__ __forceinline__ uint32_t step_ror8(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, true);
+}
+
+__global__ void __launch_bounds__(256)
+paged_step_rows_kernel(slimkv_paged_step_rows_args a) {
+    constexpr int D = 128;
+    const int64_t b = blockIdx.y;
+    const int lane16 = threadIdx.x & 15;
+    const int dd = lane16 * 8;
+    const int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+    const int64_t H = a.kv_heads;
+    const int64_t rc = a.raw_count[b];
+    const int64_t len = a.sink + rc + 1;
+    const int64_t r_item = item / H, h = item % H;
+    bool live = r_item < len && r_item < a.rows;
+    const int64_t r = live ? r_item : (len < a.rows ? len : a.rows) - 1;
+    const uint16_t* ksrc;
+    const uint16_t* vsrc;
+    uint16_t* page_row = nullptr;            // raw page row of the new token (flush), or null
+    uint16_t* sink_row = nullptr;            // root page of a sink row (flush)
+    const uint16_t* fallback = static_cast<const uint16_t*>(a.new_k) + b * a.nk_sb + h * D;
+    if (r < a.sink) {
+        const int64_t page = table_page(a.beacon_table[b * a.bt_sb], a.num_pages);
+        if (page < 0) {
+            if (live && lane16 == 0) report_bad_page(a.status);
+            live = false;
+            ksrc = vsrc = fallback;
+        } else {
+            uint16_t* root = static_cast<uint16_t*>(a.beacon_pages) + page * a.page_stride;
+            ksrc = root + h * D;
+            vsrc = root + H * D + h * D;
+            sink_row = root;
+        }
+    } else if (r < a.sink + rc) {
+        const int64_t pos = a.window_start[b] + (r - a.sink);
+        const int64_t col = pos >= 0 ? pos / a.block_size : -1;
+        const int64_t blk = col >= 0 && col < a.rt_cols ? table_page(a.raw_table[b * a.rt_sb + col], a.num_blocks) : -1;
+        if (blk < 0) {
+            if (live && lane16 == 0) report_bad_page(a.status);
+            live = false;
+            ksrc = vsrc = fallback;
+        } else {
+            const uint16_t* row = static_cast<const uint16_t*>(a.raw_pages) + blk * a.p_sblk + (pos % a.block_size) * a.p_stok;
+            ksrc = row + h * a.p_sh;
+            vsrc = row + a.p_skind + h * a.p_sh;
+        }
+    } else {
+        ksrc = fallback;
+        vsrc = static_cast<const uint16_t*>(a.new_v) + b * a.nv_sb + h * D;
+        const int64_t pos = a.window_start[b] + rc;
+        if (a.flush && pos < a.raw_write_end[b]) {
+            const int64_t col = pos >= 0 ? pos / a.block_size : -1;
+            const int64_t blk = col >= 0 && col < a.rt_cols ? table_page(a.raw_table[b * a.rt_sb + col], a.num_blocks)
+                                                             : -1;
+            if (blk < 0) {
+                if (live && lane16 == 0) report_bad_page(a.status);
+            } else {
+                page_row = static_cast<uint16_t*>(a.raw_pages) + blk * a.p_sblk + (pos % a.block_size) * a.p_stok;
+            }
+        }
+    }
+    const u32x4 xk = *reinterpret_cast<const u32x4*>(ksrc + dd);
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(vsrc + dd);
+    const int64_t prow = clamp_i64(a.positions[b * a.pos_sb + r], 0, a.rope_rows - 1) * D + dd;
+    const float4 c0 = *reinterpret_cast<const float4*>(a.cos + prow), c1 = *reinterpret_cast<const float4*>(a.cos + prow + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(a.sin + prow), s1 = *reinterpret_cast<const float4*>(a.sin + prow + 4);
+    const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float s8[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t xs[4] = {xk.x, xk.y, xk.z, xk.w};
+    const uint32_t pr[4] = {step_ror8(xk.x), step_ror8(xk.y), step_ror8(xk.z), step_ror8(xk.w)};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float sum[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const float v = hb ? hi_bf16(xs[e]) : lo_bf16(xs[e]);
+            float pt = hb ? hi_bf16(pr[e]) : lo_bf16(pr[e]);
+            if (lane16 < 8) pt = -pt;
+            sum[hb] = round_bf16_hw(v * round_bf16_hw(c8[2 * e + hb])) + round_bf16_hw(pt * round_bf16_hw(s8[2 * e + hb]));
+        }
+        o[e] = pack_bf16(sum[0], sum[1]);
+    }
+    if (!live) return;
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out_k) + b * a.ok_sb + r * a.ok_sn + h * D + dd) =
+        u32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out_v) + b * a.ov_sb + r * a.ov_sn + h * D + dd) = xv;
+    if (!a.flush) return;
+    if (page_row) {                              // the new token into its raw page, K before RoPE
+        *reinterpret_cast<u32x4*>(page_row + h * a.p_sh + dd) = xk;
+        *reinterpret_cast<u32x4*>(page_row + a.p_skind + h * a.p_sh + dd) = xv;
+    }
+    if (sink_row && a.sink_update[b]) {          // the new token becomes the sink (read above)
+        const uint16_t* nk = static_cast<const uint16_t*>(a.new_k) + b * a.nk_sb + h * D + dd;
+        const uint16_t* nv = static_cast<const uint16_t*>(a.new_v) + b * a.nv_sb + h * D + dd;
+        *reinterpret_cast<u32x4*>(sink_row + h * D + dd) = *reinterpret_cast<const u32x4*>(nk);
+        *reinterpret_cast<u32x4*>(sink_row + H * D + h * D + dd) = *reinterpret_cast<const u32x4*>(nv);
+    }
+}
+
 }  // namespace slimkv
 
 using namespace slimkv;
@@ -136,4 +242,27 @@ extern "C" int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream) {
     if (vec) hipLaunchKernelGGL(raw_pages_kernel<8>, grid, dim3(256), 0, st, *a);
     else hipLaunchKernelGGL(raw_pages_kernel<1>, grid, dim3(256), 0, st, *a);
     return check_hip(hipGetLastError(), "raw page kernel launch");
+}
+
+extern "C" int slimkv_paged_step_rows(const slimkv_paged_step_rows_args* a, void* stream) {
+    if (!a || !a->raw_pages || !a->raw_table || !a->new_k || !a->new_v || !a->window_start || !a->raw_count ||
+        !a->positions || !a->cos || !a->sin || !a->out_k || !a->out_v || (a->sink && (!a->beacon_pages || !a->beacon_table)) ||
+        (a->flush && (!a->raw_write_end || (a->sink && !a->sink_update))))
+        return fail(SLIMKV_EINVAL, "null pointer");
+    if (a->head_dim != 128) return fail(SLIMKV_EUNSUP, "paged step rows support head_dim 128");
+    if (a->batch < 0 || a->batch > 65535 || a->rows <= 0 || a->kv_heads <= 0 || a->sink < 0 || a->sink > 1 ||
+        a->block_size <= 0 || a->num_blocks <= 0 || a->rt_cols <= 0 || a->rt_sb < a->rt_cols || a->rope_rows <= 0 ||
+        (a->sink && (a->num_pages <= 0 || a->page_stride < 2 * a->kv_heads * 128)) ||
+        a->rows * a->kv_heads > ((int64_t)1 << 26))
+        return fail(SLIMKV_EINVAL, "invalid paged step rows sizes");
+    if (!all_multiple_of_8({a->p_sblk, a->p_stok, a->p_skind, a->p_sh, a->page_stride, a->nk_sb, a->nv_sb, a->ok_sb,
+                            a->ok_sn, a->ov_sb, a->ov_sn}) ||
+        !aligned16(a->raw_pages) || !aligned16(a->new_k) || !aligned16(a->new_v) || !aligned16(a->out_k) ||
+        !aligned16(a->out_v) || !aligned16(a->cos) || !aligned16(a->sin) || (a->sink && !aligned16(a->beacon_pages)))
+        return fail(SLIMKV_EINVAL, "paged step rows need 16-byte aligned rows (strides multiples of 8 elements)");
+    if (a->batch == 0) return SLIMKV_OK;
+    const int64_t threads = a->rows * a->kv_heads * 16;
+    hipLaunchKernelGGL(paged_step_rows_kernel, dim3((unsigned)((threads + 255) / 256), (unsigned)a->batch), dim3(256),
+                       0, static_cast<hipStream_t>(stream), *a);
+    return check_hip(hipGetLastError(), "paged step rows launch");
 }

@@ -828,6 +828,75 @@ def beacon_pages(pages, table, dense_k, dense_v, *, slots, key_rank, value_rank,
         check_status(status)
 
 
+def paged_step_rows(raw_pages, raw_table, beacon_pages, beacon_table, new_k, new_v, window_start, raw_count,
+                    positions, cos, sin, rows, sink, *, page_stride=None, flush=False, raw_write_end=None,
+                    sink_update=None, out_k=None, out_v=None, status=None):
+    """The dense raw set of one decode step for a batch of paged requests,
+    K rotated: out_k / out_v [B, rows, Hkv, 128] with the sink (from the root
+    beacon page beacon_table[:, 0]), the window rows (raw pages, positions
+    window_start[b] + j for j < raw_count[b]) and the new token (new_k / new_v
+    [B, Hkv, 128]) at rows 0, sink .. sink + raw_count - 1 and sink +
+    raw_count; K rotated at positions [B, >= rows] (fp32 cos/sin).  With
+    `flush`: flush_memory's writes afterwards (the new token into its raw page
+    below raw_write_end, the sink replaced where sink_update).  Rows past a
+    request's raw set are left unwritten.  Index errors as raw_pages."""
+    _need_device(raw_pages, beacon_pages, new_k, new_v, window_start, raw_count, positions, cos, sin)
+    _need_bf16(raw_pages, beacon_pages, new_k, new_v, out_k, out_v)
+    if raw_pages.dim() != 5 or raw_pages.shape[2] != 2 or raw_pages.stride(4) != 1:
+        raise ValueError('raw pages must be [blocks, block_size, 2, heads, dim] with contiguous dim')
+    blocks, block_size, _, H, D = raw_pages.shape
+    B = new_k.shape[0]
+    if new_k.shape != (B, H, D) or new_v.shape != (B, H, D) or new_k.stride()[1:] != (D, 1) or \
+            new_v.stride()[1:] != (D, 1):
+        raise ValueError('new_k / new_v must be [B, Hkv, D] with contiguous heads')
+    raw_table = _table(raw_table, raw_pages.device)
+    beacon_table = _table(beacon_table, raw_pages.device) if sink else None
+    if raw_table.shape[0] != B or (sink and beacon_table.shape[0] != B):
+        raise ValueError('one table row per request')
+    if cos.dtype != torch.float32 or sin.shape != cos.shape or cos.dim() != 2 or cos.shape[1] != D:
+        raise ValueError('RoPE tables must be fp32 [rows, head_dim]')
+    cos, sin = cos.contiguous(), sin.contiguous()
+    positions = positions.to(torch.int64)
+    positions = positions if positions.stride(-1) == 1 else positions.contiguous()
+    if positions.shape[0] != B or positions.shape[1] < rows:
+        raise ValueError('positions must be [B, >= rows]')
+    window_start = window_start.to(device=raw_pages.device, dtype=torch.int64).contiguous()
+    raw_count = raw_count.to(device=raw_pages.device, dtype=torch.int32).contiguous()
+    if out_k is None:
+        out_k = torch.empty(B, rows, H, D, dtype=BF16, device=raw_pages.device)
+    if out_v is None:
+        out_v = torch.empty_like(out_k)
+    for t in (out_k, out_v):
+        if t.shape != (B, rows, H, D) or t.stride()[2:] != (D, 1):
+            raise ValueError('outputs must be [B, rows, Hkv, D] with contiguous heads')
+    if flush:
+        raw_write_end = raw_write_end.to(device=raw_pages.device, dtype=torch.int32).contiguous()
+        if sink:
+            sink_update = sink_update.to(device=raw_pages.device, dtype=torch.uint8).contiguous()
+    status, owned = _status_word(status, raw_pages.device)
+    st = raw_pages.stride()
+    a = _lib.PagedStepRowsArgs(
+        raw_pages=_ptr(raw_pages), num_blocks=blocks, p_sblk=st[0], p_stok=st[1], p_skind=st[2], p_sh=st[3],
+        raw_table=_ptr(raw_table), rt_sb=raw_table.stride(0), rt_cols=raw_table.shape[1], block_size=block_size,
+        beacon_pages=_ptr(beacon_pages) if sink else None,
+        num_pages=beacon_pages.shape[0] if sink else 0,
+        page_stride=(beacon_pages.stride(0) if page_stride is None else page_stride) if sink else 0,
+        beacon_table=_ptr(beacon_table), bt_sb=beacon_table.stride(0) if sink else 0,
+        new_k=_ptr(new_k), nk_sb=new_k.stride(0), new_v=_ptr(new_v), nv_sb=new_v.stride(0),
+        window_start=_ptr(window_start), raw_count=_ptr(raw_count),
+        positions=_ptr(positions), pos_sb=positions.stride(0),
+        cos=_ptr(cos), sin=_ptr(sin), rope_rows=cos.shape[0],
+        out_k=_ptr(out_k), ok_sb=out_k.stride(0), ok_sn=out_k.stride(1),
+        out_v=_ptr(out_v), ov_sb=out_v.stride(0), ov_sn=out_v.stride(1),
+        batch=B, rows=rows, kv_heads=H, head_dim=D, sink=int(sink), flush=int(bool(flush)),
+        raw_write_end=_ptr(raw_write_end) if flush else None, sink_update=_ptr(sink_update) if flush and sink else None,
+        status=_ptr(status))
+    check(lib().slimkv_paged_step_rows(ctypes.byref(a), _lib.stream_handle(raw_pages.device)))
+    if owned:
+        check_status(status)
+    return out_k, out_v
+
+
 def raw_pages(pages, table, dense_k, dense_v, *, start, count, to_pages, lengths=None, status=None, starts=None):
     """Copy raw K/V between pages [blocks, block_size, 2, Hkv, D] and dense
     dense_k/dense_v [B, Hkv, count, D] (slimkv/vllm_plugin/paged_cache.py:102-127).

@@ -20,7 +20,8 @@ requests at once and touches the pages in place:
    P - P % window .. P - 1), the new token -- and its keys rotated at the
    memory's slot positions (sink 0, raw row j of the window at
    sink + history + j + j // ratio, the new token at the slot after the
-   memory), the bf16 RoPE of the reference;
+   memory), the bf16 RoPE of the reference; the same launch
+   (slimkv_paged_step_rows) makes step 5's writes;
 4. the fused latent decode with the beacon rows read through their pages
    (slimkv_paged_latent_decode; queries rotated in the kernel at the new
    token's slots, the raw query of an insertion step not seeing the new
@@ -105,13 +106,11 @@ def plan_paged_step(processed, window, ratio, sink, device):
             q_positions=q_pos, raw_positions=raw_pos,
             raw_lengths=torch.tensor([sink + rc + 1 for rc in g.raw_counts], dtype=torch.int32),
             window_start=torch.tensor([p - rc for p, rc in zip(P, g.raw_counts)], dtype=torch.int64),
-            window_end=torch.tensor(P, dtype=torch.int32),
-            new_row=torch.tensor([sink + rc for rc in g.raw_counts], dtype=torch.int64),
+            raw_count=torch.tensor(g.raw_counts, dtype=torch.int32),
             beacon_start=torch.tensor([p // ratio for p in P], dtype=torch.int64),
             lat_lengths=torch.tensor([p // ratio + size for p in P], dtype=torch.int32),
             raw_write_end=torch.tensor([p + (0 if c else 1) for p, c in zip(P, completes)], dtype=torch.int32),
-            raw_write_start=torch.tensor(P, dtype=torch.int64),
-            sink_update=torch.tensor([sink > 0 and h == 0 for h in g.histories], dtype=torch.bool),
+            sink_update=torch.tensor([sink > 0 and h == 0 for h in g.histories], dtype=torch.uint8),
             index=torch.tensor(idx, dtype=torch.int64))
         g.tensors = {k: v.to(device) for k, v in t.items()}
         g.max_raw = max_raw
@@ -175,44 +174,24 @@ def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_ta
                              value_rank=layout.value_rank, sink_elements=layout.sink_elements, start=0, count=1,
                              to_pages=True, lengths=t['lat_lengths'], status=status, starts=t['beacon_start'])
 
-    # 3. the raw set: sink (root page), the window's raw rows (raw pages), the new token
-    raw_k = torch.zeros(B, group.max_raw, kv_heads, dim, dtype=hidden.dtype, device=device)
-    raw_v = torch.zeros_like(raw_k)
-    if group.sink:
-        roots = beacon_pages[beacon_tables[:, 0], :layout.sink_elements]
-        raw_k[:, 0] = roots[:, :layout.raw_width].reshape(B, kv_heads, dim)
-        raw_v[:, 0] = roots[:, layout.raw_width:].reshape(B, kv_heads, dim)
-    window_rows = group.max_raw - group.sink - 1
-    if window_rows:
-        kernels.raw_pages(raw_pages, raw_tables, raw_k[:, group.sink:group.sink + window_rows].transpose(1, 2),
-                          raw_v[:, group.sink:group.sink + window_rows].transpose(1, 2), start=0,
-                          count=window_rows, to_pages=False, lengths=t['window_end'], status=status,
-                          starts=t['window_start'])
-    rows = torch.arange(B, device=device)
-    raw_k[rows, t['new_row']] = new_k[:, 0]
-    raw_v[rows, t['new_row']] = new_v[:, 0]
+    # 3. the raw set -- sink (root page), the window's raw rows (raw pages), the
+    # new token -- with K rotated at the memory's slots, and flush_memory's raw
+    # and sink writes (paged_model.py:55-84, memory.py:248-253), in one launch:
+    # the decode reads the dense raw set, not the pages it writes
     cos, sin = _tables(attention.rotary_emb, device)
-    raw_k_rot = kernels.rope_keys(raw_k.transpose(1, 2), cos, sin, t['raw_positions'],
-                                  torch.zeros(group.max_raw, dtype=torch.long, device=device), 0)
+    raw_k_rot, raw_v = kernels.paged_step_rows(
+        raw_pages, raw_tables, beacon_pages, beacon_tables, new_k[:, 0], new_v[:, 0], t['window_start'],
+        t['raw_count'], t['raw_positions'], cos, sin, group.max_raw, group.sink, flush=True,
+        raw_write_end=t['raw_write_end'], sink_update=t['sink_update'], status=status)
 
     # 4. the fused latent decode, beacon rows through their pages
     bd = is_block_diagonal(uk.weight, kv_heads) and is_block_diagonal(uv.weight, kv_heads)
     out, _ = kernels.paged_latent_decode(
-        q, raw_k_rot.transpose(1, 2), raw_v, beacon_pages, beacon_tables, t['lat_lengths'], group.max_beacons,
+        q, raw_k_rot, raw_v, beacon_pages, beacon_tables, t['lat_lengths'], group.max_beacons,
         layout, uk.weight, uv.weight, 1.0 / dim ** 0.5, up_k_bias=uk.bias, up_v_bias=uv.bias, block_diagonal=bd,
         lat_causal=bool(size), q_positions=t['q_positions'], cos=cos, sin=sin, raw_lengths=t['raw_lengths'],
         rows_total=group.rows_total, status=status)
 
-    # 5. flush_memory's raw and sink writes (paged_model.py:55-84, memory.py:248-253)
-    kernels.raw_pages(raw_pages, raw_tables, new_k.transpose(1, 2).contiguous(), new_v.transpose(1, 2).contiguous(),
-                      start=0, count=1, to_pages=True, lengths=t['raw_write_end'], status=status,
-                      starts=t['raw_write_start'])
-    if group.sink:
-        upd = t['sink_update']
-        sink_rows = torch.cat([new_k.reshape(B, -1), new_v.reshape(B, -1)], dim=1)
-        roots = beacon_tables[:, 0]
-        current = beacon_pages[roots, :layout.sink_elements]
-        beacon_pages[roots, :layout.sink_elements] = torch.where(upd[:, None], sink_rows, current)
     if own_status:
         kernels.check_status(status)
     output = out.reshape(B, L, attention.hidden_size)

@@ -46,7 +46,7 @@ def STRUCTS(_lib):
     return (_lib.AttentionArgs, _lib.LatentDecodeArgs, _lib.ReconstructArgs, _lib.ReconDecodeArgs,
             _lib.RopeDecodeArgs, _lib.PrefillRopeArgs, _lib.MergeArgs, _lib.PrefillAttentionArgs, _lib.DownProjectArgs,
             _lib.BeaconPagesArgs, _lib.RawPagesArgs, _lib.PagedLatentDecodeArgs, _lib.PageRows, _lib.LinearRowsArgs,
-            _lib.DecodeQKVArgs, _lib.EagerAttentionArgs)
+            _lib.DecodeQKVArgs, _lib.EagerAttentionArgs, _lib.PagedStepRowsArgs)
 
 
 def test_struct_layouts_match_header_field_order():
