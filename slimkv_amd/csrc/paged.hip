@@ -99,9 +99,9 @@ dim3 io_grid(int64_t items, int64_t batch) {
 
 // Rows of a decode step (slimkv_paged_step_rows): 16 lanes a (request, row,
 // KV head), 8 features a lane; the rotate-half partner (d +- 64) from lane
-// l ^ 8 of the same 16-lane row by a DPP rotation.  Every lane loads from a
-// valid address (dead lanes re-read a live row) so the rotation sees whole
-// rows; only live lanes store.
+// l ^ 8 of the same 16-lane row by a DPP rotation.  A row whose page entry is
+// bad still loads (a valid fallback row) so the rotation sees whole rows, and
+// stores nothing.
 __device__ __forceinline__ uint32_t step_ror8(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, true);
 }
@@ -117,8 +117,11 @@ paged_step_rows_kernel(slimkv_paged_step_rows_args a) {
     const int64_t rc = a.raw_count[b];
     const int64_t len = a.sink + rc + 1;
     const int64_t r_item = item / H, h = item % H;
-    bool live = r_item < len && r_item < a.rows;
-    const int64_t r = live ? r_item : (len < a.rows ? len : a.rows) - 1;
+    // a 16-lane row group past the request's raw set has nothing to do; the
+    // rotation's DPP reads only lanes of its own group, so it may leave
+    if (r_item >= len || r_item >= a.rows) return;
+    bool live = true;
+    const int64_t r = r_item;
     const uint16_t* ksrc;
     const uint16_t* vsrc;
     uint16_t* page_row = nullptr;            // raw page row of the new token (flush), or null

@@ -128,7 +128,7 @@ def _tables(rope, device):
 
 
 def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_tables, beacon_tables, block_size,
-                       status=None):
+                       status=None, raw_splits=0, lat_splits=0):
     """Attention output [B, 1 + size, hidden] of one layer's decode step for a
     group of requests (plan_paged_step), their pages read and written in
     place.  hidden [B, 1 + size, hidden_size] (the raw token, then the new
@@ -136,7 +136,8 @@ def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_ta
     page_elements] in BeaconPageLayout(block_size, ratio, key_rank,
     value_rank, Hkv * D); raw_tables / beacon_tables [B, T] int64 block tables
     of the group's requests.  Index errors land in `status` (device int32) or
-    raise IndexError after the step (one host synchronisation)."""
+    raise IndexError after the step (one host synchronisation).  raw_splits /
+    lat_splits: key splits of the decode (0: the library's plan)."""
     config = attention.config
     size, t = group.size, group.tensors
     B, L, _ = hidden.shape
@@ -190,7 +191,7 @@ def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_ta
         q, raw_k_rot, raw_v, beacon_pages, beacon_tables, t['lat_lengths'], group.max_beacons,
         layout, uk.weight, uv.weight, 1.0 / dim ** 0.5, up_k_bias=uk.bias, up_v_bias=uv.bias, block_diagonal=bd,
         lat_causal=bool(size), q_positions=t['q_positions'], cos=cos, sin=sin, raw_lengths=t['raw_lengths'],
-        rows_total=group.rows_total, status=status)
+        rows_total=group.rows_total, status=status, raw_splits=raw_splits, lat_splits=lat_splits)
 
     if own_status:
         kernels.check_status(status)
