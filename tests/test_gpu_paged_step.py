@@ -37,6 +37,7 @@ pytestmark = pytest.mark.gpu
 H, HKV, D, RANK = 8, 2, 128, 32
 HIDDEN = H * D
 WINDOW, RATIO, BLOCK, SINK = 32, 4, 16, 1
+DEFAULT = (WINDOW, RATIO, SINK)
 
 
 class RotaryEmbedding:          # the type name the decode path recognises
@@ -74,15 +75,16 @@ def _attention(device, bias=False, seed=0):
     return att, gen
 
 
-def _layout():
+def _layout(ratio=RATIO):
     from slimkv_amd.paged_cache import BeaconPageLayout
-    return BeaconPageLayout(BLOCK, RATIO, HKV * RANK, HKV * RANK, HKV * D)
+    return BeaconPageLayout(BLOCK, ratio, HKV * RANK, HKV * RANK, HKV * D)
 
 
-def _pool(device, processed, gen, steps=1, seed=0):
+def _pool(device, processed, gen, steps=1, seed=0, cfg=DEFAULT):
     """Random pages and permuted block tables with room for `steps` more
     tokens; table entries past a request's pages hold ids far outside the pool."""
-    layout = _layout()
+    RATIO = cfg[1]
+    layout = _layout(RATIO)
     cpu = torch.Generator().manual_seed(seed)
     last = [p + steps for p in processed]
     raw_need = [(n + BLOCK - 1) // BLOCK for n in last]
@@ -119,14 +121,16 @@ def _projections(att, hidden, size):
     return q, new_k, new_v, kl, vl
 
 
-def _oracle_request(att, layout, raw_np, beacon_np, raw_table, beacon_table, P, q, new_k, new_v, kl, vl, size):
+def _oracle_request(att, layout, raw_np, beacon_np, raw_table, beacon_table, P, q, new_k, new_v, kl, vl, size,
+                    cfg=DEFAULT):
     """Output [L, HIDDEN] of request's decode step: the memory read out of
     the pages before the step (restore_memory), the oracle's RoPE and latent
     layer (fa2_decode.decode)."""
+    WINDOW, RATIO, SINK = cfg
     rc, hist, beacons = op.restore_counts(P, WINDOW, RATIO)
     root = beacon_np[int(beacon_table[0])]
-    sink_k = root[:layout.raw_width].reshape(HKV, 1, D)
-    sink_v = root[layout.raw_width:layout.sink_elements].reshape(HKV, 1, D)
+    sink_k = root[:layout.raw_width].reshape(HKV, 1, D)[:, :SINK]
+    sink_v = root[layout.raw_width:layout.sink_elements].reshape(HKV, 1, D)[:, :SINK]
     blk, off = op.raw_indices(BLOCK, raw_table, P - rc, rc)
     raw_k = raw_np[blk, off, 0].transpose(1, 0, 2)                     # [HKV, rc, D]
     raw_v = raw_np[blk, off, 1].transpose(1, 0, 2)
@@ -156,8 +160,9 @@ def _oracle_request(att, layout, raw_np, beacon_np, raw_table, beacon_table, P, 
     return out.transpose(0, 2, 1, 3).reshape(L, HIDDEN)
 
 
-def _expected_pages(layout, raw, beacon, raw_tables, beacon_tables, processed, proj):
+def _expected_pages(layout, raw, beacon, raw_tables, beacon_tables, processed, proj, cfg=DEFAULT):
     """flush_memory's writes of one decode step on copies of the pages."""
+    WINDOW, RATIO, SINK = cfg
     raw, beacon = raw.clone(), beacon.clone()
     for b, P in enumerate(processed):
         new_k, new_v, kl, vl = proj[b]
@@ -171,16 +176,18 @@ def _expected_pages(layout, raw, beacon, raw_tables, beacon_tables, processed, p
             first = layout.sink_elements + (n % layout.slots) * layout.width
             beacon[page, first:first + layout.key_rank] = kl.reshape(-1)
             beacon[page, first + layout.key_rank:first + layout.width] = vl.reshape(-1)
-        if P < WINDOW:                                         # no history yet: the new token is the sink
+        if SINK and P < WINDOW:                                # no history yet: the new token is the sink
             root = int(beacon_tables[b, 0])
             beacon[root, :layout.sink_elements] = torch.cat([new_k.reshape(-1), new_v.reshape(-1)])
     return raw, beacon
 
 
-def _step(att, gen, device, layout, raw, beacon, raw_tables, beacon_tables, processed, check_pages=True):
+def _step(att, gen, device, layout, raw, beacon, raw_tables, beacon_tables, processed, check_pages=True,
+          cfg=DEFAULT):
     """One decode step of every request through paged_decode_layer; outputs
     against the oracle, pages against flush_memory's writes."""
     from slimkv_amd.paged_step import paged_decode_layer, plan_paged_step, step_size
+    WINDOW, RATIO, SINK = cfg
     sizes = [step_size(P, WINDOW, RATIO) for P in processed]
     hidden = [(torch.randn(1 + s, HIDDEN, generator=gen, device=device) * 0.5).to(torch.bfloat16) for s in sizes]
     proj = []
@@ -190,9 +197,9 @@ def _step(att, gen, device, layout, raw, beacon, raw_tables, beacon_tables, proc
     raw_np = to_np(raw).astype(np.float32)
     beacon_np = to_np(beacon).astype(np.float32)
     expected = [_oracle_request(att, layout, raw_np, beacon_np, to_np(raw_tables[b]), to_np(beacon_tables[b]), P,
-                                *proj[b], sizes[b]) for b, P in enumerate(processed)]
+                                *proj[b], sizes[b], cfg=cfg) for b, P in enumerate(processed)]
     want_raw, want_beacon = _expected_pages(layout, raw, beacon, raw_tables, beacon_tables, processed,
-                                            [p[1:] for p in proj])
+                                            [p[1:] for p in proj], cfg=cfg)
     groups = plan_paged_step(processed, WINDOW, RATIO, SINK, device)
     assert sorted(i for g in groups for i in g.index) == list(range(len(processed)))
     for g in groups:
@@ -247,3 +254,14 @@ def test_paged_step_bad_write_block(device):
     blk = int(raw_tables[1, 40 // BLOCK])
     changed = (raw.view(torch.int16) != before.view(torch.int16)).flatten(1).any(1).nonzero().flatten().tolist()
     assert changed == [blk]
+
+
+@pytest.mark.parametrize('cfg', [(32, 8, 0), (64, 16, 1)])
+def test_paged_step_other_configurations(device, cfg):
+    """No sink (every raw row of the memory is a window row) and a longer
+    window at a higher ratio: the same checks over one step of a mixed batch."""
+    window, ratio, sink = cfg
+    processed = [1, 7, 15, 16, 31, 33, 47, 63, 64, 95, 150, 255]
+    att, gen = _attention(device, False, seed=31 + window)
+    layout, raw, beacon, raw_tables, beacon_tables = _pool(device, processed, gen, seed=6, cfg=cfg)
+    _step(att, gen, device, layout, raw, beacon, raw_tables, beacon_tables, processed, cfg=cfg)
