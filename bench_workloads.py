@@ -547,6 +547,12 @@ def paged(args):
     attend_s = staged_attend_seconds(torch, [lambda st: paged_call(st, ws)] * 4, _STAGE_PROLOGUE, _STAGE_ATTEND)
     del ws
     kernels.check_status(status)
+    # the access pattern's own ceiling: the beacon slots of every page the
+    # decode reads (2 KB a page at its page offset), in table order
+    ids = torch.cat([pc['tables_cpu'][b, :(n + layout.slots - 1) // layout.slots] for b, n in enumerate(nb)]).to(dev)
+    gather = gather_probe(torch, pool, ids, pool.stride(0) * 2, layout.sink_elements * 2,
+                          layout.slots * layout.width * 2)
+    del ids
     algo = sum(n * 2 * R * 2 + c * HKV * D * 2 * 2 for n, c in zip(nb, raw_count)) + NSEQ * 2 * HQ * D * 2 \
         + 2 * HKV * D * R * 2
     split_bytes = sum(n * 2 * R * 2 + c * HKV * D * 2 * 2 for n, c in zip(nb, raw_count)) + NSEQ * HQ * D * 2 \
@@ -563,7 +569,11 @@ def paged(args):
                                'frac': round(achieved / HBM_PEAK_GBPS, 4), 'traffic': PAGED_TRAFFIC_BYTES,
                                'traffic_source': TRAFFIC_SOURCE,
                                'kernel': 'split_kernel<KA,8,paged,0,raw pages> (attend stage)', 'avg_us': round(attend_s * 1e6, 2),
-                               'bytes_per_launch': split_bytes},
+                               'bytes_per_launch': split_bytes,
+                               'ceiling': {'gather_gbps': max(gather.values()), 'by_waves_per_cu': gather,
+                                           'frac_of_gather': round(achieved / max(gather.values()), 4),
+                                           'source': 'slimkv_probe_gather_read (libslimkv_probe.so): the 2 KB '
+                                                     'beacon slots of every page the decode reads, in table order'}},
                      raw_gather_path_gbps=round(algo / raw_gather_s / 1e9, 1),
                      raw_gather_path_ms=round(raw_gather_s * 1e3, 4),
                      restore_path_gbps=round(algo / restore_s / 1e9, 1), restore_path_ms=round(restore_s * 1e3, 4),
@@ -653,6 +663,34 @@ def ceiling_probe(torch, dev, gib=4, reps=10):
     del buf
     best = {kind: max(v for k, v in rates.items() if k.startswith(kind)) for kind in ('plain', 'nt')}
     return rates, best
+
+
+def gather_probe(torch, buf, ids, stride_bytes, offset_bytes, chunk_bytes, reps=10):
+    """Read rate of slimkv_probe_gather_read over `buf` at the chunks `ids`
+    (device int64), for 8 to 64 resident waves a CU: {config: GB/s}."""
+    import ctypes
+    from slimkv_amd import _lib
+    dev = buf.device
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(cu * 16 * 256, dtype=torch.int32, device=dev)
+    lib, stream = _lib.probe_lib(), _lib.stream_handle(dev)
+    nbytes = buf.numel() * buf.element_size()
+    rates = {}
+    for waves in (8, 16, 32, 64):
+        def launch():
+            _lib.probe_check(lib.slimkv_probe_gather_read(
+                ctypes.c_void_p(buf.data_ptr()), nbytes, ctypes.c_void_p(ids.data_ptr()), ids.numel(), stride_bytes,
+                offset_bytes, chunk_bytes, ctypes.c_void_p(sink.data_ptr()), sink.numel(), waves, stream))
+        for _ in range(2):
+            launch()
+        a, b = _events(torch)
+        a.record()
+        for _ in range(reps):
+            launch()
+        b.record()
+        torch.cuda.synchronize()
+        rates[f'w{waves}'] = round(ids.numel() * chunk_bytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9, 1)
+    return rates
 
 
 def lds_probe(torch, dev, iters=256, reps=5):

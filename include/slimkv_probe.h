@@ -21,6 +21,18 @@ const char* slimkv_probe_last_error(void);
 int slimkv_probe_stream_read(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_words,
                              int32_t waves_per_cu, int32_t depth, int32_t non_temporal, void* stream);
 
+/* HBM read rate of scattered chunks (the access pattern of rows read through
+ * a block table): chunk i is `chunk_bytes` (a multiple of 16, at most 16384)
+ * at src + ids[i] * stride_bytes + offset_bytes, i < count (ids int64 on the
+ * device; a chunk that would end past `bytes` reads chunk 0 instead).  The
+ * chunks' 16-byte pieces are dealt grid-stride over waves_per_cu resident
+ * waves a CU (consecutive lanes, consecutive pieces), four loads in flight a
+ * thread; one folded word a thread to sink (grid * 256 words).  Bytes read =
+ * count * chunk_bytes. */
+int slimkv_probe_gather_read(const void* src, int64_t bytes, const int64_t* ids, int64_t count, int64_t stride_bytes,
+                             int64_t offset_bytes, int32_t chunk_bytes, uint32_t* sink, int64_t sink_words,
+                             int32_t waves_per_cu, void* stream);
+
 /* LDS read rate of a CU: workgroups_per_cu (1 or 2) workgroups of 256
  * threads a CU, each with 64 KB of LDS, read it `iters` x 16 times a lane,
  * `width` (8 or 16) bytes a read, conflict free; one word a thread to sink

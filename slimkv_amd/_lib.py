@@ -299,6 +299,8 @@ PROBE_SIGNATURES = {
     'slimkv_probe_last_error': (ctypes.c_char_p, []),
     'slimkv_probe_stream_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
     'slimkv_probe_lds_read': (ctypes.c_int, [c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
+    'slimkv_probe_gather_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i32, c_ptr, c_i64,
+                                                c_i32, c_ptr]),
 }
 
 

@@ -15,6 +15,10 @@
 //   contiguous 512 B or 1 KB, bank-conflict free, as the prefill kernel's
 //   operand reads are laid out -- `iters` passes of 16 reads, and folds the
 //   words into one per lane.  Bytes read = grid threads x iters x 16 x width.
+// * slimkv_probe_gather_read: the HBM read rate of scattered chunks at table
+//   offsets (a chunk a page, as a paged decode reads its rows): the chunks'
+//   16-byte pieces dealt grid-stride, four in flight a thread, each piece's
+//   chunk id looked up first (as a decode looks up its page ids).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -106,9 +110,58 @@ __global__ void __launch_bounds__(256) lds_read_kernel(int iters, uint32_t* __re
     sink[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
 }
 
+__global__ void __launch_bounds__(256) gather_read_kernel(const uint8_t* __restrict__ src, int64_t bytes,
+                                                          const int64_t* __restrict__ ids, int64_t pieces,
+                                                          int64_t per_chunk, int64_t stride, int64_t offset,
+                                                          int64_t chunk, uint32_t* __restrict__ sink) {
+    constexpr int DEPTH = 4;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    for (int64_t base = tid; base < pieces; base += step * DEPTH) {
+        int64_t at[DEPTH];
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int64_t p = base + d * step;
+            const int64_t c = (p < pieces ? p : 0) / per_chunk;
+            int64_t start = ids[c] * stride + offset;
+            if (start < 0 || start + chunk > bytes) start = offset;          // out of the buffer: chunk 0
+            at[d] = p < pieces ? start + (p % per_chunk) * 16 : -1;
+        }
+        u32x4 v[DEPTH];
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d)
+            v[d] = *reinterpret_cast<const u32x4*>(src + (at[d] >= 0 ? at[d] : offset));
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d)
+            if (at[d] >= 0) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+    }
+    sink[tid] = acc;
+}
+
 }  // namespace
 
 extern "C" const char* slimkv_probe_last_error(void) { return g_probe_error.c_str(); }
+
+extern "C" int slimkv_probe_gather_read(const void* src, int64_t bytes, const int64_t* ids, int64_t count,
+                                        int64_t stride_bytes, int64_t offset_bytes, int32_t chunk_bytes,
+                                        uint32_t* sink, int64_t sink_words, int32_t waves_per_cu, void* stream) {
+    if (!src || !ids || !sink || (reinterpret_cast<uintptr_t>(src) & 15) || count <= 0)
+        return probe_fail("gather probe needs a 16-byte aligned buffer and chunk ids");
+    if (chunk_bytes < 16 || chunk_bytes > 16384 || (chunk_bytes & 15) || (stride_bytes & 15) || (offset_bytes & 15) ||
+        offset_bytes < 0 || offset_bytes + chunk_bytes > bytes)
+        return probe_fail("gather probe: chunk, stride and offset multiples of 16, chunk 16..16384 inside the buffer");
+    if (waves_per_cu < 4 || waves_per_cu % 4 || waves_per_cu > 64)
+        return probe_fail("waves_per_cu must be a multiple of 4 in [4, 64]");
+    const int grid = cu_count() * waves_per_cu / 4;
+    if (grid <= 0) return probe_fail("no device");
+    if (sink_words < (int64_t)grid * 256) return probe_fail("sink too small (grid * 256 words)");
+    const int64_t per_chunk = chunk_bytes / 16;
+    hipLaunchKernelGGL(gather_read_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint8_t*>(src), bytes, ids, count * per_chunk, per_chunk, stride_bytes,
+                       offset_bytes, (int64_t)chunk_bytes, sink);
+    return probe_hip(hipGetLastError(), "gather read probe launch");
+}
 
 extern "C" int slimkv_probe_stream_read(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_words,
                                         int32_t waves_per_cu, int32_t depth, int32_t non_temporal, void* stream) {
