@@ -139,38 +139,61 @@ def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_ta
     raise IndexError after the step (one host synchronisation).  raw_splits /
     lat_splits: key splits of the decode (0: the library's plan)."""
     config = attention.config
-    size, t = group.size, group.tensors
+    size = group.size
     B, L, _ = hidden.shape
     if L != 1 + size or B != len(group.index):
         raise ValueError('hidden must be [requests of the group, 1 + size, hidden]')
-    if not getattr(config, 'beacon_skip_rope_for_beacon_k', False):
-        raise ValueError('paged latent decode reads beacon K without RoPE (model.py:45-46)')
-    uk, uv = attention.beacon_k_up_proj, attention.beacon_v_up_proj
     heads, kv_heads, dim = attention.num_heads, attention.num_key_value_heads, attention.head_dim
-    layout = BeaconPageLayout(block_size, group.ratio, uk.in_features, uv.in_features, kv_heads * dim)
-    device = hidden.device
-    own_status = status is None
-    if own_status:
-        status = torch.zeros(1, dtype=torch.int32, device=device)
-    raw_tables = raw_tables.to(device=device, dtype=torch.long)
-    beacon_tables = beacon_tables.to(device=device, dtype=torch.long)
-
-    # 1. projections of the step (fa2_decode.py:88-100)
+    # projections of the step (fa2_decode.py:88-100)
     raw_hidden = hidden[:, :1]
     q = attention.q_proj(hidden)
     if size and 'q' in config.beacon_param:
         q = torch.cat([q[:, :1], attention.beacon_q_proj(hidden[:, 1:])], dim=1)
     q = q.reshape(B, L, heads, dim)
-    new_k = attention.k_proj(raw_hidden).reshape(B, 1, kv_heads, dim)
-    new_v = attention.v_proj(raw_hidden).reshape(B, 1, kv_heads, dim)
+    new_k = attention.k_proj(raw_hidden).reshape(B, kv_heads, dim)
+    new_v = attention.v_proj(raw_hidden).reshape(B, kv_heads, dim)
+    kl = vl = None
+    if size:
+        kl, vl = _beacon_latents(attention, hidden[:, 1:])
+    own_status = status is None
+    if own_status:
+        status = torch.zeros(1, dtype=torch.int32, device=hidden.device)
+    out = _attend(attention, q, new_k, new_v, kl, vl, group, raw_pages, beacon_pages, raw_tables, beacon_tables,
+                  block_size, status, raw_splits, lat_splits)
+    if own_status:
+        kernels.check_status(status)
+    output = out.reshape(B, L, attention.hidden_size)
+    # roles of the step's rows (raw token, then its beacon) for the beacon O projection
+    roles = torch.arange(L, device=hidden.device) if size else None
+    return attention.o_proj_with_beacon(output, size, roles)
+
+
+def _beacon_latents(attention, beacon_hidden):
+    """The new beacons' K/V latents [B, 1, rank] (the module's down projections)."""
+    shared = attention._use_shared_kv_down_proj()
+    kd = attention.beacon_kv_down_proj if shared else attention.beacon_k_down_proj
+    vd = attention.beacon_kv_down_proj if shared else attention.beacon_v_down_proj
+    return kd(beacon_hidden).contiguous(), vd(beacon_hidden).contiguous()
+
+
+def _attend(attention, q, new_k, new_v, kl, vl, group, raw_pages, beacon_pages, raw_tables, beacon_tables,
+            block_size, status, raw_splits, lat_splits):
+    """Steps 2-5 of the module docstring for one group: q [B, L, Hq, D],
+    new_k / new_v [B, Hkv, D], kl / vl [B, 1, rank] on an insertion step.
+    Returns the attention output [B, L, Hq, D]."""
+    config = attention.config
+    size, t = group.size, group.tensors
+    if not getattr(config, 'beacon_skip_rope_for_beacon_k', False):
+        raise ValueError('paged latent decode reads beacon K without RoPE (model.py:45-46)')
+    uk, uv = attention.beacon_k_up_proj, attention.beacon_v_up_proj
+    kv_heads, dim = attention.num_key_value_heads, attention.head_dim
+    layout = BeaconPageLayout(block_size, group.ratio, uk.in_features, uv.in_features, kv_heads * dim)
+    device = q.device
+    raw_tables = raw_tables.to(device=device, dtype=torch.long)
+    beacon_tables = beacon_tables.to(device=device, dtype=torch.long)
 
     # 2. the new beacon's latents appended at beacon P // ratio
     if size:
-        shared = attention._use_shared_kv_down_proj()
-        kd = attention.beacon_kv_down_proj if shared else attention.beacon_k_down_proj
-        vd = attention.beacon_kv_down_proj if shared else attention.beacon_v_down_proj
-        kl = kd(hidden[:, 1:]).contiguous()
-        vl = vd(hidden[:, 1:]).contiguous()
         kernels.beacon_pages(beacon_pages, beacon_tables, kl, vl, slots=layout.slots, key_rank=layout.key_rank,
                              value_rank=layout.value_rank, sink_elements=layout.sink_elements, start=0, count=1,
                              to_pages=True, lengths=t['lat_lengths'], status=status, starts=t['beacon_start'])
@@ -181,7 +204,7 @@ def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_ta
     # the decode reads the dense raw set, not the pages it writes
     cos, sin = _tables(attention.rotary_emb, device)
     raw_k_rot, raw_v = kernels.paged_step_rows(
-        raw_pages, raw_tables, beacon_pages, beacon_tables, new_k[:, 0], new_v[:, 0], t['window_start'],
+        raw_pages, raw_tables, beacon_pages, beacon_tables, new_k, new_v, t['window_start'],
         t['raw_count'], t['raw_positions'], cos, sin, group.max_raw, group.sink, flush=True,
         raw_write_end=t['raw_write_end'], sink_update=t['sink_update'], status=status)
 
@@ -192,10 +215,4 @@ def paged_decode_layer(attention, hidden, group, raw_pages, beacon_pages, raw_ta
         layout, uk.weight, uv.weight, 1.0 / dim ** 0.5, up_k_bias=uk.bias, up_v_bias=uv.bias, block_diagonal=bd,
         lat_causal=bool(size), q_positions=t['q_positions'], cos=cos, sin=sin, raw_lengths=t['raw_lengths'],
         rows_total=group.rows_total, status=status, raw_splits=raw_splits, lat_splits=lat_splits)
-
-    if own_status:
-        kernels.check_status(status)
-    output = out.reshape(B, L, attention.hidden_size)
-    # roles of the step's rows (raw token, then its beacon) for the beacon O projection
-    roles = torch.arange(L, device=device) if size else None
-    return attention.o_proj_with_beacon(output, size, roles)
+    return out
