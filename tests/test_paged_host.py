@@ -60,3 +60,37 @@ def test_pages_constructor_checks_without_gpu():
         RawPages(torch.zeros(8, 4, 3, 2, 3, dtype=torch.bfloat16))
     with pytest.raises(ValueError):                                              # no CPU compute path
         pages.read(torch.tensor([0, 1, 2]), 4)
+
+
+def test_paged_step_plan_matches_oracle():
+    """plan_paged_step's per-request counts and slot positions against the
+    oracle's restatement of restore_memory (paged_model.py:12-35), the decode
+    key positions of fa2_decode.decode (fa2_decode.py:122-126), the insertion
+    rule (memory.py:122-124: a beacon after every `ratio` raw tokens, so at
+    (P + 1) % ratio == 0) and flush_memory's raw start (paged_model.py:58-59)."""
+    import numpy as np
+    from oracle import rope as orope
+    from slimkv_amd.paged_step import plan_paged_step
+    for window, ratio, sink in [(32, 4, 1), (1024, 8, 1), (64, 16, 0)]:
+        for P in [1, 2, 3, 7, 15, 16, window - 1, window, window + 1, 3 * window - 1, 5 * window + 7, 100_001]:
+            (g,) = plan_paged_step([P], window, ratio, sink, 'cpu')
+            t = {k: v[0] for k, v in g.tensors.items()}
+            rc, hist, beacons = opaged.restore_counts(P, window, ratio)
+            roles = opaged.window_roles(rc, ratio)
+            size = int((P + 1) % ratio == 0)
+            mem = sink + hist + roles.size
+            keys = sink + rc + 1
+            want = orope.decode_key_positions(keys, sink, hist, np.nonzero(roles == 0)[0], mem)
+            assert g.size == size, (window, ratio, P)
+            assert t['raw_positions'][:keys].tolist() == want.tolist(), (window, ratio, P)
+            assert t['q_positions'].tolist() == list(range(mem, mem + 1 + size))
+            assert (int(t['raw_lengths']), int(t['raw_count']), int(t['window_start'])) == (keys, rc, P - rc)
+            assert (int(t['beacon_start']), int(t['lat_lengths'])) == (beacons, beacons + size)
+            raw_start = opaged.flush_raw_start(P, P + 1, window)
+            assert int(t['raw_write_end']) == (P + 1 if P + 1 > raw_start else P)
+            assert bool(t['sink_update']) == (sink > 0 and hist == 0)
+            assert (g.max_raw, g.max_beacons, g.rows_total) == (keys, beacons + size, beacons + size)
+    with pytest.raises(ValueError):
+        plan_paged_step([5], 24, 4, 1, 'cpu')                  # window not a multiple of 16
+    with pytest.raises(ValueError):
+        plan_paged_step([0], 32, 4, 1, 'cpu')                  # a decode step follows a prefill
