@@ -23,6 +23,11 @@
 //                   same order (one 16-byte read).  The query stays in the
 //                   lane, so softmax statistics never cross lanes except for
 //                   the two-step max/sum over grp.
+//   l  = 1 . P^T    The row sums come from the matrix cores too: one more
+//                   MFMA per P^T operand with an A whose row 0 is all ones, so
+//                   the denominator sums the same bf16 P the numerator uses
+//                   (32 fewer dependent VALU adds a tile: C3 step 1.879 ->
+//                   1.833 ms, same box).
 //
 // Scheduling.  Workgroups sharing a KV head (the g query heads of one group
 // for one query block) are placed on the same XCD so the group's K/V tiles
@@ -199,7 +204,9 @@ prefill_kernel(PrefillParams p) {
     const int h = kvh * g + slot % g;
     const int n = p.seqlens ? max(0, min(p.seqlens[b], p.Nk)) : p.Nk;
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index in a scalar register: the full-tile test below is then a
+    // scalar branch, and the masked path's index arithmetic stays inside it
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, grp = lane >> 4;
     const int q0 = qb * kQRows + wave * 32;
     const int shift = n - p.Lq;
@@ -240,7 +247,11 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) o[md][nt] = v4f{0.f, 0.f, 0.f, 0.f};
     float m[2] = {kNegInf, kNegInf};
-    float l[2] = {0.f, 0.f};
+    // row sums of P on the matrix cores: A row 0 all ones, so row 0 of the
+    // accumulator (lanes of lane group 0, element 0) is the sum over keys
+    v4f lacc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    const uint32_t one2 = col == 0 ? 0x3f803f80u : 0u;
+    const u32x4 ones = u32x4{one2, one2, one2, one2};
 
     const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)kvh * p.k_sh;
     const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)kvh * p.v_sh;
@@ -291,8 +302,6 @@ prefill_kernel(PrefillParams p) {
         u32x4 pb[2][2];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const int qi = q0 + 16 * nt + col;
-            const int last = p.causal ? min(qi + shift, n - 1) : n - 1;
             float mx = kNegInf;
             // raw scores: the scale (> 0) is applied inside the exponent's FMA
             if (full) {
@@ -301,11 +310,14 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nt][i]);
             } else {
+                // key k0 + 16 mt + 4 grp + i is visible while 16 mt + i <= lim
+                const int qi = q0 + 16 * nt + col;
+                const int lim = (p.causal ? min(qi + shift, n - 1) : n - 1) - k0 - 4 * grp;
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float x = k0 + 16 * mt + 4 * grp + i <= last ? s[mt][nt][i] : kNegInf;
+                        const float x = 16 * mt + i <= lim ? s[mt][nt][i] : kNegInf;
                         s[mt][nt][i] = x;
                         mx = fmaxf(mx, x);
                     }
@@ -315,21 +327,16 @@ prefill_kernel(PrefillParams p) {
             const float base = m_new == kNegInf ? 0.f : m_new;
             const float alpha = fast_exp2(m[nt] - base);
             m[nt] = m_new;
-            float sum = 0.f;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float e = fast_exp2(__builtin_fmaf(s[mt][nt][i], p.scale_log2, -base));
-                    s[mt][nt][i] = e;
-                    sum += e;
-                }
-            l[nt] = l[nt] * alpha + sum;
+                for (int i = 0; i < 4; ++i) s[mt][nt][i] = fast_exp2(__builtin_fmaf(s[mt][nt][i], p.scale_log2, -base));
             // once the running maxima settle (most tiles of a long window) no
             // column's alpha moves off 1, and the wave skips the rescale
             if (__ballot(alpha != 1.f)) {
 #pragma unroll
                 for (int md = 0; md < 8; ++md) o[md][nt] *= alpha;
+                lacc[nt] *= alpha;
             }
 #pragma unroll
             for (int ss = 0; ss < 2; ++ss)
@@ -347,6 +354,8 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) o[md][nt] = mfma32(a, pb[ss][nt], o[md][nt]);
             }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) lacc[nt] = mfma32(ones, pb[ss][nt], lacc[nt]);
         }
         // tile t + 1 (in registers) into the other buffer, then fetch tile t + 2;
         // the barrier orders this write after every wave's reads of tile t - 1
@@ -360,8 +369,7 @@ prefill_kernel(PrefillParams p) {
 
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        float tot = l[nt];
-        tot = rows_sum(tot);
+        const float tot = rows_sum(lacc[nt][0]);
         const float inv = tot > 0.f ? 1.f / tot : 0.f;
         const int qi = q0 + 16 * nt + col;
         if (qi >= p.Lq) continue;
