@@ -314,8 +314,10 @@ def main():
     # The read rate a plain grid-stride stream reaches on this GPU (the
     # slimkv_probe_stream_read ceiling probe), to read the split kernel's rate
     # against beside the 8 TB/s peak.
-    from bench_workloads import ceiling_probe
+    from bench_workloads import ceiling_probe, launch_floor_probe
     _, ceiling = ceiling_probe(torch, device)
+    # what a launch and its hand-off cost with no work (the combine's grid)
+    floor_us = launch_floor_probe(torch, device, workgroups=B * HQ)
     dom = 32 if 32 in durations else max(durations, key=lambda r: len(durations[r]))
     dur = durations[dom]
     dur_avg = sum(dur) / len(dur)
@@ -330,6 +332,7 @@ def main():
                 'ceiling': {'plain_gbps': ceiling['plain'], 'nt_gbps': ceiling['nt'],
                             'frac_of_plain': round(achieved / ceiling['plain'], 4),
                             'source': 'slimkv_probe_stream_read over 4 GiB, best configuration, same run'},
+                'launch_floor_us': floor_us,
                 'avg_us_by_rank': {str(r): round(sum(v) / len(v) * 1e6, 2) for r, v in sorted(durations.items())},
                 'attend_stage_us_by_rank': {str(r): round(v * 1e6, 2) for r, v in sorted(staged.items())}}
 

@@ -693,6 +693,24 @@ def gather_probe(torch, buf, ids, stride_bytes, offset_bytes, chunk_bytes, reps=
     return rates
 
 
+def launch_floor_probe(torch, dev, workgroups=512, launches=64):
+    """Microseconds a launch of slimkv_probe_touch (`workgroups` one-wave
+    workgroups, one store each) costs when `launches` of them are captured back
+    to back in a graph: the dispatch-and-hand-off floor every launch of a
+    decode layer pays.  512 workgroups is the batch-16 combine's grid."""
+    import ctypes
+    from slimkv_amd import _lib
+    sink = torch.zeros(workgroups, dtype=torch.int32, device=dev)
+    lib = _lib.probe_lib()
+
+    def body():
+        stream = _lib.stream_handle(dev)
+        for _ in range(launches):
+            _lib.probe_check(lib.slimkv_probe_touch(ctypes.c_void_p(sink.data_ptr()), sink.numel(), workgroups,
+                                                    stream))
+    return round(_timed_graph(torch, body) / launches * 1e6, 2)
+
+
 def lds_probe(torch, dev, iters=256, reps=5):
     """LDS read rate of a CU (slimkv_probe_lds_read): 8- and 16-byte reads, one
     and two 256-thread workgroups a CU.  {config: GB/s a CU} and, at the shader
@@ -727,8 +745,9 @@ def lds_probe(torch, dev, iters=256, reps=5):
 def ceiling(args):
     """The HBM read ceiling of this GPU: a grid-stride stream of 16-byte loads
     (slimkv_probe_stream_read) over 4 GiB, the best of several resident-wave /
-    loads-in-flight configurations, plain and non-temporal; and the LDS read
-    rate of a CU (slimkv_probe_lds_read)."""
+    loads-in-flight configurations, plain and non-temporal; the LDS read rate
+    of a CU (slimkv_probe_lds_read); and the per-launch floor of a graph of
+    back-to-back launches (slimkv_probe_touch)."""
     import torch
     dev = torch.device('cuda:0')
     t0 = time.perf_counter()
@@ -739,7 +758,7 @@ def ceiling(args):
                           'configs': [list(c) for c in CEILING_CONFIGS]},
                    hbm_frac=round(best['plain'] / HBM_PEAK_GBPS, 4), nt_gbps=best['nt'],
                    nt_frac=round(best['nt'] / HBM_PEAK_GBPS, 4), rates=rates, lds=lds_probe(torch, dev),
-                   clocks=_replays_clocks())
+                   launch_floor_us=launch_floor_probe(torch, dev), clocks=_replays_clocks())
 
 
 def _replays_clocks():

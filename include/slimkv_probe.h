@@ -41,6 +41,12 @@ int slimkv_probe_gather_read(const void* src, int64_t bytes, const int64_t* ids,
 int slimkv_probe_lds_read(uint32_t* sink, int64_t sink_words, int32_t workgroups_per_cu, int32_t iters,
                           int32_t width, void* stream);
 
+/* The per-launch floor: `workgroups` (1..65536) one-wave workgroups, each
+ * storing one word to sink (at least `workgroups` words).  Timed as graph
+ * replays of back-to-back launches it gives the cost of a launch and its
+ * hand-off alone. */
+int slimkv_probe_touch(uint32_t* sink, int64_t sink_words, int32_t workgroups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

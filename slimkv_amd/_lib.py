@@ -301,6 +301,7 @@ PROBE_SIGNATURES = {
     'slimkv_probe_lds_read': (ctypes.c_int, [c_ptr, c_i64, c_i32, c_i32, c_i32, c_ptr]),
     'slimkv_probe_gather_read': (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i32, c_ptr, c_i64,
                                                 c_i32, c_ptr]),
+    'slimkv_probe_touch': (ctypes.c_int, [c_ptr, c_i64, c_i32, c_ptr]),
 }
 
 

@@ -19,6 +19,9 @@
 //   offsets (a chunk a page, as a paged decode reads its rows): the chunks'
 //   16-byte pieces dealt grid-stride, four in flight a thread, each piece's
 //   chunk id looked up first (as a decode looks up its page ids).
+// * slimkv_probe_touch: the per-launch floor.  One wave a workgroup, one store
+//   a wave; captured back to back in a graph, a launch costs its dispatch and
+//   hand-off and nothing else, the floor every kernel of a decode layer pays.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -139,6 +142,10 @@ __global__ void __launch_bounds__(256) gather_read_kernel(const uint8_t* __restr
     sink[tid] = acc;
 }
 
+__global__ void __launch_bounds__(64) touch_kernel(uint32_t* __restrict__ sink) {
+    if (threadIdx.x == 0) sink[blockIdx.x] = blockIdx.x;
+}
+
 }  // namespace
 
 extern "C" const char* slimkv_probe_last_error(void) { return g_probe_error.c_str(); }
@@ -198,4 +205,11 @@ extern "C" int slimkv_probe_lds_read(uint32_t* sink, int64_t sink_words, int32_t
     if (width == 16) hipLaunchKernelGGL(lds_read_kernel<16>, dim3(grid), dim3(256), 0, st, iters, sink);
     else hipLaunchKernelGGL(lds_read_kernel<8>, dim3(grid), dim3(256), 0, st, iters, sink);
     return probe_hip(hipGetLastError(), "lds read probe launch");
+}
+
+extern "C" int slimkv_probe_touch(uint32_t* sink, int64_t sink_words, int32_t workgroups, void* stream) {
+    if (!sink || workgroups < 1 || workgroups > 65536 || sink_words < workgroups)
+        return probe_fail("touch probe: 1..65536 workgroups, a sink word each");
+    hipLaunchKernelGGL(touch_kernel, dim3(workgroups), dim3(64), 0, static_cast<hipStream_t>(stream), sink);
+    return probe_hip(hipGetLastError(), "touch probe launch");
 }
