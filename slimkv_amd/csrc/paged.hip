@@ -117,6 +117,9 @@ paged_step_rows_kernel(slimkv_paged_step_rows_args a) {
     const int64_t rc = a.raw_count[b];
     const int64_t len = a.sink + rc + 1;
     const int64_t r_item = item / H, h = item % H;
+    // a raw set longer than the dense buffer's rows would lose its new token's
+    // row (and the flush write): report it as a slot outside the buffer
+    if (item == 0 && lane16 == 0 && len > a.rows && a.status) *a.status = SLIMKV_STATUS_BAD_SLOT;
     // a 16-lane row group past the request's raw set has nothing to do; the
     // rotation's DPP reads only lanes of its own group, so it may leave
     if (r_item >= len || r_item >= a.rows) return;

@@ -839,7 +839,9 @@ def paged_step_rows(raw_pages, raw_table, beacon_pages, beacon_table, new_k, new
     raw_count; K rotated at positions [B, >= rows] (fp32 cos/sin).  With
     `flush`: flush_memory's writes afterwards (the new token into its raw page
     below raw_write_end, the sink replaced where sink_update).  Rows past a
-    request's raw set are left unwritten.  Index errors as raw_pages."""
+    request's raw set are left unwritten; a request whose raw set (sink +
+    raw_count + 1 rows) does not fit `rows` is an index error (the status
+    word's bad-slot code).  Index errors as raw_pages."""
     _need_device(raw_pages, beacon_pages, new_k, new_v, window_start, raw_count, positions, cos, sin)
     _need_bf16(raw_pages, beacon_pages, new_k, new_v, out_k, out_v)
     if raw_pages.dim() != 5 or raw_pages.shape[2] != 2 or raw_pages.stride(4) != 1:
@@ -862,6 +864,10 @@ def paged_step_rows(raw_pages, raw_table, beacon_pages, beacon_table, new_k, new
         raise ValueError('positions must be [B, >= rows]')
     window_start = window_start.to(device=raw_pages.device, dtype=torch.int64).contiguous()
     raw_count = raw_count.to(device=raw_pages.device, dtype=torch.int32).contiguous()
+    per_request = [window_start, raw_count] + ([raw_write_end] if flush else []) + \
+        ([sink_update] if flush and sink else [])
+    if any(t is None or t.numel() < B for t in per_request):
+        raise ValueError('window_start, raw_count (and with flush raw_write_end, sink_update) need an entry per request')
     if out_k is None:
         out_k = torch.empty(B, rows, H, D, dtype=BF16, device=raw_pages.device)
     if out_v is None:

@@ -256,6 +256,33 @@ def test_paged_step_bad_write_block(device):
     assert changed == [blk]
 
 
+def test_paged_step_rows_bounds(device):
+    """A dense raw set too short for a request's sink + window rows + new
+    token raises IndexError after the launch; per-request tensors shorter than
+    the batch are refused before it."""
+    from slimkv_amd import kernels
+    from slimkv_amd.paged_step import plan_paged_step
+    att, gen = _attention(device, False, seed=29)
+    processed = [9, 20]
+    layout, raw, beacon, raw_tables, beacon_tables = _pool(device, processed, gen, seed=7)
+    (g,) = plan_paged_step(processed, WINDOW, RATIO, SINK, device)
+    t = g.tensors
+    new_k = torch.randn(2, HKV, D, generator=gen, device=device).to(torch.bfloat16)
+    new_v = torch.randn_like(new_k)
+    cos, sin = att.rotary_emb.cos_cached, att.rotary_emb.sin_cached
+    args = (raw, raw_tables, beacon, beacon_tables, new_k, new_v, t['window_start'], t['raw_count'],
+            t['raw_positions'])
+    ok_k, ok_v = kernels.paged_step_rows(*args, cos, sin, g.max_raw, SINK)
+    torch.cuda.synchronize()
+    with pytest.raises(IndexError):             # request 1 needs sink + 20 + 1 = 22 rows
+        kernels.paged_step_rows(*args, cos, sin, g.max_raw - 1, SINK)
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError):
+        kernels.paged_step_rows(raw, raw_tables, beacon, beacon_tables, new_k, new_v, t['window_start'][:1],
+                                t['raw_count'], t['raw_positions'], cos, sin, g.max_raw, SINK)
+    assert ok_k.shape == (2, g.max_raw, HKV, D) and ok_v.shape == ok_k.shape
+
+
 @pytest.mark.parametrize('cfg', [(32, 8, 0), (64, 16, 1)])
 def test_paged_step_other_configurations(device, cfg):
     """No sink (every raw row of the memory is a window row) and a longer
