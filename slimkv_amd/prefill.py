@@ -183,6 +183,8 @@ class PrefillHistory:
                 raise ValueError('prefill history needs key and value latents of the same rows')
             heads = attention.num_key_value_heads
             base = self.sink + self.history
+            if base + n > self.k.shape[2] or key_latent.shape[0] != self.k.shape[0]:
+                raise ValueError('prefill history capacity exceeded')
             for lat, up, dst in ((key_latent, attention.beacon_k_up_proj, self.k),
                                  (value_latent, attention.beacon_v_up_proj, self.v)):
                 kernels.reconstruct(lat, up.weight, up.bias, kv_heads=heads,

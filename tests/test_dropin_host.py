@@ -134,4 +134,8 @@ def test_prefill_history_follows_the_memory():
         store.reserve(2, 29)
     with pytest.raises(ValueError, match='capacity'):
         store.reserve(3, 16)
+    # 12 held rows + 29 new beacons pass the 40-row capacity: refused before any launch
+    with pytest.raises(ValueError, match='capacity'):
+        store.append(att, torch.zeros(2, 29, 64), torch.zeros(2, 29, 64), sink_size=4)
+    assert store.history == 8
     assert store.follows(empty, empty) and (store.sink, store.history) == (0, 0)
