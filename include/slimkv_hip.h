@@ -36,7 +36,8 @@ extern "C" {
  * SLIMKV_STATUS_BAD_PAGE there with an ordinary store; nothing clears it. */
 #define SLIMKV_STATUS_BAD_PAGE 1
 /* slimkv_decode_qkv: the cache slot lies outside [0, capacity); no cache row
- * is written (the reference's index_copy_ raises IndexError). */
+ * is written (the reference's index_copy_ raises IndexError).
+ * slimkv_paged_step_rows: a request's raw set does not fit the dense rows. */
 #define SLIMKV_STATUS_BAD_SLOT 2
 
 /* Message describing the last failure on the calling thread ("" if none). */
@@ -629,7 +630,10 @@ int slimkv_raw_pages(const slimkv_raw_pages_args* a, void* stream);
  * raw_write_end[b], and the root page's sink replaced by the new token where
  * sink_update[b] (one byte per request) is non-zero.  Table entries follow
  * torch's indexing; an entry outside the pool moves nothing for its row and
- * stores SLIMKV_STATUS_BAD_PAGE in the optional status word.
+ * stores SLIMKV_STATUS_BAD_PAGE in the optional status word.  A request whose
+ * raw set (sink + raw_count[b] + 1 rows) exceeds `rows` stores
+ * SLIMKV_STATUS_BAD_SLOT there (its rows past `rows`, the new token's among
+ * them, are neither gathered nor flushed).
  * ---------------------------------------------------------------------- */
 typedef struct slimkv_paged_step_rows_args {
     void* raw_pages; int64_t num_blocks, p_sblk, p_stok, p_skind, p_sh;
@@ -651,7 +655,7 @@ typedef struct slimkv_paged_step_rows_args {
 
 int slimkv_paged_step_rows(const slimkv_paged_step_rows_args* a, void* stream);
 
-/* The measurement probes (HBM and LDS read ceilings) are in
+/* The measurement probes (HBM and LDS read ceilings, the launch floor) are in
  * libslimkv_probe.so, declared in slimkv_probe.h. */
 
 #ifdef __cplusplus
