@@ -756,11 +756,13 @@ def _status_word(status, device):
 def check_status(status):
     """Raise IndexError when a kernel reported an index error in `status`: a
     block-table entry outside the pool (the reference's torch indexing raises
-    IndexError, paged_cache.py:60-67) or a decode cache slot outside the
-    caches (index_copy_, static_decode.py:156-163).  Synchronises the host."""
+    IndexError, paged_cache.py:60-67) or a row outside its buffer: a decode
+    cache slot past the caches (index_copy_, static_decode.py:156-163) or a
+    paged request's raw set past the step's dense rows.  Synchronises the
+    host."""
     code = int(status.reshape(-1)[0].item())
     if code == _lib.STATUS_BAD_SLOT:
-        raise IndexError('decode cache slot outside the cache capacity')
+        raise IndexError('cache slot outside the buffer (decode cache capacity or the dense raw rows)')
     if code != 0:
         raise IndexError('block table refers to a page outside the allocation')
 
