@@ -12,6 +12,10 @@ V lift.  The step gathers the RoPE table rows at its query positions once (every
 layer rotates at the same positions) and passes them to each layer.  The
 32-layer sweep is captured once in a HIP graph and replayed.
 
+`--workload qwen` runs the same sweep at the Qwen2.5-14B layer shape: 40 query
+heads on 8 KV heads (five a KV head), biases on both up-projections (the
+model's attention_bias), 48 layers.
+
 value  = algorithmic bytes of the sweep / sweep time (GB/s), inputs resident in HBM.
 roofline = the split-K attention kernel alone (it makes its own query operands):
            its algorithmic bytes per launch / its average duration measured with
@@ -34,6 +38,14 @@ METRIC = 'decode attn GB/s and % HBM peak, Llama-3.1-8B t4f4 b16 ctx32K; decode 
 HBM_PEAK_GBPS = 8000.0
 
 B, HQ, HKV, D = 16, 32, 8, 128
+# Layer shapes of the latent sweep (B16, 32K context, t4, ranks by seed):
+# the headline Llama-3.1-8B layer and the Qwen2.5-14B layer (GQA group 5,
+# up-projection biases).
+SHAPES = {
+    'latent': dict(model='Llama-3.1-8B', hq=32, bias=False, layers=32, metric=METRIC),
+    'qwen': dict(model='Qwen2.5-14B', hq=40, bias=True, layers=48,
+                 metric='decode attn GB/s and % HBM peak, Qwen2.5-14B t4f4 b16 ctx32K; decode tokens/s'),
+}
 CONTEXT, RATIO, SINKS, TAIL = 32768, 4, 4, 128
 BEACONS = CONTEXT // RATIO          # 8192 latent rows
 RAW = SINKS + TAIL + 1              # sinks + tail + current token
@@ -50,25 +62,31 @@ RANKS = (16, 32, 48)
 SPLIT_TRAFFIC_BYTES = {32: (2 * 70_840.53 + 2_628.01) * 1024, 16: (2 * 37_944.51 + 2_628.01) * 1024,
                        48: (2 * 107_667.30 + 3_140.01) * 1024}
 SPLIT_TRAFFIC_BYTES = {r: int(v) for r, v in SPLIT_TRAFFIC_BYTES.items()}
+# the same for the Qwen2.5-14B layers (`bench.py --workload qwen --layers 5
+# --steps 2 --warmup 1 --no-cpu --no-graph`, same scaling)
+QWEN_SPLIT_TRAFFIC_BYTES = {32: (2 * 70_980.81 + 3_288.15) * 1024, 16: (2 * 38_075.66 + 3_614.12) * 1024,
+                            48: (2 * 109_590.98 + 3_928.19) * 1024}
+QWEN_SPLIT_TRAFFIC_BYTES = {r: int(v) for r, v in QWEN_SPLIT_TRAFFIC_BYTES.items()}
 TRAFFIC_SOURCE = ('rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, split_kernel, scaled by the ceiling probe\'s '
                   '4 GiB stream reads and 256 MiB fills')
 
 
-def layer_bytes(rk, rv):
+def layer_bytes(rk, rv, hq=HQ, bias=False):
     """Algorithmic bytes of one layer step: latent rows, raw rows, q in, out,
-    and the two up-projection weights once."""
+    and the two up-projection weights (and their biases) once."""
     rows = B * (BEACONS * HKV * (rk + rv) * 2 + RAW * HKV * D * 2 * 2)
-    return rows + B * 2 * HQ * D * 2 + HKV * D * (rk + rv) * 2
+    return rows + B * 2 * hq * D * 2 + HKV * D * (rk + rv) * 2 + (2 * HKV * D * 2 if bias else 0)
 
 
-def split_kernel_bytes(rk, rv):
+def split_kernel_bytes(rk, rv, hq=HQ):
     """Bytes the split-K kernel must read: latent rows, raw rows and q once."""
-    return B * (BEACONS * HKV * (rk + rv) * 2 + RAW * HKV * D * 2 * 2 + HQ * D * 2)
+    return B * (BEACONS * HKV * (rk + rv) * 2 + RAW * HKV * D * 2 * 2 + hq * D * 2)
 
 
-def fused_kernel_bytes(rk, rv):
-    """The split kernel that makes its own query operands also reads U_K once."""
-    return split_kernel_bytes(rk, rv) + HKV * D * rk * 2
+def fused_kernel_bytes(rk, rv, hq=HQ, bias=False):
+    """The split kernel that makes its own query operands also reads U_K (and
+    its bias) once."""
+    return split_kernel_bytes(rk, rv, hq) + HKV * D * rk * 2 + (HKV * D * 2 if bias else 0)
 
 
 REPLAYS = 50
@@ -115,7 +133,7 @@ def draw_ranks(layers, seed):
     return [rng.choice(RANKS) for _ in range(layers)]
 
 
-def make_layer(torch, device, rank, seed, cos, sin):
+def make_layer(torch, device, rank, seed, cos, sin, hq=HQ, bias=False):
     from slimkv_amd import kernels
     from slimkv_amd.workloads import block_diagonal, orthonormal_columns
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -128,9 +146,12 @@ def make_layer(torch, device, rank, seed, cos, sin):
     lat_v = randn(B, BEACONS, HKV * rank)
     raw_k = randn(B, RAW, HKV, D)
     raw_v = randn(B, RAW, HKV, D)
-    q = randn(B, 1, HQ, D)
+    q = randn(B, 1, hq, D)
     up_k = block_diagonal([orthonormal_columns(D, rank, cpu_gen) for _ in range(HKV)]).to(device, torch.bfloat16)
     up_v = block_diagonal([orthonormal_columns(D, rank, cpu_gen) for _ in range(HKV)]).to(device, torch.bfloat16)
+    # up-projection biases of the size a trained Qwen2.5 layer's K/V biases take
+    bk = (0.5 * randn(HKV * D).float()).to(torch.bfloat16) if bias else None
+    bv = (0.5 * randn(HKV * D).float()).to(torch.bfloat16) if bias else None
     q_pos = torch.full((B, 1), CONTEXT, dtype=torch.int64, device=device)
     # Raw K is kept rotated in the cache (rotated once when appended): sinks at
     # 0..3, tail at CONTEXT-TAIL.., current token at CONTEXT.
@@ -140,20 +161,20 @@ def make_layer(torch, device, rank, seed, cos, sin):
                                    SINKS, history)
     raw_k = k_rot.transpose(1, 2).contiguous()
     return dict(rank=rank, q=q, q_pos=q_pos, raw_k=raw_k, raw_v=raw_v, lat_k=lat_k, lat_v=lat_v,
-                up_k=up_k, up_v=up_v,
-                out=torch.empty(B, 1, HQ, D, dtype=torch.bfloat16, device=device),
-                lse=torch.empty(B, HQ, 1, dtype=torch.float32, device=device))
+                up_k=up_k, up_v=up_v, bk=bk, bv=bv,
+                out=torch.empty(B, 1, hq, D, dtype=torch.bfloat16, device=device),
+                lse=torch.empty(B, hq, 1, dtype=torch.float32, device=device))
 
 
 def run_layer(kernels, L, rows, scale, workspace, stages=7):
     """One layer's fused decode; `rows` = the step's RoPE rows at the query
     positions (kernels.query_rope_rows), shared by every layer of the step."""
     kernels.latent_decode(L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'], scale,
-                          block_diagonal=True, cos=rows[0], sin=rows[1],
-                          out=L['out'], lse=L['lse'], workspace=workspace, stages=stages)
+                          up_k_bias=L.get('bk'), up_v_bias=L.get('bv'), block_diagonal=True, cos=rows[0],
+                          sin=rows[1], out=L['out'], lse=L['lse'], workspace=workspace, stages=stages)
 
 
-def cpu_baseline(torch, layer, cos, sin, scale):
+def cpu_baseline(torch, layer, cos, sin, scale, hq=HQ, bias=False):
     """The torch fp32 eager restatement of the reference decode path on the
     host: one full-shape layer, at every host thread and at one thread."""
     from bench_workloads import cpu_baseline as timed
@@ -161,17 +182,18 @@ def cpu_baseline(torch, layer, cos, sin, scale):
     from slimkv_amd import kernels
     q_rot, _ = kernels.rope_decode(layer['q'].transpose(1, 2), layer['raw_k'].transpose(1, 2)[:, :, :1].contiguous(),
                                    cos, sin, layer['q_pos'], None, 0, 0)
-    cpu = {k: layer[k].float().cpu() for k in ('raw_k', 'raw_v', 'lat_k', 'lat_v', 'up_k', 'up_v')}
+    cpu = {k: None if layer.get(k) is None else layer[k].float().cpu()
+           for k in ('raw_k', 'raw_v', 'lat_k', 'lat_v', 'up_k', 'up_v', 'bk', 'bv')}
     q_cpu = q_rot.float().cpu()
     lat_k, lat_v = cpu['lat_k'][:, :, None], cpu['lat_v'][:, :, None]
 
     def once():
         return eager_torch.latent_layer(q_cpu, cpu['raw_k'], cpu['raw_v'], lat_k, lat_v, cpu['up_k'], cpu['up_v'],
-                                        scale, HKV)
+                                        scale, HKV, cpu['bk'], cpu['bv'])
     rk = layer['rank']
-    return timed(torch, once, layer_bytes(rk, rk), 'GB/s', 1e9,
-                 f'one full-shape rank-{rk} layer (B16, 8192 beacons, 133 raw), torch fp32 eager restatement of the '
-                 f'reference decode')
+    return timed(torch, once, layer_bytes(rk, rk, hq, bias), 'GB/s', 1e9,
+                 f'one full-shape rank-{rk} layer (B16, {hq}/{HKV} heads, 8192 beacons, 133 raw'
+                 f'{", up-projection biases" if bias else ""}), torch fp32 eager restatement of the reference decode')
 
 
 def main():
@@ -179,12 +201,14 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--layers', type=int, default=32)
+    ap.add_argument('--layers', type=int, default=None, help='layers of the latent sweep (32; 48 for qwen)')
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--no-graph', action='store_true', help='time eager launches instead of graph replay')
-    ap.add_argument('--workload', default='latent', choices=('latent', 'prefill', 'recon', 'paged', 'paged_step', 'b1', 'ceiling'),
-                    help='latent: the headline decode sweep; prefill / recon / paged: the window prefill, '
+    ap.add_argument('--workload', default='latent',
+                    choices=('latent', 'qwen', 'prefill', 'recon', 'paged', 'paged_step', 'b1', 'ceiling'),
+                    help='latent: the headline decode sweep; qwen: the same sweep at the Qwen2.5-14B layer '
+                         'shape; prefill / recon / paged: the window prefill, '
                          'reconstruction decode and paged-cache decode workloads; paged_step: one attention '
                          'layer of a batched vLLM decode step over the pages; b1: batch-1 ms per token '
                          'at the contexts the reference publishes; ceiling: the HBM read rate a plain '
@@ -198,10 +222,14 @@ def main():
         # an A/B override of the library: the line says so ("library"."override")
         print(f"bench: SLIMKV_HIP_LIBRARY={os.environ['SLIMKV_HIP_LIBRARY']} overrides the in-tree library",
               file=sys.stderr, flush=True)
-    if args.workload != 'latent':
+    if args.workload not in SHAPES:
         from bench_workloads import run_workload
         print(json.dumps(run_workload(args)), flush=True)
         return
+    shape = SHAPES[args.workload]
+    hq, bias = shape['hq'], shape['bias']
+    if args.layers is None:
+        args.layers = shape['layers']
 
     import torch
     from slimkv_amd import _lib, kernels
@@ -213,10 +241,10 @@ def main():
     cos, sin = rope_tables(CONTEXT + 1, D, 500000.0, device)
     ranks = draw_ranks(args.layers, args.seed)
     print(f'bench: building {args.layers} layers, ranks {ranks}', file=sys.stderr, flush=True)
-    layers = [make_layer(torch, device, r, args.seed * 1000 + i, cos, sin) for i, r in enumerate(ranks)]
+    layers = [make_layer(torch, device, r, args.seed * 1000 + i, cos, sin, hq, bias) for i, r in enumerate(ranks)]
     ws_bytes = max(kernels.latent_decode_workspace_bytes(
-        L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'], block_diagonal=True,
-        q_positions=L['q_pos'], cos=cos, sin=sin) for L in layers)
+        L['q'], L['raw_k'], L['raw_v'], L['lat_k'], L['lat_v'], L['up_k'], L['up_v'], up_k_bias=L['bk'],
+        up_v_bias=L['bv'], block_diagonal=True, q_positions=L['q_pos'], cos=cos, sin=sin) for L in layers)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     torch.cuda.synchronize()
 
@@ -253,15 +281,15 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
-    sweep_bytes = sum(layer_bytes(r, r) for r in ranks)
+    sweep_bytes = sum(layer_bytes(r, r, hq, bias) for r in ranks)
     gbps = sweep_bytes / (elapsed / args.steps) / 1e9
     print(f'bench: sweep {ms_per_step:.3f} ms, {gbps:.1f} GB/s', file=sys.stderr, flush=True)
     replay_ms = replay_median_ms(torch, step, REPLAYS)
 
-    # The split kernel alone, as the sweep runs it: with per-head bases and no
-    # K bias a call of the prologue and attend stages is one launch of the
-    # split kernel that makes its own query operands (query RoPE, absorption
-    # into U_K).  One rank's layers -- each with its own buffers, so the cache
+    # The split kernel alone, as the sweep runs it: with per-head bases a call
+    # of the prologue and attend stages is one launch of the split kernel that
+    # makes its own query operands (query RoPE, absorption into U_K, the K
+    # bias's LSE shift).  One rank's layers -- each with its own buffers, so the cache
     # holds none of them -- are captured back to back in one graph and timed
     # with HIP events over PROFILE_REPLAYS replays: the per-launch average
     # includes the hand-off between launches, as the kernel trace does, and no
@@ -317,15 +345,16 @@ def main():
     from bench_workloads import ceiling_probe, launch_floor_probe
     _, ceiling = ceiling_probe(torch, device)
     # what a launch and its hand-off cost with no work (the combine's grid)
-    floor_us = launch_floor_probe(torch, device, workgroups=B * HQ)
+    floor_us = launch_floor_probe(torch, device, workgroups=B * hq)
     dom = 32 if 32 in durations else max(durations, key=lambda r: len(durations[r]))
     dur = durations[dom]
     dur_avg = sum(dur) / len(dur)
-    achieved = fused_kernel_bytes(dom, dom) / dur_avg / 1e9
+    achieved = fused_kernel_bytes(dom, dom, hq, bias) / dur_avg / 1e9
     all_split = sum(sum(v) / len(v) * ranks.count(r) for r, v in durations.items())
     roofline = {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                 'frac': round(achieved / HBM_PEAK_GBPS, 4),
-                'traffic': SPLIT_TRAFFIC_BYTES.get(dom), 'traffic_source': TRAFFIC_SOURCE,
+                'traffic': (QWEN_SPLIT_TRAFFIC_BYTES if bias else SPLIT_TRAFFIC_BYTES).get(dom),
+                'traffic_source': TRAFFIC_SOURCE,
                 'kernel': f'split_kernel, query operands made in the kernel (rank-{dom} layers)',
                 'avg_us': round(dur_avg * 1e6, 2),
                 'split_kernel_sweep_frac': round(all_split / (elapsed / args.steps), 3),
@@ -337,12 +366,13 @@ def main():
                 'attend_stage_us_by_rank': {str(r): round(v * 1e6, 2) for r, v in sorted(staged.items())}}
 
     result = {
-        'metric': METRIC, 'value': round(gbps, 1), 'unit': 'GB/s', 'n_gpus': 1, 'steps': args.steps,
+        'metric': shape['metric'], 'value': round(gbps, 1), 'unit': 'GB/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': round(ms_per_step, 4), 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic',
-        'config': {'workload': 'latent beacon decode, 32-layer sweep, Llama-3.1-8B layer shape t4f4',
+        'config': {'workload': f"latent beacon decode, {len(layers)}-layer sweep, {shape['model']} layer shape t4f4"
+                               + (', up-projection biases' if bias else ''),
                    'batch': B, 'context': CONTEXT, 'beacons': BEACONS, 'raw_tokens': RAW,
-                   'q_heads': HQ, 'kv_heads': HKV, 'head_dim': D, 'layer_ranks': ranks,
+                   'q_heads': hq, 'kv_heads': HKV, 'head_dim': D, 'layer_ranks': ranks,
                    'graph': not args.no_graph},
         'hbm_frac': round(gbps / HBM_PEAK_GBPS, 4),
         'tokens_per_s': round(B / (elapsed / args.steps), 1),
@@ -356,7 +386,7 @@ def main():
     if not args.no_cpu:
         rank32 = next((L for L in layers if L['rank'] == 32), layers[0])
         print('bench: CPU baseline leg', file=sys.stderr, flush=True)
-        result['cpu_baseline'] = cpu_baseline(torch, rank32, cos, sin, scale)
+        result['cpu_baseline'] = cpu_baseline(torch, rank32, cos, sin, scale, hq, bias)
     print(json.dumps(result), flush=True)
 
 

@@ -42,12 +42,21 @@ def project_value(out, weight, kv_heads):
     return (grouped @ weight.reshape(kv_heads, dim, rank).transpose(-1, -2)).reshape(batch, heads, length, dim)
 
 
-def latent_layer(q_rot, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, kv_heads):
-    """q_rot [B,H,1,D]; raw_k/raw_v [B,Nr,Hkv,D]; lat_k/lat_v [B,Nl,1,R]; fp32."""
+def latent_layer(q_rot, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, kv_heads, up_k_bias=None, up_v_bias=None):
+    """q_rot [B,H,1,D]; raw_k/raw_v [B,Nr,Hkv,D]; lat_k/lat_v [B,Nl,1,R];
+    biases [Hkv*D] or None (fa2_decode.py:157-163: the K bias shifts the latent
+    LSE by (q . b_k) * scale, the V bias adds to the lifted output); fp32."""
     raw_out, raw_lse = eager_forward(q_rot.transpose(1, 2), raw_k, raw_v, scale)
     latent_q = project_query(q_rot, up_k, kv_heads)
     lat_out, lat_lse = eager_forward(latent_q.transpose(1, 2), lat_k, lat_v, scale)
     lat_out = project_value(lat_out.transpose(1, 2), up_v, kv_heads)
+    heads, dim = q_rot.shape[1], q_rot.shape[-1]
+    if up_k_bias is not None:
+        bias = up_k_bias.reshape(kv_heads, dim).repeat_interleave(heads // kv_heads, dim=0)
+        lat_lse = lat_lse + (q_rot.float() * bias[None, :, None].float()).sum(-1) * scale
+    if up_v_bias is not None:
+        bias = up_v_bias.reshape(kv_heads, dim).repeat_interleave(heads // kv_heads, dim=0)
+        lat_out = lat_out + bias[None, :, None].float()
     total = torch.logaddexp(raw_lse, lat_lse)
     return (torch.exp(raw_lse - total)[..., None] * raw_out.transpose(1, 2)
             + torch.exp(lat_lse - total)[..., None] * lat_out)

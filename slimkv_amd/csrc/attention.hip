@@ -112,6 +112,16 @@ struct QAbsorb {
     int wq;                                          // per-head K rank
 };
 
+// K bias of the latent rows when the split kernel makes the query operands:
+// the raw waves of split 0 write each query row's LSE shift (q . b_k of its KV
+// head, times the natural-log scale) for the combine, as the prologue does
+// when it runs.  bias null: no K bias.
+struct QShift {
+    const uint16_t* bias;                            // up_k_bias [Hkv * 128]
+    float* shift;                                    // [B][Hq*Lq]
+    float scale;
+};
+
 struct SplitParams {
     Seg seg[2];
     int nseg;
@@ -121,6 +131,7 @@ struct SplitParams {
     RawPagesArg rawp;
     QRope qrope;                                     // q null: seg[].q holds rotated rows
     QAbsorb absorb;
+    QShift kshift;
 };
 
 constexpr int kWaves = 4;
@@ -516,6 +527,24 @@ __device__ __forceinline__ void absorb_apply(u32x4 (&qv)[KS / 2], const AbsorbRo
     }
 }
 
+// q . b_k of one query row: lane (col, grp) holds elements 32c + 8grp + [0, 8)
+// of the rotated row and of its KV head's bias; the lane groups' sums meet by
+// two swaps.  The prologue and the split kernel's raw waves both take the
+// shift from here, so it is the same bits whichever of them runs.
+__device__ __forceinline__ float kbias_dot(const u32x4 (&q)[4], const u32x4 (&bk)[4]) {
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            dot += bf16_to_f32(q[c][e] & 0xffffu) * bf16_to_f32(bk[c][e] & 0xffffu);
+            dot += bf16_to_f32(q[c][e] >> 16) * bf16_to_f32(bk[c][e] >> 16);
+        }
+    dot += shfl_xor_f(dot, 16);
+    dot += shfl_xor_f(dot, 32);
+    return dot;
+}
+
 // A workgroup owns (batch b, group of 4 tile slots, key split s); a slot is a
 // (KV head, column tile) pair and each wave takes one slot.  The four waves
 // therefore stream the same keys' rows at the same time (whole DRAM pages),
@@ -526,7 +555,7 @@ template <int KS, int DEPTH, int PAGED = 0, int SEG2 = 0, int RAWPG = 0, int FQ 
 __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int Lq, int Hq,
                                               float scale_log2, char* lds, const SegRows2* two = nullptr,
                                               const RawPagesArg* rawp = nullptr, const QRope* qr = nullptr,
-                                              const QAbsorb* qa = nullptr) {
+                                              const QAbsorb* qa = nullptr, const QShift* qs = nullptr) {
     static_assert(!FQ || KS <= 8, "fused query operands are built for tiles up to 128 columns");
     constexpr int VT = KS;                   // V tiles of 16 (same width budget as K)
     constexpr int RS = SplitLds<KS>::RS;
@@ -906,6 +935,19 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
     }
     // Column sums: every lane group holds a quarter of the keys.
     lsum = rows_sum(lsum);
+    if constexpr (FQ && KS == 8) {
+        // Raw waves of split 0 with a latent K bias: the row's LSE shift, from
+        // the operand rotated above.  Loaded after the tiles, when the raw
+        // wave's registers are free; raw work drains long before the latent.
+        if (qs && qs->bias && s == 0) {
+            const uint16_t* bk = qs->bias + (int64_t)h * 128 + 8 * grp;
+            u32x4 kb[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kb[c] = *reinterpret_cast<const u32x4*>(bk + 32 * c);
+            const float dot = kbias_dot(qv, kb);
+            if (colv && grp == 0) qs->shift[(int64_t)b * Hq * Lq + j * Lq + lq] = dot * qs->scale;
+        }
+    }
     if (!colv) return;
     const int pr = j * Lq + lq;
     const int64_t slot_out = ((int64_t)b * Hq * Lq + pr) * sg.splits + s;
@@ -961,13 +1003,15 @@ split_kernel(SplitParams prm) {
         // which held half the beacon items back until they drained).
         if (w >= prm.seg[0].nwg) {
             split_segment<KB, 1, 0, 0, RAWPG, FQ>(prm.seg[1], w - prm.seg[0].nwg, prm.B, prm.Lq, prm.Hq,
-                                                  prm.scale_log2, lds, nullptr, &prm.rawp, FQ ? &prm.qrope : nullptr);
+                                                  prm.scale_log2, lds, nullptr, &prm.rawp, FQ ? &prm.qrope : nullptr,
+                                                  nullptr, FQ ? &prm.kshift : nullptr);
             return;
         }
     } else if constexpr (KB > 0) {
         if (w < prm.seg[1].nwg) {
             split_segment<KB, 1, 0, 0, RAWPG, FQ>(prm.seg[1], w, prm.B, prm.Lq, prm.Hq, prm.scale_log2, lds, nullptr,
-                                                  &prm.rawp, FQ ? &prm.qrope : nullptr);
+                                                  &prm.rawp, FQ ? &prm.qrope : nullptr, nullptr,
+                                                  FQ ? &prm.kshift : nullptr);
             return;
         }
         w -= prm.seg[1].nwg;
@@ -2144,18 +2188,7 @@ prologue_mfma_kernel(PrologueParams pp) {
                 u32x2{pack_bf16(t4[0], t4[1]), pack_bf16(t4[2], t4[3])};
     }
     if (pp.shift) {
-        float dot = 0.f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const u32x4 bb = kb[c];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                dot += bf16_to_f32(qr[c][e] & 0xffffu) * bf16_to_f32(bb[e] & 0xffffu);
-                dot += bf16_to_f32(qr[c][e] >> 16) * bf16_to_f32(bb[e] >> 16);
-            }
-        }
-        dot += shfl_xor_f(dot, 16);
-        dot += shfl_xor_f(dot, 32);
+        const float dot = kbias_dot(qr, kb);
         if (valid && grp == 0) pp.shift[(int64_t)b * pp.Hq * pp.Lq + j * pp.Lq + l] = dot * pp.scale;
     }
 }
@@ -2587,7 +2620,22 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
     // to 16 take sixteen rows (four KV heads a wave), so a wave's tile is 64
     // latent columns wide as at rank 32 (rank-16 C1 layer 27.7 -> 24.4 us);
     // at rank 48 sixteen rows measured slower.
-    const int cols = bd && std::max(rk, rv) <= 16 ? 16 : 8;
+    int cols = bd && std::max(rk, rv) <= 16 ? 16 : 8;
+    if (bd && cols % (g * (int)Lq) != 0) {
+        // A GQA group that does not pack into those rows (Qwen2.5's five
+        // query heads a KV head) takes whole KV heads a wave -- four at ranks
+        // up to 16, else two, as many as fit sixteen rows and divide the KV
+        // heads -- so no tile spans a head it shares with the next tile, and a
+        // sequence's waves split each latent row evenly.  Eight rows of
+        // five-head groups gave tiles of two or three KV heads (96 columns at
+        // rank 32) and read every latent row 1.5 times: a B16 32K layer at
+        // rank 32 in 51.1 us, 34.1 us this way.  At rank 16 three heads a wave
+        // (48-column pieces of the 256-byte rows, shared by waves of other
+        // workgroups) ran 29.7 us, two heads 25.2.
+        int heads = std::max(1, std::min(std::max(rk, rv) <= 16 ? 4 : 2, kMaxRows / (g * (int)Lq)));
+        while (Hkv % heads) --heads;
+        cols = heads * g * (int)Lq;
+    }
     const int span = span_of(cols);
     const int lat_ks = round_even_tile(span);
     if (lat_ks < 0) return fail(SLIMKV_EUNSUP, "latent width not supported");
@@ -2725,12 +2773,13 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     const bool mfma_prologue = has_lat && bd && pp.ut && pp.wq % 16 == 0 && nct >= 1 && nct <= 3 &&
                                g * Lq <= 16 && ptr_aligned16(pp.ut) && ptr_aligned16(a->q) &&
                                (!a->up_k_bias || ptr_aligned16(a->up_k_bias));
-    // With per-head bases and no K bias, a call that runs the prologue and the
-    // attend stage together makes the query operands inside the split kernel
-    // (its raw waves rotate their rows, its latent waves rotate and absorb
-    // theirs): two launches a layer instead of three, the same bits.
-    const bool fused = mfma_prologue && !a->up_k_bias && (stages & SLIMKV_STAGE_PROLOGUE) &&
-                       (stages & SLIMKV_STAGE_ATTEND) && split_fq_ok(p.lat.ks, pg != nullptr, pg ? (int)pg->slots : 0);
+    // With per-head bases, a call that runs the prologue and the attend stage
+    // together makes the query operands inside the split kernel (its raw waves
+    // rotate their rows and, with a K bias, write the rows' LSE shifts; its
+    // latent waves rotate and absorb theirs): two launches a layer instead of
+    // three, the same bits.
+    const bool fused = mfma_prologue && (stages & SLIMKV_STAGE_PROLOGUE) && (stages & SLIMKV_STAGE_ATTEND) &&
+                       split_fq_ok(p.lat.ks, pg != nullptr, pg ? (int)pg->slots : 0);
     if (fused || !(stages & SLIMKV_STAGE_PROLOGUE)) {
         // the query operands of an earlier prologue stage are in the workspace
     } else if (mfma_prologue) {
@@ -2750,6 +2799,7 @@ int latent_decode_run(const slimkv_latent_decode_args* a, const PagedRows* pg, v
     if (fused) {
         prm.qrope = QRope{pp.q, pp.q_sb, pp.q_sl, pp.q_sh, pp.pos, pp.pos_sb, pp.cos, pp.sin, pp.rope_rows};
         prm.absorb = QAbsorb{pp.ut, pp.wq};
+        if (pp.shift) prm.kshift = QShift{pp.up_k_bias, pp.shift, pp.scale};
     }
     // Latent rows (the bulk, pipelined) are segment 0; the short raw segment is
     // segment 1, whose workgroups split_kernel places first in the grid.

@@ -19,6 +19,8 @@ C4  the paged workload's own seeded draw (64 sequences, 400K-page pool):
     and sampled sequences against the oracle.
     The benchmark's own call (raw rows through their raw pages too, the
     automatic compact schedule) on every sequence against the oracle.
+Qwen2.5-14B latent beacon decode (bench.py --workload qwen): B16 x 8192
+    beacons, 40/8 heads, up-projection biases, one layer per rank.
 Bar: max abs 2e-2, mean abs 2e-3 and relative l2 1e-2 on bf16 outputs; LSE
 within 2e-3.  C1 also runs with queries twice the benchmark's (a peaked
 softmax).
@@ -70,6 +72,30 @@ def test_c1_latent_decode_full_size(device, rank, q_scale):
                                      scale, bench.HKV)
     assert_close(to_np(layer['out'].transpose(1, 2)), want, what=f'C1 rank {rank} q x{q_scale}')
     assert_lse_close(to_np(layer['lse']), want_lse, what=f'C1 rank {rank} q x{q_scale}')
+
+
+@pytest.mark.parametrize('rank', [16, 32, 48])
+def test_qwen_latent_decode_full_size(device, rank):
+    """The sweep's Qwen2.5-14B layer (bench.py --workload qwen): B16 x 8192
+    beacons, 40/8 heads, biases on both up-projections."""
+    import bench
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import rope_tables
+    print(f'Qwen2.5-14B: B{bench.B} beacons {bench.BEACONS} rank {rank}', flush=True)
+    cos, sin = rope_tables(bench.CONTEXT + 1, bench.D, 500000.0, device)
+    layer = bench.make_layer(torch, device, rank, 9100 + rank, cos, sin, hq=40, bias=True)
+    pos = torch.full((bench.B, 1), bench.CONTEXT, dtype=torch.int64, device=device)
+    rows = kernels.query_rope_rows(cos, sin, pos)
+    scale = 1.0 / math.sqrt(bench.D)
+    bench.run_layer(kernels, layer, rows, scale, None)
+    torch.cuda.synchronize()
+    q_rot = _rot_at(layer['q'].transpose(1, 2), cos, sin, bench.CONTEXT)
+    want, want_lse = oa.latent_layer(q_rot, to_np(layer['raw_k'].transpose(1, 2)),
+                                     to_np(layer['raw_v'].transpose(1, 2)), to_np(layer['lat_k'])[:, None],
+                                     to_np(layer['lat_v'])[:, None], to_np(layer['up_k']), to_np(layer['up_v']),
+                                     scale, bench.HKV, to_np(layer['bk']), to_np(layer['bv']))
+    assert_close(to_np(layer['out'].transpose(1, 2)), want, what=f'Qwen rank {rank}')
+    assert_lse_close(to_np(layer['lse']), want_lse, what=f'Qwen rank {rank}')
 
 
 # ----------------------------------------------------------------------------- C2

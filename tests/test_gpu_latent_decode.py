@@ -329,3 +329,52 @@ def test_operands_made_in_the_split_kernel_equal_the_prologue(device, rank, quer
                                  case.scale, case.kv_heads, lat_causal=queries == 2)
         assert_close(to_np(one[0][b:b + 1].transpose(1, 2)), eo, what=f'sequence {b} ({m} beacons)')
         assert_lse_close(to_np(one[1][b:b + 1]), el)
+
+
+@pytest.mark.parametrize('rank,queries,bias', [(32, 1, True), (16, 1, True), (48, 1, True), (32, 2, True),
+                                               (16, 2, False), (48, 2, False), (32, 1, False)])
+def test_qwen_gqa5_shape(device, rank, queries, bias):
+    """Qwen2.5-14B's head layout: 40 query heads on 8 KV heads (five a KV
+    head, which does not pack into the eight- or sixteen-row tiles of a GQA
+    group of four: every wave takes whole KV heads) with biases on both
+    up-projections (attention_bias).  One call -- the split kernel makes the
+    query operands and, from its raw waves, the K bias's LSE shift -- is
+    bit-identical to the prologue stage's operands and shift consumed by the
+    attend and combine stages, over ragged latent lengths; and against the
+    oracle (fa2_decode.py:143-164, the biases at :157-163)."""
+    from slimkv_amd import kernels
+    B, H = 5, 40
+    case = latent_case(batch=B, heads=H, context=1400 + 132, tail=128, rank_k=rank, rank_v=rank,
+                       seed=7 * rank + queries + bias, device=device)
+    if queries == 2:
+        gen = torch.Generator(device=device).manual_seed(93)
+        case.q = torch.randn(B, 2, H, 128, generator=gen, device=device).to(torch.bfloat16)
+        case.q_positions = torch.tensor([[1532, 1533]] * B, device=device)
+        case.cos, case.sin = rope_tables(1534, 128, 500000.0, device)
+    q_rot, k_rot = _rotated(case)
+    bk = bv = None
+    if bias:
+        gen = torch.Generator(device=device).manual_seed(94)
+        bk = (0.5 * torch.randn(case.up_k.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+        bv = (0.5 * torch.randn(case.up_v.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+    n = case.lat_k.shape[1]
+    lat_len = torch.tensor([n, 1, 30, 257, n - 5], dtype=torch.int32, device=device)
+    common = dict(up_k_bias=bk, up_v_bias=bv, block_diagonal=True, lat_causal=queries == 2,
+                  q_positions=case.q_positions, cos=case.cos, sin=case.sin, lat_lengths=lat_len)
+
+    def call(stages, workspace):
+        return kernels.latent_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v,
+                                     case.up_k, case.up_v, case.scale, stages=stages, workspace=workspace, **common)
+    nbytes = kernels.latent_decode_workspace_bytes(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v,
+                                                   case.up_k, case.up_v, case.scale, **common)
+    one, two = _fused_and_staged(call, nbytes, device)
+    assert torch.equal(one[0], two[0]) and torch.equal(one[1], two[1])
+    for b in range(B):
+        m = int(lat_len[b])
+        eo, el = oa.latent_layer(to_np(q_rot[b:b + 1]), to_np(k_rot[b:b + 1]),
+                                 to_np(case.raw_v[b:b + 1].transpose(1, 2)), to_np(case.lat_k[b:b + 1, :m])[:, None],
+                                 to_np(case.lat_v[b:b + 1, :m])[:, None], to_np(case.up_k), to_np(case.up_v),
+                                 case.scale, case.kv_heads, None if bk is None else to_np(bk),
+                                 None if bv is None else to_np(bv), lat_causal=queries == 2)
+        assert_close(to_np(one[0][b:b + 1].transpose(1, 2)), eo, what=f'sequence {b} ({m} beacons)')
+        assert_lse_close(to_np(one[1][b:b + 1]), el)

@@ -130,15 +130,18 @@ def test_project_query_and_value_are_per_group_contractions():
         np.testing.assert_allclose(lv[:, j, 0], o[:, j, 0] @ w[(j // 4) * 16:(j // 4 + 1) * 16].T, rtol=1e-12)
 
 
-def test_torch_restatement_agrees_with_numpy_oracle():
+@pytest.mark.parametrize('bias', [False, True])
+def test_torch_restatement_agrees_with_numpy_oracle(bias):
+    """Also with GQA groups of five (the Qwen2.5 layout) and both biases."""
     import torch
     from oracle import eager_torch
-    q, raw_k, raw_v, lat_k, lat_v, uk, uv, _, _ = _layer(B=2, H=8, Hkv=2, D=16, Nr=6, Nl=11)
-    t = lambda x: torch.tensor(x, dtype=torch.float32)
+    q, raw_k, raw_v, lat_k, lat_v, uk, uv, bk, bv = _layer(B=2, H=10 if bias else 8, Hkv=2, D=16, Nr=6, Nl=11,
+                                                           bias=bias)
+    t = lambda x: None if x is None else torch.tensor(x, dtype=torch.float32)
     out = eager_torch.latent_layer(t(q), t(raw_k.transpose(0, 2, 1, 3)), t(raw_v.transpose(0, 2, 1, 3)),
                                    t(lat_k.transpose(0, 2, 1, 3)), t(lat_v.transpose(0, 2, 1, 3)), t(uk), t(uv),
-                                   0.25, 2)
-    expected, _ = oa.latent_layer(q, raw_k, raw_v, lat_k, lat_v, uk, uv, 0.25, 2, bf16_boundaries=False)
+                                   0.25, 2, t(bk), t(bv))
+    expected, _ = oa.latent_layer(q, raw_k, raw_v, lat_k, lat_v, uk, uv, 0.25, 2, bk, bv, bf16_boundaries=False)
     np.testing.assert_allclose(out.numpy(), expected, rtol=1e-4, atol=1e-5)
 
 
