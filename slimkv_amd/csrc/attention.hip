@@ -2615,23 +2615,21 @@ int plan_latent(const slimkv_latent_decode_args* a, LatentPlan* p, const PagedRo
         }
         return worst;
     };
-    // Eight packed rows per tile: 32 heads give four tiles, one per wave of a
-    // workgroup, all streaming the same latent rows.  Block-diagonal ranks up
-    // to 16 take sixteen rows (four KV heads a wave), so a wave's tile is 64
-    // latent columns wide as at rank 32 (rank-16 C1 layer 27.7 -> 24.4 us);
-    // at rank 48 sixteen rows measured slower.
-    int cols = bd && std::max(rk, rv) <= 16 ? 16 : 8;
-    if (bd && cols % (g * (int)Lq) != 0) {
-        // A GQA group that does not pack into those rows (Qwen2.5's five
-        // query heads a KV head) takes whole KV heads a wave -- four at ranks
-        // up to 16, else two, as many as fit sixteen rows and divide the KV
-        // heads -- so no tile spans a head it shares with the next tile, and a
-        // sequence's waves split each latent row evenly.  Eight rows of
-        // five-head groups gave tiles of two or three KV heads (96 columns at
-        // rank 32) and read every latent row 1.5 times: a B16 32K layer at
-        // rank 32 in 51.1 us, 34.1 us this way.  At rank 16 three heads a wave
-        // (48-column pieces of the 256-byte rows, shared by waves of other
-        // workgroups) ran 29.7 us, two heads 25.2.
+    // Whole KV heads a wave with per-head bases: four at ranks up to 16, else
+    // two -- a 64-column tile at ranks 16 and 32, 96 at rank 48 -- as many as
+    // fit the MFMA's sixteen query rows and divide the KV heads, so no tile
+    // spans a head it shares with the next tile and a sequence's waves split
+    // each latent row evenly (B16 32K layers, GQA group of four: rank 16 with
+    // four heads a wave 24.4 us against 27.7 with two; rank 48 with two heads
+    // against four faster).  Eight rows for every group before: a group of
+    // five got tiles of two or three KV heads and read every latent row 1.5
+    // times (rank 32: 51.1 against 34.1 us); a group of eight, or four with
+    // two queries, one head a tile (ranks 32 / 48: 40.0 / 68.4 against 34.9 /
+    // 51.6 us); a group of two, four heads a tile (ranks 16 / 32 / 48: 26.9 /
+    // 36.9 / 55.6 against 22.7 / 32.9 / 48.3 us).  General bases: eight query
+    // rows a tile, every tile reads whole rows.
+    int cols = 8;
+    if (bd) {
         int heads = std::max(1, std::min(std::max(rk, rv) <= 16 ? 4 : 2, kMaxRows / (g * (int)Lq)));
         while (Hkv % heads) --heads;
         cols = heads * g * (int)Lq;

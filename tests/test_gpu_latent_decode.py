@@ -331,21 +331,29 @@ def test_operands_made_in_the_split_kernel_equal_the_prologue(device, rank, quer
         assert_lse_close(to_np(one[1][b:b + 1]), el)
 
 
-@pytest.mark.parametrize('rank,queries,bias', [(32, 1, True), (16, 1, True), (48, 1, True), (32, 2, True),
-                                               (16, 2, False), (48, 2, False), (32, 1, False)])
-def test_qwen_gqa5_shape(device, rank, queries, bias):
+QWEN_CASES = [(40, 32, 1, True), (40, 16, 1, True), (40, 48, 1, True), (40, 32, 2, True), (40, 16, 2, False),
+              (40, 48, 2, False), (40, 32, 1, False)]
+# GQA groups of eight (64 query heads, the Llama-70B layout) and of two, one
+# and two queries: every wave takes whole KV heads, two or four of them
+GROUP_CASES = [(64, 32, 1, False), (64, 48, 1, True), (64, 16, 2, False), (16, 16, 1, False), (16, 32, 2, True),
+               (16, 48, 1, False), (32, 48, 2, True), (32, 32, 2, False)]
+
+
+@pytest.mark.parametrize('H,rank,queries,bias', QWEN_CASES + GROUP_CASES)
+def test_qwen_gqa5_shape(device, H, rank, queries, bias):
     """Qwen2.5-14B's head layout: 40 query heads on 8 KV heads (five a KV
     head, which does not pack into the eight- or sixteen-row tiles of a GQA
     group of four: every wave takes whole KV heads) with biases on both
-    up-projections (attention_bias).  One call -- the split kernel makes the
-    query operands and, from its raw waves, the K bias's LSE shift -- is
-    bit-identical to the prologue stage's operands and shift consumed by the
-    attend and combine stages, over ragged latent lengths; and against the
-    oracle (fa2_decode.py:143-164, the biases at :157-163)."""
+    up-projections (attention_bias); and groups of eight and two.  One call
+    -- the split kernel makes the query operands and, from its raw waves, the
+    K bias's LSE shift -- is bit-identical to the prologue stage's operands
+    and shift consumed by the attend and combine stages, over ragged latent
+    lengths; and against the oracle (fa2_decode.py:143-164, the biases at
+    :157-163)."""
     from slimkv_amd import kernels
-    B, H = 5, 40
+    B = 5
     case = latent_case(batch=B, heads=H, context=1400 + 132, tail=128, rank_k=rank, rank_v=rank,
-                       seed=7 * rank + queries + bias, device=device)
+                       seed=7 * rank + queries + bias + H, device=device)
     if queries == 2:
         gen = torch.Generator(device=device).manual_seed(93)
         case.q = torch.randn(B, 2, H, 128, generator=gen, device=device).to(torch.bfloat16)
