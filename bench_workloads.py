@@ -179,15 +179,15 @@ def _result(metric, value, unit, args, seconds, dtype, config, **extra):
 def prefill(args):
     """The window prefill step as prefill_forward runs it over a prefill
     history (slimkv_amd.prefill.PrefillHistory): per window the window's
-    beacon rows are down-projected and rebuilt as up(latent) in the
-    projection's K/V rows, the V rows are written after [sink | up(history)]
-    in the append-only store, the prefill RoPE rotates the window's keys
-    (beacon keys copied unrotated) into the store after the held keys, the
+    beacon rows are down-projected (K and V in one launch) and rebuilt as
+    up(latent) in the projection's K/V rows (one launch), the prefill RoPE
+    rotates the window's keys (beacon keys copied unrotated) into the store
+    after the held keys and copies its values beside them (one launch), the
     causal attention rotates its queries as it loads them and runs over
     [sink | history | window], and the window's 256 new beacons are rebuilt
-    onto the history.  The q/k/v
-    projections of the window (nn.Linear layers of the model) stand as given
-    rows, copied into the projection's output buffer each window."""
+    onto the history (one launch).  The k/v projections of the window
+    (nn.Linear layers of the model) stand as given rows, copied into the
+    projections' output buffers each window."""
     import torch
     from slimkv_amd import kernels
     from slimkv_amd.workloads import block_diagonal, orthonormal_columns, rope_tables
@@ -204,6 +204,7 @@ def prefill(args):
     work_k = torch.zeros(B, n_max, HKV, D, dtype=torch.bfloat16, device=dev)   # rotated keys as attended
     work_v = torch.zeros_like(work_k)
     proj_k = torch.zeros(B, L, HKV, D, dtype=torch.bfloat16, device=dev)      # the window's K projection
+    proj_v = torch.zeros_like(proj_k)                                           # and its V projection
     latents = [torch.zeros(B, NB * WINDOWS, R, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     qs = [rnd(B, L, HQ, D) for _ in range(WINDOWS)]
     cur = [(rnd(B, L, HKV, D), rnd(B, L, HKV, D)) for _ in range(WINDOWS)]
@@ -229,19 +230,22 @@ def prefill(args):
         n = keys(w)
         base = 0 if w == 0 else S + NB * w           # the window follows [sink | history]
         proj_k.copy_(cur[w][0])
-        work_v[:, base:base + L].copy_(cur[w][1])
-        for j, dst in ((0, proj_k), (1, work_v[:, base:base + L])):
-            lat = latents[j][:, NB * w:NB * (w + 1)]
-            kernels.down_project(cur[w][j].view(B, L, HKV * D), down[j], beacon_rows, blocks=HKV, out=lat)
-            kernels.reconstruct(lat, up[j], kv_heads=HKV, out=dst, dst_rows=beacon_rows, block_diagonal=True)
+        proj_v.copy_(cur[w][1])
+        lats = [latents[j][:, NB * w:NB * (w + 1)] for j in (0, 1)]
+        kernels.down_project_pair(*({'x': cur[w][j].view(B, L, HKV * D), 'weight': down[j], 'rows': beacon_rows,
+                                     'blocks': HKV, 'out': lats[j]} for j in (0, 1)))
+        kernels.reconstruct_pair(*({'latent': lats[j], 'weight': up[j], 'kv_heads': HKV, 'out': dst,
+                                    'dst_rows': beacon_rows, 'block_diagonal': True}
+                                   for j, dst in ((0, proj_k), (1, proj_v))))
         kernels.rope_keys(proj_k.transpose(1, 2), cos, sin, positions[:, base:n], roles, 0,
-                          out_k=work_k[:, base:n].transpose(1, 2))
+                          out_k=work_k[:, base:n].transpose(1, 2), v=proj_v.transpose(1, 2),
+                          out_v=work_v[:, base:n].transpose(1, 2))
         attend(w)
         # the window's new beacons onto the history (after the sink of window 0)
         hist = S + NB * w
-        for j, dst in ((0, work_k), (1, work_v)):
-            kernels.reconstruct(latents[j][:, NB * w:NB * (w + 1)], up[j], kv_heads=HKV,
-                                out=dst[:, hist:hist + NB], block_diagonal=True)
+        kernels.reconstruct_pair(*({'latent': lats[j], 'weight': up[j], 'kv_heads': HKV,
+                                    'out': dst[:, hist:hist + NB], 'block_diagonal': True}
+                                   for j, dst in ((0, work_k), (1, work_v))))
 
     def step():
         for w in range(WINDOWS):
@@ -271,9 +275,10 @@ def prefill(args):
                      {'workload': 'window prefill, 8192-token prompt, t4, per-head rank 32', 'batch': B,
                       'window': WIN, 'beacons_per_window': NB, 'windows': WINDOWS, 'q_heads': HQ, 'kv_heads': HKV,
                       'head_dim': D, 'sinks': S,
-                      'step': 'window K/V writes, beacon down-projection and rebuild, prefill RoPE of the window '
-                              'keys into the kept key set, attention (query RoPE inside), the 256 new beacons '
-                              'rebuilt onto an append-only history'},
+                      'step': 'window K/V projection outputs, beacon K/V down-projection and rebuild (one launch '
+                              'each), prefill RoPE of the window keys into the kept key set with its values copied '
+                              'beside them, attention (query RoPE inside), the 256 new beacons rebuilt onto an '
+                              'append-only history'},
                      roofline={'bound': 'mfma', 'achieved': round(achieved, 1), 'peak': MFMA_BF16_PEAK_TFLOPS,
                                'unit': 'TFLOP/s', 'frac': round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                                'traffic': None, 'kernel': 'prefill_kernel', 'kernel_ms': round(kernel_s * 1e3, 3)},

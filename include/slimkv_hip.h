@@ -263,6 +263,15 @@ typedef struct slimkv_reconstruct_args {
 
 int slimkv_reconstruct(const slimkv_reconstruct_args* a, void* stream);
 
+/* Two reconstructions in one launch where both take the streaming kernel (a
+ * contracted latent width up to 64) at the same width -- the K and the V
+ * rebuild of one set of beacon rows -- else in two launches; the results are
+ * those of two slimkv_reconstruct calls, bit for bit.  The reference runs the
+ * K and V up-projections of ReconstructionCache.materialize as two nn.Linear
+ * calls (slimkv/llama3/memory.py:29-36); this saves a launch where both are
+ * rebuilt together (a prefill window's beacon rows, modeling_llama.py:1347-1367). */
+int slimkv_reconstruct_pair(const slimkv_reconstruct_args* a, const slimkv_reconstruct_args* b, void* stream);
+
 /* ------------------------------------------------------------------------
  * Reconstruction decode for one attention layer: rebuild every beacon's K
  * (RoPE'd at `beacon_positions` when given) and V from the latents, then one
@@ -355,6 +364,11 @@ typedef struct slimkv_prefill_rope_args {
     const int64_t* positions; int64_t pos_sb;
     const int64_t* roles; int64_t role_len;
     int64_t batch, heads, kv_heads, queries, keys, dim, sink;
+    /* optional (v NULL: none): value rows [B, Hk, Nk, D] copied unchanged
+     * into out_v in the same launch, row for row with the keys -- the window's
+     * V written into the attention's value set beside its rotated keys */
+    const void* v; int64_t v_sb, v_sh, v_ss;
+    void* out_v; int64_t ov_sb, ov_sh, ov_ss;
 } slimkv_prefill_rope_args;
 
 int slimkv_prefill_rope(const slimkv_prefill_rope_args* a, void* stream);
@@ -526,6 +540,16 @@ typedef struct slimkv_down_project_args {
 size_t slimkv_down_project_workspace(const slimkv_down_project_args* a);
 int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* Two down-projections (the K and V latents of one set of beacon rows,
+ * beacon_k_down_proj and beacon_v_down_proj at modeling_llama.py:383-390,
+ * 444-451) in one launch where neither splits its contraction into partials,
+ * else one after the other; the results are those of two slimkv_down_project
+ * calls, bit for bit.  The workspace holds
+ * slimkv_down_project_pair_workspace(a, b) bytes. */
+size_t slimkv_down_project_pair_workspace(const slimkv_down_project_args* a, const slimkv_down_project_args* b);
+int slimkv_down_project_pair(const slimkv_down_project_args* a, const slimkv_down_project_args* b, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 /* The down-projection with its epilogue writing the latents straight into
  * beacon pages (no dense staging, no separate append).  Replaces the

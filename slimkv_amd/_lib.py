@@ -124,6 +124,8 @@ PrefillRopeArgs = _struct('slimkv_prefill_rope_args', [
     ('positions', c_ptr), ('pos_sb', c_i64),
     ('roles', c_ptr), ('role_len', c_i64),
     *_i64s('batch', 'heads', 'kv_heads', 'queries', 'keys', 'dim', 'sink'),
+    ('v', c_ptr), *_i64s('v_sb', 'v_sh', 'v_ss'),
+    ('out_v', c_ptr), *_i64s('ov_sb', 'ov_sh', 'ov_ss'),
 ])
 
 MergeArgs = _struct('slimkv_merge_args', [
@@ -241,6 +243,7 @@ SIGNATURES = {
     'slimkv_prepare_latent_bases': (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
     'slimkv_prepare_rope_pairs': (ctypes.c_int, [c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr]),
     'slimkv_reconstruct': (ctypes.c_int, [ctypes.POINTER(ReconstructArgs), c_ptr]),
+    'slimkv_reconstruct_pair': (ctypes.c_int, [ctypes.POINTER(ReconstructArgs), ctypes.POINTER(ReconstructArgs), c_ptr]),
     'slimkv_recon_decode_workspace': (ctypes.c_size_t, [ctypes.POINTER(ReconDecodeArgs)]),
     'slimkv_recon_decode': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_recon_decode_stages': (ctypes.c_int, [ctypes.POINTER(ReconDecodeArgs), ctypes.c_int, c_ptr,
@@ -255,6 +258,10 @@ SIGNATURES = {
     'slimkv_prefill_attention': (ctypes.c_int, [ctypes.POINTER(PrefillAttentionArgs), c_ptr]),
     'slimkv_down_project_workspace': (ctypes.c_size_t, [ctypes.POINTER(DownProjectArgs)]),
     'slimkv_down_project': (ctypes.c_int, [ctypes.POINTER(DownProjectArgs), c_ptr, ctypes.c_size_t, c_ptr]),
+    'slimkv_down_project_pair_workspace': (ctypes.c_size_t, [ctypes.POINTER(DownProjectArgs),
+                                                             ctypes.POINTER(DownProjectArgs)]),
+    'slimkv_down_project_pair': (ctypes.c_int, [ctypes.POINTER(DownProjectArgs), ctypes.POINTER(DownProjectArgs),
+                                                c_ptr, ctypes.c_size_t, c_ptr]),
     'slimkv_down_project_to_pages': (ctypes.c_int, [ctypes.POINTER(DownProjectArgs), ctypes.POINTER(PageRows), c_ptr,
                                                     ctypes.c_size_t, c_ptr]),
     'slimkv_beacon_pages': (ctypes.c_int, [ctypes.POINTER(BeaconPagesArgs), c_ptr]),
@@ -262,7 +269,7 @@ SIGNATURES = {
     'slimkv_paged_step_rows': (ctypes.c_int, [ctypes.POINTER(PagedStepRowsArgs), c_ptr]),
 }
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 STAGE_PROLOGUE, STAGE_ATTEND, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 7
 NOALLOC_SCRATCH_BYTES = 32 << 20

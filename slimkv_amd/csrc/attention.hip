@@ -2445,7 +2445,7 @@ using namespace slimkv;
 
 extern "C" const char* slimkv_last_error(void) { return g_error.c_str(); }
 
-extern "C" int slimkv_abi_version(void) { return 14; }
+extern "C" int slimkv_abi_version(void) { return 15; }
 
 extern "C" size_t slimkv_attention_workspace(const slimkv_attention_args* a) {
     AttnPlan plan{};

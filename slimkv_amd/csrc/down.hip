@@ -57,14 +57,14 @@ __device__ __forceinline__ u32x4 zero_if_not(bool ok, u32x4 v) {
     return u32x4{ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
 }
 
-__global__ void __launch_bounds__(256) down_kernel(DownParams p) {
+__device__ __forceinline__ void down_body(const DownParams& p, int block) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int ngroups = (p.N + 63) / 64;
     const int M = p.B * p.n;
     const int mtiles = (M + 16 * kMFrags - 1) / (16 * kMFrags);
-    const int s = blockIdx.x % p.splits;
-    const int rest = blockIdx.x / p.splits;
+    const int s = block % p.splits;
+    const int rest = block / p.splits;
     const int ng = rest % ngroups;
     const int mt = rest / ngroups;
     if (mt >= mtiles) return;
@@ -133,6 +133,16 @@ __global__ void __launch_bounds__(256) down_kernel(DownParams p) {
     }
 }
 
+__global__ void __launch_bounds__(256) down_kernel(DownParams p) { down_body(p, blockIdx.x); }
+
+// Two down-projections without split partials in one launch (the K and V
+// latents of a window's beacon rows): the first `blocks0` workgroups run the
+// first, the rest the second, each as the single kernel's workgroup.
+__global__ void __launch_bounds__(256) down_pair_kernel(DownParams p0, DownParams p1, int blocks0) {
+    if ((int)blockIdx.x < blocks0) down_body(p0, blockIdx.x);
+    else down_body(p1, blockIdx.x - blocks0);
+}
+
 // Sum the split partials in split order and round once to bf16.
 __global__ void __launch_bounds__(256) down_reduce_kernel(DownParams p) {
     const int64_t M = (int64_t)p.B * p.n;
@@ -198,15 +208,8 @@ extern "C" size_t slimkv_down_project_workspace(const slimkv_down_project_args* 
 
 namespace {
 
-int down_run(const slimkv_down_project_args* a, const slimkv_page_rows* pg, void* workspace, size_t workspace_bytes,
-             void* stream) {
-    DownPlan plan{};
-    int rc = plan_down(a, &plan);
-    if (rc != SLIMKV_OK) return rc;
-    if (plan.bytes && (!workspace || workspace_bytes < plan.bytes))
-        return fail(SLIMKV_EWORKSPACE, "workspace too small");
-    const int64_t M = a->batch * a->row_count;
-    if (M == 0) return SLIMKV_OK;
+DownParams down_params(const slimkv_down_project_args* a, const slimkv_page_rows* pg, const DownPlan& plan,
+                       void* workspace) {
     DownParams p{};
     p.x = static_cast<const uint16_t*>(a->x); p.x_sb = a->x_sb; p.x_sl = a->x_sl;
     p.rows = a->rows; p.length = a->length;
@@ -222,7 +225,25 @@ int down_run(const slimkv_down_project_args* a, const slimkv_page_rows* pg, void
         p.start = pg->start;
         p.status = pg->status;
     }
-    const int64_t grid = (p.N + 63) / 64 * ((M + 63) / 64) * p.splits;
+    return p;
+}
+
+int64_t down_grid(const DownParams& p) {
+    const int64_t M = (int64_t)p.B * p.n;
+    return (p.N + 63) / 64 * ((M + 63) / 64) * p.splits;
+}
+
+int down_run(const slimkv_down_project_args* a, const slimkv_page_rows* pg, void* workspace, size_t workspace_bytes,
+             void* stream) {
+    DownPlan plan{};
+    int rc = plan_down(a, &plan);
+    if (rc != SLIMKV_OK) return rc;
+    if (plan.bytes && (!workspace || workspace_bytes < plan.bytes))
+        return fail(SLIMKV_EWORKSPACE, "workspace too small");
+    const int64_t M = a->batch * a->row_count;
+    if (M == 0) return SLIMKV_OK;
+    const DownParams p = down_params(a, pg, plan, workspace);
+    const int64_t grid = down_grid(p);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(down_kernel, dim3((unsigned)grid), dim3(256), 0, st, p);
     rc = check_hip(hipGetLastError(), "down-projection launch");
@@ -232,11 +253,46 @@ int down_run(const slimkv_down_project_args* a, const slimkv_page_rows* pg, void
     return check_hip(hipGetLastError(), "down-projection reduce launch");
 }
 
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
 }  // namespace
 
 extern "C" int slimkv_down_project(const slimkv_down_project_args* a, void* workspace, size_t workspace_bytes,
                                    void* stream) {
     return down_run(a, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t slimkv_down_project_pair_workspace(const slimkv_down_project_args* a,
+                                                     const slimkv_down_project_args* b) {
+    DownPlan pa{}, pb{};
+    if (plan_down(a, &pa) != SLIMKV_OK || plan_down(b, &pb) != SLIMKV_OK) return 0;
+    return std::max<size_t>(align256(pa.bytes) + pb.bytes, 1);
+}
+
+extern "C" int slimkv_down_project_pair(const slimkv_down_project_args* a, const slimkv_down_project_args* b,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+    DownPlan pa{}, pb{};
+    int rc = plan_down(a, &pa);
+    if (rc != SLIMKV_OK) return rc;
+    rc = plan_down(b, &pb);
+    if (rc != SLIMKV_OK) return rc;
+    const size_t need = align256(pa.bytes) + pb.bytes;
+    if (need && (!workspace || workspace_bytes < need)) return fail(SLIMKV_EWORKSPACE, "workspace too small");
+    char* ws = static_cast<char*>(workspace);
+    const int64_t Ma = a->batch * a->row_count, Mb = b->batch * b->row_count;
+    if (pa.splits > 1 || pb.splits > 1 || Ma == 0 || Mb == 0) {
+        // split partials (a reduce launch each) or an empty problem: one at a time
+        rc = down_run(a, nullptr, ws, align256(pa.bytes), stream);
+        if (rc != SLIMKV_OK) return rc;
+        return down_run(b, nullptr, ws ? ws + align256(pa.bytes) : nullptr, pb.bytes, stream);
+    }
+    const DownParams p0 = down_params(a, nullptr, pa, nullptr);
+    const DownParams p1 = down_params(b, nullptr, pb, nullptr);
+    const int64_t g0 = down_grid(p0), g1 = down_grid(p1);
+    if (g0 + g1 > 0x7fffffff) return fail(SLIMKV_EINVAL, "down-projection grid too large");
+    hipLaunchKernelGGL(down_pair_kernel, dim3((unsigned)(g0 + g1)), dim3(256), 0, static_cast<hipStream_t>(stream), p0,
+                       p1, (int)g0);
+    return check_hip(hipGetLastError(), "down-projection pair launch");
 }
 
 extern "C" int slimkv_down_project_to_pages(const slimkv_down_project_args* a, const slimkv_page_rows* dst,

@@ -104,14 +104,13 @@ recon_kernel(ReconParams p) {
 // the next tile's latent rows already in flight, so W is read once per
 // wavefront instead of once per tile.  Same epilogue as recon_kernel.
 template <int KSTEPS>
-__global__ void __launch_bounds__(kReconWaves * 64)
-recon_stream_kernel(ReconParams p, int segs) {
+__device__ __forceinline__ void recon_stream_body(const ReconParams& p, int segs, int block) {
     constexpr int D = 128;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    const int h = blockIdx.x % p.Hkv;
-    const int seg = (blockIdx.x / p.Hkv) % segs;
-    const int b = blockIdx.x / (p.Hkv * segs);
+    const int h = block % p.Hkv;
+    const int seg = (block / p.Hkv) % segs;
+    const int b = block / (p.Hkv * segs);
     const int tiles = (p.n + 15) / 16;
     const int stride = segs * kReconWaves;
     const int k_lo = p.blockdiag ? h * p.k_lo_step : 0;
@@ -192,6 +191,23 @@ recon_stream_kernel(ReconParams p, int segs) {
     }
 }
 
+template <int KSTEPS>
+__global__ void __launch_bounds__(kReconWaves * 64)
+recon_stream_kernel(ReconParams p, int segs) {
+    recon_stream_body<KSTEPS>(p, segs, blockIdx.x);
+}
+
+// Two reconstructions of the same latent width in one launch (the K and the
+// V rebuild of a window's beacons): the first `blocks0` workgroups run the
+// first, the rest the second -- each the single kernel's workgroup, so the
+// results are the single launches' bits.
+template <int KSTEPS>
+__global__ void __launch_bounds__(kReconWaves * 64)
+recon_stream_pair_kernel(ReconParams p0, ReconParams p1, int segs0, int segs1, int blocks0) {
+    if ((int)blockIdx.x < blocks0) recon_stream_body<KSTEPS>(p0, segs0, blockIdx.x);
+    else recon_stream_body<KSTEPS>(p1, segs1, blockIdx.x - blocks0);
+}
+
 namespace {
 bool al4(int64_t x) { return (x & 3) == 0; }
 bool pal8(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 7) == 0; }
@@ -209,11 +225,17 @@ hipError_t launch_stream(const ReconParams& p, int segs, hipStream_t st) {
 }
 }  // namespace
 
-int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
-    if (!a || !a->latent || !a->weight || !a->out) return fail(SLIMKV_EINVAL, "null pointer");
+// Checks a reconstruction and fills its kernel parameters; `segs` > 0 when it
+// takes the streaming kernel (latent width kw <= 64), whose workgroup count is
+// B * Hkv * segs.
+int prepare_recon(const slimkv_reconstruct_args* a, ReconParams* out, int* segs, int* kw_out) {
+    if (!a) return fail(SLIMKV_EINVAL, "null pointer");
     if (a->batch <= 0 || a->rows < 0 || a->rank <= 0 || a->kv_heads <= 0 || a->head_dim != 128)
         return fail(SLIMKV_EINVAL, "invalid reconstruction sizes (head_dim must be 128)");
-    if (a->rows == 0) return SLIMKV_OK;
+    *segs = 0;
+    *kw_out = 0;
+    if (a->rows == 0) return SLIMKV_OK;               // nothing to read or write (empty tensors may be null)
+    if (!a->latent || !a->weight || !a->out) return fail(SLIMKV_EINVAL, "null pointer");
     const bool bd = a->block_diagonal != 0;
     const int64_t kw = bd ? a->rank / a->kv_heads : a->rank;
     if ((bd && a->rank % a->kv_heads) || kw % 16 || kw > 512)
@@ -225,7 +247,8 @@ int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
     if (a->positions && (!a->cos || !a->sin || a->rope_rows <= 0)) return fail(SLIMKV_EINVAL, "RoPE needs tables");
     if (a->positions && a->batch > 1 && a->pos_sb < a->rows)
         return fail(SLIMKV_EINVAL, "positions rows are shorter than the row count");
-    ReconParams p{};
+    ReconParams& p = *out;
+    p = ReconParams{};
     p.latent = static_cast<const uint16_t*>(a->latent); p.l_sb = a->l_sb; p.l_sn = a->l_sn;
     p.w = static_cast<const uint16_t*>(a->weight); p.bias = static_cast<const uint16_t*>(a->bias); p.w_ld = a->rank;
     p.out = static_cast<uint16_t*>(a->out); p.o_sb = a->o_sb; p.o_sn = a->o_sn; p.o_sh = a->o_sh;
@@ -234,15 +257,23 @@ int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
     p.positions = a->positions; p.pos_sb = a->pos_sb;
     p.B = (int)a->batch; p.n = (int)a->rows; p.R = (int)a->rank; p.Hkv = (int)a->kv_heads;
     p.blockdiag = bd ? 1 : 0; p.k_lo_step = (int)kw;
-    hipError_t e;
+    *kw_out = (int)kw;
     const bool tables16 = !a->positions || (((reinterpret_cast<uintptr_t>(a->cos) | reinterpret_cast<uintptr_t>(a->sin)) & 15) == 0);
     if (kw <= 64 && tables16) {
         // streaming kernel: about 1024 workgroups, each wavefront at least one tile
         const int row_tiles = (p.n + 15) / 16;
         const int64_t heads = (int64_t)p.B * p.Hkv;
-        const int segs = (int)std::max<int64_t>(1, std::min<int64_t>((row_tiles + kReconWaves - 1) / kReconWaves,
-                                                                     (1024 + heads - 1) / heads));
-        if ((int64_t)p.B * p.Hkv * segs > 0x7fffffff) return fail(SLIMKV_EINVAL, "reconstruction grid too large");
+        const int sg = (int)std::max<int64_t>(1, std::min<int64_t>((row_tiles + kReconWaves - 1) / kReconWaves,
+                                                                   (1024 + heads - 1) / heads));
+        if ((int64_t)p.B * p.Hkv * sg > 0x3fffffff) return fail(SLIMKV_EINVAL, "reconstruction grid too large");
+        *segs = sg;
+    }
+    return SLIMKV_OK;
+}
+
+int launch_prepared(const ReconParams& p, int segs, int kw, hipStream_t st) {
+    hipError_t e;
+    if (segs > 0) {
         switch (kw / 16) {
             case 1: e = launch_stream<1>(p, segs, st); break;
             case 2: e = launch_stream<2>(p, segs, st); break;
@@ -268,8 +299,54 @@ int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
     return check_hip(e, "reconstruction kernel launch");
 }
 
+template <int K>
+hipError_t launch_stream_pair(const ReconParams& p0, int segs0, const ReconParams& p1, int segs1, hipStream_t st) {
+    const int blocks0 = p0.B * p0.Hkv * segs0;
+    const int blocks1 = p1.B * p1.Hkv * segs1;
+    hipLaunchKernelGGL((recon_stream_pair_kernel<K>), dim3(blocks0 + blocks1), dim3(kReconWaves * 64), 0, st, p0, p1,
+                       segs0, segs1, blocks0);
+    return hipGetLastError();
+}
+
+int reconstruct(const slimkv_reconstruct_args* a, hipStream_t st) {
+    ReconParams p;
+    int segs = 0, kw = 0;
+    const int rc = prepare_recon(a, &p, &segs, &kw);
+    if (rc != SLIMKV_OK || a->rows == 0) return rc;
+    return launch_prepared(p, segs, kw, st);
+}
+
+int reconstruct_pair(const slimkv_reconstruct_args* a, const slimkv_reconstruct_args* b, hipStream_t st) {
+    ReconParams pa, pb;
+    int sa = 0, sb = 0, ka = 0, kb = 0;
+    int rc = prepare_recon(a, &pa, &sa, &ka);
+    if (rc != SLIMKV_OK) return rc;
+    rc = prepare_recon(b, &pb, &sb, &kb);
+    if (rc != SLIMKV_OK) return rc;
+    if (a->rows == 0) return b->rows == 0 ? SLIMKV_OK : launch_prepared(pb, sb, kb, st);
+    if (b->rows == 0) return launch_prepared(pa, sa, ka, st);
+    if (sa > 0 && sb > 0 && ka == kb) {
+        hipError_t e;
+        switch (ka / 16) {
+            case 1: e = launch_stream_pair<1>(pa, sa, pb, sb, st); break;
+            case 2: e = launch_stream_pair<2>(pa, sa, pb, sb, st); break;
+            case 3: e = launch_stream_pair<3>(pa, sa, pb, sb, st); break;
+            default: e = launch_stream_pair<4>(pa, sa, pb, sb, st); break;
+        }
+        return check_hip(e, "reconstruction pair launch");
+    }
+    // different kernels or widths: two launches
+    rc = launch_prepared(pa, sa, ka, st);
+    return rc != SLIMKV_OK ? rc : launch_prepared(pb, sb, kb, st);
+}
+
 }  // namespace slimkv
 
 extern "C" int slimkv_reconstruct(const slimkv_reconstruct_args* a, void* stream) {
     return slimkv::reconstruct(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int slimkv_reconstruct_pair(const slimkv_reconstruct_args* a, const slimkv_reconstruct_args* b,
+                                       void* stream) {
+    return slimkv::reconstruct_pair(a, b, static_cast<hipStream_t>(stream));
 }

@@ -136,6 +136,11 @@ prefill_rope_kernel(PrefillRopeParams p) {
         }
         const int64_t pos = beacon ? -1 : clamp_i64(a.positions[b * a.pos_sb + s], 0, a.rope_rows - 1);
         rope8(src, dst, dd, D, a.cos, a.sin, pos);
+        if (a.v) {
+            const uint16_t* vs = static_cast<const uint16_t*>(a.v) + b * a.v_sb + hh * a.v_sh + s * a.v_ss;
+            uint16_t* vd = static_cast<uint16_t*>(a.out_v) + b * a.ov_sb + hh * a.ov_sh + s * a.ov_ss;
+            *reinterpret_cast<u32x4*>(vd + dd) = *reinterpret_cast<const u32x4*>(vs + dd);
+        }
     }
 }
 
@@ -164,6 +169,10 @@ prefill_rope_rows_kernel(PrefillRopeParams p) {
     int64_t pos[kRopeRows];
     bool live[kRopeRows], beacon[kRopeRows];
     u32x4 x[kRopeRows];
+    // value rows copied beside the key rows (a.v set): source and destination
+    // of row i, null for query rows
+    const uint16_t* vsrc[kRopeRows];
+    uint16_t* vdst[kRopeRows];
 #pragma unroll
     for (int i = 0; i < kRopeRows; ++i) {
         const uint32_t r = group * kRopeRows + i;
@@ -175,6 +184,8 @@ prefill_rope_rows_kernel(PrefillRopeParams p) {
             dst[i] = static_cast<uint16_t*>(a.out_q) + (int64_t)b * a.oq_sb + (int64_t)hh * a.oq_sh + (int64_t)s * a.oq_ss;
             pos[i] = a.positions[(int64_t)b * a.pos_sb + a.keys - a.queries + s];
             beacon[i] = false;
+            vsrc[i] = nullptr;
+            vdst[i] = nullptr;
         } else {
             const uint32_t kr = rr - Q;
             const uint32_t s = kr % keys, t = kr / keys, hh = t % kv_heads, b = t / kv_heads;
@@ -184,9 +195,19 @@ prefill_rope_rows_kernel(PrefillRopeParams p) {
             const bool in_window = (int64_t)s >= prefix;
             const int64_t role = in_window ? a.roles[(int64_t)s - prefix] : 0;
             beacon[i] = in_window ? (role == 1 || role == 2) : ((int64_t)s >= a.sink);
+            vsrc[i] = a.v ? static_cast<const uint16_t*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hh * a.v_sh +
+                                (int64_t)s * a.v_ss
+                          : nullptr;
+            vdst[i] = a.v ? static_cast<uint16_t*>(a.out_v) + (int64_t)b * a.ov_sb + (int64_t)hh * a.ov_sh +
+                                (int64_t)s * a.ov_ss
+                          : nullptr;
         }
         x[i] = *reinterpret_cast<const u32x4*>(src[i] + dd);
     }
+    // the value rows go out with the key rows' loads and are stored as they are
+#pragma unroll
+    for (int i = 0; i < kRopeRows; ++i)
+        if (live[i] && vsrc[i]) *reinterpret_cast<u32x4*>(vdst[i] + dd) = *reinterpret_cast<const u32x4*>(vsrc[i] + dd);
     float4 cv[kRopeRows][2], sv[kRopeRows][2];
 #pragma unroll
     for (int i = 0; i < kRopeRows; ++i) {
@@ -300,6 +321,13 @@ extern "C" int slimkv_prefill_rope(const slimkv_prefill_rope_args* a, void* stre
         if (!al8(st)) return fail(SLIMKV_EINVAL, "strides must be multiples of 8 elements");
     if (!pal16(a->q) || !pal16(a->k) || !pal16(a->out_q) || !pal16(a->out_k))
         return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
+    if (a->v) {
+        if (!a->out_v) return fail(SLIMKV_EINVAL, "null pointer");
+        const int64_t vstrides[] = {a->v_sb, a->v_sh, a->v_ss, a->ov_sb, a->ov_sh, a->ov_ss};
+        for (int64_t st : vstrides)
+            if (!al8(st)) return fail(SLIMKV_EINVAL, "strides must be multiples of 8 elements");
+        if (!pal16(a->v) || !pal16(a->out_v)) return fail(SLIMKV_EINVAL, "tensors must be 16-byte aligned");
+    }
     PrefillRopeParams p{};
     p.a = *a;
     p.q_rows = a->batch * a->heads * a->queries;

@@ -129,6 +129,42 @@ def down_project(x, weight, rows=None, *, blocks=1, out=None):
     (all rows).  `blocks` > 1 declares a block-diagonal weight.  Returns
     out [B, n, N] bf16.
     """
+    a, out, keep = _down_args(x, weight, rows, blocks, out)
+    nbytes = lib().slimkv_down_project_workspace(ctypes.byref(a))
+    if nbytes == 0:
+        check(-1)
+    ws = _workspace(nbytes, out.device)
+    check(lib().slimkv_down_project(ctypes.byref(a), _ptr(ws), nbytes, _lib.stream_handle(out.device)))
+    return out
+
+
+def down_project_pair(first, second):
+    """Two down-projections in one launch where the library can (the K and V
+    latents of a window's beacon rows), the same bits as two down_project
+    calls.  `first` / `second`: dicts of down_project's arguments (x, weight,
+    rows, blocks, out).  Returns the two outputs."""
+    names = ('x', 'weight', 'rows', 'blocks', 'out')
+    for kw in (first, second):
+        if set(kw) - set(names):
+            raise TypeError(f'unknown down_project arguments {sorted(set(kw) - set(names))}')
+    a, out_a, keep_a = _down_args(first['x'], first['weight'], first.get('rows'), first.get('blocks', 1),
+                                  first.get('out'))
+    b, out_b, keep_b = _down_args(second['x'], second['weight'], second.get('rows'), second.get('blocks', 1),
+                                  second.get('out'))
+    if out_a.device != out_b.device:
+        raise ValueError('both down-projections must be on one device')
+    nbytes = lib().slimkv_down_project_pair_workspace(ctypes.byref(a), ctypes.byref(b))
+    if nbytes == 0:
+        check(-1)
+    ws = _workspace(nbytes, out_a.device)
+    check(lib().slimkv_down_project_pair(ctypes.byref(a), ctypes.byref(b), _ptr(ws), nbytes,
+                                         _lib.stream_handle(out_a.device)))
+    return out_a, out_b
+
+
+def _down_args(x, weight, rows, blocks, out):
+    """The slimkv_down_project_args of one down-projection, its output and the
+    tensors the arguments point into."""
     _need_device(x, weight, rows)
     _need_bf16(x, weight)
     if x.dim() != 3 or weight.dim() != 2 or weight.shape[1] != x.shape[2]:
@@ -146,12 +182,7 @@ def down_project(x, weight, rows=None, *, blocks=1, out=None):
         raise ValueError('out must be [B, n, N] with contiguous rows')
     a = _lib.DownProjectArgs(_ptr(x), x.stride(0), x.stride(1), _ptr(rows), n, L, _ptr(weight),
                              _ptr(out), out.stride(0), out.stride(1), B, K, N, int(blocks))
-    nbytes = lib().slimkv_down_project_workspace(ctypes.byref(a))
-    if nbytes == 0:
-        check(-1)
-    ws = _workspace(nbytes, x.device)
-    check(lib().slimkv_down_project(ctypes.byref(a), _ptr(ws), nbytes, _lib.stream_handle(x.device)))
-    return out
+    return a, out, (x, weight, rows, out)
 
 
 def down_project_to_pages(x, weight, pages, table, layout, start, kind, rows=None, *, blocks=1, status=None):
@@ -449,6 +480,38 @@ def reconstruct(latent, weight, bias=None, *, kv_heads, out=None, dst_rows=None,
     """Up-project latent rows [B, n, R] with an nn.Linear weight [Hkv*D, R] into
     out [B, rows, Hkv, D] (any 4-D view with a contiguous last dim), optionally
     scattered to dst_rows and RoPE'd at positions [B, n]."""
+    a, out, keep = _reconstruct_args(latent, weight, bias, kv_heads, out, dst_rows, positions, cos, sin,
+                                     block_diagonal)
+    check(lib().slimkv_reconstruct(ctypes.byref(a), _lib.stream_handle(keep[0].device)))
+    return out
+
+
+def reconstruct_pair(first, second):
+    """Two reconstructions in one launch where the library can (both on its
+    streaming kernel at one latent width, as the K and V rebuild of a
+    window's beacon rows are), the same bits as two reconstruct calls.
+    `first` / `second`: dicts of reconstruct's arguments.  Returns the two
+    outputs."""
+    a, out_a, keep_a = _reconstruct_args(**_recon_kwargs(first))
+    b, out_b, keep_b = _reconstruct_args(**_recon_kwargs(second))
+    if keep_a[0].device != keep_b[0].device:
+        raise ValueError('both reconstructions must be on one device')
+    check(lib().slimkv_reconstruct_pair(ctypes.byref(a), ctypes.byref(b), _lib.stream_handle(keep_a[0].device)))
+    return out_a, out_b
+
+
+def _recon_kwargs(kw):
+    names = ('latent', 'weight', 'bias', 'kv_heads', 'out', 'dst_rows', 'positions', 'cos', 'sin', 'block_diagonal')
+    unknown = set(kw) - set(names)
+    if unknown:
+        raise TypeError(f'unknown reconstruct arguments {sorted(unknown)}')
+    defaults = dict(bias=None, out=None, dst_rows=None, positions=None, cos=None, sin=None, block_diagonal=False)
+    return {n: kw.get(n, defaults.get(n)) for n in names}
+
+
+def _reconstruct_args(latent, weight, bias, kv_heads, out, dst_rows, positions, cos, sin, block_diagonal):
+    """The slimkv_reconstruct_args of one reconstruction, its output, and the
+    tensors the arguments point into (kept alive until the launch)."""
     _need_device(latent, weight, bias, out)
     _need_bf16(latent, weight, bias, out)
     latent = _last_contiguous(latent)
@@ -468,8 +531,7 @@ def reconstruct(latent, weight, bias=None, *, kv_heads, out=None, dst_rows=None,
         _ptr(cos), _ptr(sin), 0 if cos is None else cos.shape[0],
         _ptr(positions), 0 if positions is None else positions.stride(0),
         B, n, R, kv_heads, D, int(bool(block_diagonal)))
-    check(lib().slimkv_reconstruct(ctypes.byref(a), _lib.stream_handle(latent.device)))
-    return out
+    return a, out, (latent, weight, bias, out, dst_rows, positions, cos, sin)
 
 
 def recon_decode(q, raw_k, raw_v, lat_k, lat_v, up_k, up_v, scale, *, beacon_positions=None, up_k_bias=None,
@@ -664,15 +726,22 @@ def prefill_rope(q, k, cos, sin, positions, roles, sink, out_q=None, out_k=None)
     return oq, ok
 
 
-def rope_keys(k, cos, sin, positions, roles, sink, out_k=None):
+def rope_keys(k, cos, sin, positions, roles, sink, out_k=None, v=None, out_v=None):
     """The key half of prefill_rope: k [B,Hk,Nk,D] rotated (beacon keys
     copied unchanged) into out_k (default empty_like); for an attention that
-    rotates its own queries (prefill_attention with q_positions)."""
-    _need_device(k, cos, sin, positions, roles, out_k)
-    _need_bf16(k, out_k)
+    rotates its own queries (prefill_attention with q_positions).  With v
+    and out_v (both of k's shape) the value rows are copied into out_v in the
+    same launch."""
+    _need_device(k, cos, sin, positions, roles, out_k, v, out_v)
+    _need_bf16(k, out_k, v, out_v)
     ok = torch.empty_like(k) if out_k is None else out_k
     if ok.shape != k.shape or ok.stride(-1) != 1:
         raise ValueError('the RoPE output must have the shape of k with contiguous rows')
+    if (v is None) != (out_v is None):
+        raise ValueError('the value rows need both v and out_v')
+    if v is not None and (v.shape != k.shape or out_v.shape != k.shape or v.stride(-1) != 1 or
+                          out_v.stride(-1) != 1):
+        raise ValueError('v and out_v must have the shape of k with contiguous rows')
     pos = positions if positions.stride(-1) == 1 else positions.contiguous()
     roles = roles.to(device=k.device, dtype=torch.int64).contiguous()
     B, Hk, Nk, D = k.shape
@@ -681,7 +750,9 @@ def rope_keys(k, cos, sin, positions, roles, sink, out_k=None):
         None, 0, 0, 0, _ptr(ok), *ok.stride()[:3],
         _ptr(cos), _ptr(sin), cos.shape[0], _ptr(pos), pos.stride(0),
         _ptr(roles), roles.numel(),
-        B, Hk, Hk, 0, Nk, D, int(sink))
+        B, Hk, Hk, 0, Nk, D, int(sink),
+        _ptr(v), *(v.stride()[:3] if v is not None else (0, 0, 0)),
+        _ptr(out_v), *(out_v.stride()[:3] if out_v is not None else (0, 0, 0)))
     check(lib().slimkv_prefill_rope(ctypes.byref(a), _lib.stream_handle(k.device)))
     return ok
 

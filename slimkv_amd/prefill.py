@@ -69,6 +69,17 @@ def _low_rank(attention, hidden, rows, down, up, dest, heads):
     return latent
 
 
+def _low_rank_pair(hidden, rows, downs, ups, dests, heads):
+    """_low_rank for K and V together: both down-projections in one launch,
+    then both reconstructions in one (the same bits as one at a time)."""
+    latents = kernels.down_project_pair(
+        *({'x': hidden, 'weight': d.weight, 'rows': rows, 'blocks': _blocks(d.weight, heads)} for d in downs))
+    kernels.reconstruct_pair(
+        *({'latent': lat, 'weight': u.weight, 'bias': u.bias, 'kv_heads': heads, 'out': dst, 'dst_rows': rows,
+           'block_diagonal': is_block_diagonal(u.weight, heads)} for lat, u, dst in zip(latents, ups, dests)))
+    return latents
+
+
 def project_with_beacon(attention, hidden, beacon_size, beacon_indices, metadata):
     """(q [B,L,Hq*D], k [B,L,Hk,D], v [B,L,Hk,D], key latents, value latents);
     qkv_proj_with_beacon with return_latents (modeling_llama.py:1291-1345)."""
@@ -87,12 +98,15 @@ def project_with_beacon(attention, hidden, beacon_size, beacon_indices, metadata
     if 'q' in config.beacon_param and rows.numel():
         q[:, rows] = attention.beacon_q_proj(hidden[:, rows])
     key_latent = value_latent = None
-    if 'k' in config.beacon_param:
-        down = attention.beacon_kv_down_proj if shared else attention.beacon_k_down_proj
-        key_latent = _low_rank(attention, hidden, rows, down, attention.beacon_k_up_proj, k, Hk)
-    if 'v' in config.beacon_param:
-        down = attention.beacon_kv_down_proj if shared else attention.beacon_v_down_proj
-        value_latent = _low_rank(attention, hidden, rows, down, attention.beacon_v_up_proj, v, Hk)
+    k_down = attention.beacon_kv_down_proj if shared else getattr(attention, 'beacon_k_down_proj', None)
+    v_down = attention.beacon_kv_down_proj if shared else getattr(attention, 'beacon_v_down_proj', None)
+    if 'k' in config.beacon_param and 'v' in config.beacon_param:
+        key_latent, value_latent = _low_rank_pair(hidden, rows, (k_down, v_down),
+                                                  (attention.beacon_k_up_proj, attention.beacon_v_up_proj), (k, v), Hk)
+    elif 'k' in config.beacon_param:
+        key_latent = _low_rank(attention, hidden, rows, k_down, attention.beacon_k_up_proj, k, Hk)
+    elif 'v' in config.beacon_param:
+        value_latent = _low_rank(attention, hidden, rows, v_down, attention.beacon_v_up_proj, v, Hk)
     if replicas:
         # role 2 rows replicate the window's first beacons (parallel encoding)
         firsts, copies = _rows_where(current, 1), _rows_where(current, 2)
@@ -185,11 +199,11 @@ class PrefillHistory:
             base = self.sink + self.history
             if base + n > self.k.shape[2] or key_latent.shape[0] != self.k.shape[0]:
                 raise ValueError('prefill history capacity exceeded')
-            for lat, up, dst in ((key_latent, attention.beacon_k_up_proj, self.k),
-                                 (value_latent, attention.beacon_v_up_proj, self.v)):
-                kernels.reconstruct(lat, up.weight, up.bias, kv_heads=heads,
-                                    out=dst[:, :, base:base + n].transpose(1, 2),
-                                    block_diagonal=is_block_diagonal(up.weight, heads))
+            kernels.reconstruct_pair(
+                *({'latent': lat, 'weight': up.weight, 'bias': up.bias, 'kv_heads': heads,
+                   'out': dst[:, :, base:base + n].transpose(1, 2), 'block_diagonal': is_block_diagonal(up.weight, heads)}
+                  for lat, up, dst in ((key_latent, attention.beacon_k_up_proj, self.k),
+                                       (value_latent, attention.beacon_v_up_proj, self.v))))
             self.history += n
 
 
@@ -244,8 +258,10 @@ def prefill_forward(attention, hidden_states, position_ids, past_key_value, hist
         cos, sin = _rope_tables(attention.rotary_emb, query, current_k, metadata, base + L)
         if roles.numel() != L:
             raise ValueError('the prefill history rotates the window\'s keys: roles must cover the window')
-        value_rows.copy_(current_v)
-        kernels.rope_keys(current_k, cos, sin, positions[:, base:], roles, 0, out_k=key_rows)
+        # the window's keys rotated into the key set, its values copied into
+        # the value set, in one launch
+        kernels.rope_keys(current_k, cos, sin, positions[:, base:], roles, 0, out_k=key_rows, v=current_v,
+                          out_v=value_rows)
         k_rot, value_states = store.sets(L)
     else:
         key_states = past_key.materialize(attention, current_k)

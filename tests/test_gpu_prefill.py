@@ -281,3 +281,80 @@ def test_prefill_window_matches_oracle(device, per_head_down, bias, n_hist):
     assert none is None
     assert_close(to_np(out), want.reshape(B, L, 8 * D))
     assert update[2] == 8 and update.raw_indices.tolist() == (roles == 0).nonzero().flatten().tolist()
+
+
+@pytest.mark.parametrize('rk,rv,rows_v', [(32, 32, 256), (16, 16, 100), (32, 16, 256), (64, 64, 0)])
+def test_reconstruct_pair_equals_single_launches(device, rk, rv, rows_v):
+    """slimkv_reconstruct_pair (the K and V rebuild of a window's beacon rows
+    in one launch; widths that differ, or an empty second problem, take two
+    launches): the bits of two slimkv_reconstruct calls, scatter and bias
+    included."""
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import block_diagonal, orthonormal_columns
+    gen = torch.Generator(device=device).manual_seed(rk + rv + rows_v)
+    cpu = torch.Generator().manual_seed(5)
+    B, Hk, D, L = 3, 8, 128, 300
+    lat_k = torch.randn(B, 256, Hk * rk, generator=gen, device=device).to(torch.bfloat16)
+    lat_v = torch.randn(B, rows_v, Hk * rv, generator=gen, device=device).to(torch.bfloat16)
+    up_k = block_diagonal([orthonormal_columns(D, rk, cpu) for _ in range(Hk)]).to(device, torch.bfloat16)
+    up_v = block_diagonal([orthonormal_columns(D, rv, cpu) for _ in range(Hk)]).to(device, torch.bfloat16)
+    bias = torch.randn(Hk * D, generator=gen, device=device).to(torch.bfloat16)
+    rows_k = torch.randperm(L, generator=torch.Generator().manual_seed(6))[:256].sort().values.to(device)
+    outs = [torch.zeros(B, L, Hk, D, dtype=torch.bfloat16, device=device) for _ in range(4)]
+    first = dict(latent=lat_k, weight=up_k, bias=bias, kv_heads=Hk, dst_rows=rows_k, block_diagonal=True)
+    second = dict(latent=lat_v, weight=up_v, kv_heads=Hk, block_diagonal=True)
+    kernels.reconstruct_pair(dict(first, out=outs[0]), dict(second, out=outs[1]))
+    kernels.reconstruct(**dict(first, out=outs[2]))
+    kernels.reconstruct(**dict(second, out=outs[3]))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+    assert outs[0].abs().sum() > 0 and (rows_v == 0 or outs[1].abs().sum() > 0)
+
+
+@pytest.mark.parametrize('K,N,blocks,n', [(1024, 256, 8, 256), (4096, 256, 1, 64), (512, 128, 1, 1000)])
+def test_down_project_pair_equals_single_launches(device, K, N, blocks, n):
+    """slimkv_down_project_pair: one launch for two projections without split
+    partials, one after the other with them (the long contraction of the
+    second case); the bits of two slimkv_down_project calls."""
+    from slimkv_amd import kernels
+    gen = torch.Generator(device=device).manual_seed(K + N + n)
+    B, L = 2, max(n, 300)
+    x = [torch.randn(B, L, K, generator=gen, device=device).to(torch.bfloat16) for _ in range(2)]
+    w = []
+    for _ in range(2):
+        m = torch.randn(N, K, generator=gen, device=device)
+        if blocks > 1:
+            mask = torch.block_diag(*[torch.ones(N // blocks, K // blocks, device=device)] * blocks)
+            m = m * mask
+        w.append(m.to(torch.bfloat16))
+    rows = torch.randperm(L, generator=torch.Generator().manual_seed(7))[:n].to(device)
+    pair = kernels.down_project_pair(*({'x': x[j], 'weight': w[j], 'rows': rows, 'blocks': blocks} for j in (0, 1)))
+    single = [kernels.down_project(x[j], w[j], rows, blocks=blocks) for j in (0, 1)]
+    torch.cuda.synchronize()
+    assert torch.equal(pair[0], single[0]) and torch.equal(pair[1], single[1])
+
+
+def test_rope_keys_copies_values_in_the_same_launch(device):
+    """rope_keys with v / out_v: the rotated keys are rope_keys' alone and the
+    value rows land unchanged, strided views on both sides."""
+    from slimkv_amd import kernels
+    from slimkv_amd.workloads import rope_tables
+    gen = torch.Generator(device=device).manual_seed(8)
+    B, Hk, L, D, cap = 2, 8, 333, 128, 500
+    k = torch.randn(B, L, Hk, D, generator=gen, device=device).to(torch.bfloat16).transpose(1, 2)
+    v = torch.randn(B, L, Hk, D, generator=gen, device=device).to(torch.bfloat16).transpose(1, 2)
+    cos, sin = rope_tables(cap, D, 500000.0, device)
+    positions = torch.arange(cap, device=device)[None].expand(B, -1)[:, 100:100 + L]
+    roles = torch.zeros(L, dtype=torch.long, device=device)
+    roles[4::5] = 1
+    store_k = torch.zeros(B, Hk, cap, D, dtype=torch.bfloat16, device=device)
+    store_v = torch.zeros_like(store_k)
+    kernels.rope_keys(k, cos, sin, positions, roles, 0, out_k=store_k[:, :, 100:100 + L], v=v,
+                      out_v=store_v[:, :, 100:100 + L])
+    alone = kernels.rope_keys(k, cos, sin, positions, roles, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(store_k[:, :, 100:100 + L], alone)
+    assert torch.equal(store_v[:, :, 100:100 + L], v)
+    assert not store_v[:, :, :100].any() and not store_v[:, :, 100 + L:].any()
+    with pytest.raises(ValueError):
+        kernels.rope_keys(k, cos, sin, positions, roles, 0, v=v)

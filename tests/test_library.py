@@ -55,7 +55,7 @@ def test_struct_layouts_match_header_field_order():
     header = (ROOT / 'include' / 'slimkv_hip.h').read_text()
     for struct in STRUCTS(_lib):
         body = re.search(r'typedef struct %s \{(.*?)\}' % struct.__name__, header, re.S).group(1)
-        body = re.sub(r'/\*.*?\*/', '', body)
+        body = re.sub(r'/\*.*?\*/', '', body, flags=re.S)
         fields = re.findall(r'\*?\s*([a-z_][a-z0-9_]*)\s*(?=[,;])', body)
         assert fields == [f[0] for f in struct._fields_], struct.__name__
 
