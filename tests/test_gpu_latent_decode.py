@@ -350,10 +350,45 @@ def test_qwen_gqa5_shape(device, H, rank, queries, bias):
     and shift consumed by the attend and combine stages, over ragged latent
     lengths; and against the oracle (fa2_decode.py:143-164, the biases at
     :157-163)."""
+    _gqa_layer(device, H, 8, rank, queries, bias)
+
+
+# (query heads, KV heads, rank, queries, bias): Qwen2.5-7B's 28 on 4 (seven a
+# KV head: one or two KV heads a wave, 14 query rows with two queries),
+# multi-query attention (one KV head: one wave column set of 8 or 16 rows),
+# and groups of three on 4 KV heads.
+KV_HEAD_CASES = [(28, 4, 32, 1, True), (28, 4, 16, 2, False), (28, 4, 48, 1, False), (8, 1, 32, 1, False),
+                 (8, 1, 48, 2, True), (8, 1, 16, 1, True), (12, 4, 16, 1, True), (12, 4, 32, 2, False),
+                 (16, 2, 32, 1, False)]
+
+
+@pytest.mark.parametrize('H,Hkv,rank,queries,bias', KV_HEAD_CASES)
+def test_kv_head_counts(device, H, Hkv, rank, queries, bias):
+    """Other KV head counts: the tile plan keeps whole KV heads in a wave and
+    its head count divides the KV heads; same checks as the Qwen2.5-14B
+    layout."""
+    _gqa_layer(device, H, Hkv, rank, queries, bias)
+
+
+def test_more_than_sixteen_query_rows_a_kv_head_is_refused(device):
+    """128 query heads on 8 KV heads with two queries are 32 query rows a KV
+    head, beyond one 16-column MFMA tile: the library refuses the call (the
+    workspace query, which plans the call first, reports the planner's
+    error)."""
+    from slimkv_amd import kernels
+    case = latent_case(batch=1, heads=128, context=400 + 132, tail=128, rank_k=32, rank_v=32, seed=5,
+                       device=device)
+    q = torch.zeros(1, 2, 128, 128, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match='16 query rows'):
+        kernels.latent_decode(q, case.raw_k, case.raw_v, case.lat_k, case.lat_v, case.up_k, case.up_v,
+                              case.scale, block_diagonal=True, lat_causal=True)
+
+
+def _gqa_layer(device, H, Hkv, rank, queries, bias):
     from slimkv_amd import kernels
     B = 5
-    case = latent_case(batch=B, heads=H, context=1400 + 132, tail=128, rank_k=rank, rank_v=rank,
-                       seed=7 * rank + queries + bias + H, device=device)
+    case = latent_case(batch=B, heads=H, kv_heads=Hkv, context=1400 + 132, tail=128, rank_k=rank, rank_v=rank,
+                       seed=7 * rank + queries + bias + H + 1000 * (Hkv != 8), device=device)
     if queries == 2:
         gen = torch.Generator(device=device).manual_seed(93)
         case.q = torch.randn(B, 2, H, 128, generator=gen, device=device).to(torch.bfloat16)
