@@ -33,7 +33,7 @@ _STAGE_PROLOGUE, _STAGE_ATTEND, _STAGE_ALL = 1, 2, 7      # SLIMKV_STAGE_* of in
 # `bench.py --workload recon|paged --steps 1 --warmup 1 --no-cpu`, scaled as the
 # latent decode's (FETCH_SIZE counts half the bytes read, WRITE_SIZE the bytes
 # written, from the ceiling probe's transfers of known size).
-RECON_TRAFFIC_BYTES = int((2 * 38_287.3 + 1_644.0) * 1024)      # recon_split_kernel<2, 1, 2>
+RECON_TRAFFIC_BYTES = int((2 * 38_293.9 + 1_644.2) * 1024)      # recon_split_kernel<2, 1, 2>
 PAGED_TRAFFIC_BYTES = int((2 * 321_411.8 + 10_669.7) * 1024)    # split_kernel<4, 8, 1, 0, 1>
 TRAFFIC_SOURCE = ('rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this workload\'s kernel, scaled by the ceiling '
                   'probe\'s stream reads and fills')

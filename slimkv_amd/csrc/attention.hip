@@ -1059,7 +1059,10 @@ struct ReconSeg {
 // lane's row (its RoPE pairs are fetched two tiles before the tile is used).
 template <int KSR, int VL>
 struct ReconTile {
-    u32x2 k[KSR];         // latent K pieces of the lane's key (B operand of the rebuild)
+    // latent K pieces of the lane's key (B operand of the rebuild): 32 latent
+    // dims a 16x16x32 MFMA, then 16 a 16x16x16 one when KSR is odd
+    u32x4 kq[KSR / 2 > 0 ? KSR / 2 : 1];
+    u32x2 kr;
     u32x4 v[VL];          // latent V pieces on their way to LDS
     int64_t pos;
 };
@@ -1118,7 +1121,8 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
     const int vis = min(lim, r_end);
     const int last_row = sg.n - 1;
 
-    const uint16_t* kbase = sg.lk + (int64_t)b * sg.lk_sb + (int64_t)h * rk + 4 * grp;
+    constexpr int KP = KSR / 2, KO = KSR & 1;         // 32-deep rebuild steps, then a 16-deep one
+    const uint16_t* kbase = sg.lk + (int64_t)b * sg.lk_sb + (int64_t)h * rk;
     const uint16_t* vbase = sg.lv + (int64_t)b * sg.lv_sb + (int64_t)h * RV;
     const int64_t* pbase = ROPE ? sg.pos + (int64_t)b * sg.pos_sb : nullptr;
 
@@ -1130,7 +1134,8 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         const int r0 = it < ntile ? r_begin + it * r_step : r_begin;
         const uint16_t* src = kbase + (int64_t)min(r0 + col, last_row) * sg.lk_sn;
 #pragma unroll
-        for (int ks = 0; ks < KSR; ++ks) t.k[ks] = *reinterpret_cast<const u32x2*>(src + 16 * ks);
+        for (int m = 0; m < KP; ++m) t.kq[m] = *reinterpret_cast<const u32x4*>(src + 32 * m + 8 * grp);
+        if constexpr (KO) t.kr = *reinterpret_cast<const u32x2*>(src + 32 * KP + 4 * grp);
 #pragma unroll
         for (int c = 0; c < VL; ++c) {
             const int p = 64 * c + lane;
@@ -1147,14 +1152,18 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         for (int tt = 0; tt < 4; ++tt) cs[tt] = *reinterpret_cast<const u32x4*>(src + 16 * tt);
     };
 
-    // U_K tile of this head (A operand of the rebuild) and the bias, once.
-    u32x2 wa[8][KSR];
+    // U_K tile of this head (A operand of the rebuild) and the bias, once:
+    // lane (col, grp) holds row 16tt + col at the latent dims its latent
+    // pieces hold (32m + 8grp + [0, 8), then 32KP + 4grp + [0, 4)).
+    u32x4 wq[8][KP > 0 ? KP : 1];
+    u32x2 wr[8];
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt)
+    for (int tt = 0; tt < 8; ++tt) {
+        const uint16_t* wrow = sg.w + ((int64_t)h * D + 16 * tt + col) * sg.w_ld + h * rk;
 #pragma unroll
-        for (int ks = 0; ks < KSR; ++ks)
-            wa[tt][ks] = *reinterpret_cast<const u32x2*>(sg.w + ((int64_t)h * D + 16 * tt + col) * sg.w_ld + h * rk +
-                                                         16 * ks + 4 * grp);
+        for (int m = 0; m < KP; ++m) wq[tt][m] = *reinterpret_cast<const u32x4*>(wrow + 32 * m + 8 * grp);
+        if constexpr (KO) wr[tt] = *reinterpret_cast<const u32x2*>(wrow + 32 * KP + 4 * grp);
+    }
     uint32_t bias2[8][2];
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt) {
@@ -1252,10 +1261,13 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
 #pragma unroll
         for (int tt = 0; tt < 8; ++tt) kc[tt] = kinit[tt];
 #pragma unroll
-        for (int ks = 0; ks < KSR; ++ks) {
-            const v4s bop = as_v4s(t.k[ks].x, t.k[ks].y);
+        for (int m = 0; m < KP; ++m)
 #pragma unroll
-            for (int tt = 0; tt < 8; ++tt) kc[tt] = mfma16(as_v4s(wa[tt][ks].x, wa[tt][ks].y), bop, kc[tt]);
+            for (int tt = 0; tt < 8; ++tt) kc[tt] = mfma32(wq[tt][m], t.kq[m], kc[tt]);
+        if constexpr (KO) {
+            const v4s bop = as_v4s(t.kr.x, t.kr.y);
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) kc[tt] = mfma16(as_v4s(wr[tt].x, wr[tt].y), bop, kc[tt]);
         }
         if constexpr (ROPE == 2) {
             // x = acc + bias (the bias was the accumulator's start), y[d] =
@@ -1318,12 +1330,17 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
     auto phase_b = [&](const u32x2 (&kop)[8], int it) {
         const int r0 = r_begin + it * r_step;
         uint16_t* vb = vbuf + (it & 1) * 16 * RSV;
-        // scores S^T[key, col]
+        // scores S^T[key, col] on 16x16x32 MFMAs: a lane's eight k values are
+        // dims 32p + 4grp + [0, 4) and 32p + 16 + 4grp + [0, 4) of both the
+        // rotated key (kop) and the query (qop), so the contraction covers
+        // each dim once
         v4f sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tt = 0; tt < 8; tt += 2) {
-            sc0 = mfma16(as_v4s(kop[tt].x, kop[tt].y), as_v4s(qop[tt].x, qop[tt].y), sc0);
-            sc1 = mfma16(as_v4s(kop[tt + 1].x, kop[tt + 1].y), as_v4s(qop[tt + 1].x, qop[tt + 1].y), sc1);
+        for (int tt = 0; tt < 8; tt += 4) {
+            sc0 = mfma32(u32x4{kop[tt].x, kop[tt].y, kop[tt + 1].x, kop[tt + 1].y},
+                         u32x4{qop[tt].x, qop[tt].y, qop[tt + 1].x, qop[tt + 1].y}, sc0);
+            sc1 = mfma32(u32x4{kop[tt + 2].x, kop[tt + 2].y, kop[tt + 3].x, kop[tt + 3].y},
+                         u32x4{qop[tt + 2].x, qop[tt + 2].y, qop[tt + 3].x, qop[tt + 3].y}, sc1);
         }
         const v4f sc = sc0 + sc1;
         float sv[4];
@@ -2994,8 +3011,8 @@ struct ReconPlan {
     size_t qrot_off, k_off, v_off, rml_off, racc_off, bml_off, bacc_off, total;
 };
 
-// The fused route: block-diagonal bases, per-head K rank 16..48 and V rank 32
-// or 64, the alignment its 8- and 16-byte loads need, and prepared RoPE pairs
+// The fused route: block-diagonal bases, per-head K rank 16, 32 or 48 and V
+// rank 32 or 64, the alignment its 8- and 16-byte loads need, and prepared RoPE pairs
 // when the beacon keys are rotated.
 bool recon_fused_ok(const slimkv_recon_decode_args* r) {
     const slimkv_latent_decode_args* a = &r->base;
@@ -3005,7 +3022,11 @@ bool recon_fused_ok(const slimkv_recon_decode_args* r) {
     const int64_t rk = a->rank_k / Hkv, rv = a->rank_v / Hkv;
     if (rk % 16 || rk < 16 || rk > 48 || (rv != 32 && rv != 64) || (rk == 48 && rv == 64)) return false;
     auto al = [](const void* ptr, uintptr_t m) { return (reinterpret_cast<uintptr_t>(ptr) & (m - 1)) == 0; };
-    if (!al(a->lat_k, 8) || (a->lk_sb & 3) || (a->lk_sn & 3) || !al(a->up_k, 8) || (a->rank_k & 3)) return false;
+    // 16-byte latent K and U_K pieces at per-head K ranks of 32 and 48 (the
+    // 32-deep rebuild MFMA), 8-byte ones at 16
+    const int64_t km = rk >= 32 ? 8 : 4;
+    if (!al(a->lat_k, 2 * km) || (a->lk_sb % km) || (a->lk_sn % km) || !al(a->up_k, 2 * km) || (a->rank_k % km))
+        return false;
     if (a->up_k_bias && !al(a->up_k_bias, 8)) return false;
     if (!al(a->lat_v, 16) || !aligned8(a->lv_sb) || !aligned8(a->lv_sn)) return false;
     if (!al(a->up_v, 16) || !aligned8(a->rank_v)) return false;
@@ -3055,8 +3076,9 @@ int plan_recon(const slimkv_recon_decode_args* r, ReconPlan* p) {
         // One beacon workgroup per CU (the split count rounded down): a
         // launch whose workgroups do not spread evenly over the CUs lasts as
         // long as its most loaded CU, and two per CU measured slower than one
-        // (C2 layer: 16 splits, one a CU, 35.3 us; 32 splits 37.8 us; 24 or
-        // 40 splits 47-52 us).  The short raw workgroups run ahead of them.
+        // (B8 layer, 40/8 heads, 8192 beacons of rank 32: 16 splits, one a
+        // CU, 34.8 us; 32 splits 40.1 us; 8, 12, 20, 24 or 48 splits 41.6-52.9
+        // us).  The short raw workgroups run ahead of them.
         const int64_t groups = (int64_t)B * ((Hkv + kWaves - 1) / kWaves);
         // as for the latent decode: stay within the fast combine's split count
         const int wv = 32 * p->vl;
