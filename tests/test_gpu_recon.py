@@ -154,6 +154,48 @@ def test_recon_decode_qwen14b_layer_shape(device, beacon_rope, reference_roundin
     assert_lse_close(to_np(lse), lse_e)
 
 
+# (query heads, KV heads, rank, two queries, bias): Qwen2.5-7B's 28 on 4,
+# multi-query attention (one KV head: three of a workgroup's four waves have
+# no head), 16 on 2 and groups of three on 4 KV heads
+RECON_KV_HEAD_CASES = [(28, 4, 32, False, True), (28, 4, 48, True, False), (8, 1, 32, False, False),
+                       (8, 1, 16, True, True), (16, 2, 32, True, True), (12, 4, 32, False, False)]
+
+
+@pytest.mark.parametrize('reference_rounding', [False, True])
+@pytest.mark.parametrize('H,Hkv,rank,insertion,bias', RECON_KV_HEAD_CASES)
+def test_recon_decode_fused_kv_head_counts(device, H, Hkv, rank, insertion, bias, reference_rounding):
+    """The fused route (a wave per KV head, K rebuilt and rotated per tile)
+    over other KV head counts and GQA groups, with beacon K-RoPE, against
+    the float64 and bf16-eager oracles."""
+    from slimkv_amd import kernels
+    B = 3
+    case = latent_case(batch=B, heads=H, kv_heads=Hkv, context=1536 + 132, tail=128, rank_k=rank, rank_v=32,
+                       seed=H + 10 * Hkv + rank, device=device)
+    gen = torch.Generator(device=device).manual_seed(H + rank)
+    bk = bv = None
+    if bias:
+        bk = (0.3 * torch.randn(case.up_k.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+        bv = (0.3 * torch.randn(case.up_v.shape[0], generator=gen, device=device)).to(torch.bfloat16)
+    if insertion:
+        case.q = torch.cat([case.q, torch.randn(case.q.shape, generator=gen, device=device).to(torch.bfloat16)], 1)
+        case.q_positions = torch.cat([case.q_positions, case.q_positions + 1], 1)
+        case.cos, case.sin = rope_tables(int(case.q_positions.max()) + 1, 128, 500000.0, device)
+    q_rot, k_rot = _rotate(case)
+    nl = case.lat_k.shape[1]
+    bpos = (torch.arange(nl, device=device) * 4 + 4)[None].expand(B, -1).contiguous()
+    out, lse = kernels.recon_decode(case.q, k_rot.transpose(1, 2), case.raw_v, case.lat_k, case.lat_v, case.up_k,
+                                    case.up_v, case.scale, beacon_positions=bpos, up_k_bias=bk, up_v_bias=bv,
+                                    block_diagonal=True, lat_causal=insertion, q_positions=case.q_positions,
+                                    cos=case.cos, sin=case.sin, reference_rounding=reference_rounding)
+    torch.cuda.synchronize()
+    exact, eager, lse_e = _recon_oracles(case, q_rot, k_rot, bpos, insertion, bk, bv,
+                                         rounding='reference' if reference_rounding else 'fp32')
+    got = to_np(out.transpose(1, 2))
+    assert_close(got, exact, what='vs float64')
+    assert_close(got, eager, what='vs bf16 eager')
+    assert_lse_close(to_np(lse), lse_e)
+
+
 @pytest.mark.parametrize('rank', [256, 64])
 def test_recon_decode_insertion_step_with_biases_general_weights(device, rank):
     """General (not block-diagonal) bases: rank 256 rebuilds V, rank 64 keeps V
