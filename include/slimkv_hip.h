@@ -282,9 +282,11 @@ int slimkv_reconstruct_pair(const slimkv_reconstruct_args* a, const slimkv_recon
  *   (tools/benchmark/context_decode_runtime.py:298-344).
  * Argument meaning as slimkv_latent_decode; lat_causal makes the beacon
  * segment bottom-right causal (the raw query of an insertion step does not
- * see the new beacon).  With block-diagonal bases (per-head K rank 16..48, V
- * rank 32 or 64) each K tile is rebuilt and rotated inside the attention
- * kernel and V is lifted after the weighted sum; rotated beacon keys then
+ * see the new beacon).  With block-diagonal bases (per-head K rank 16, 32 or
+ * 48, V rank 32 or 64; lat_k and up_k 16-byte aligned with row strides a
+ * multiple of 8 elements at K ranks 32 and 48, 8-byte and 4 at rank 16) each
+ * K tile is rebuilt and rotated inside the attention kernel and V is lifted
+ * after the weighted sum; rotated beacon keys then
  * need rope_pairs (slimkv_prepare_rope_pairs of the same cos/sin tables) and
  * rope_repeats = 1 (rotate-half tables, cos/sin = cat(f, f): the reference's
  * RotaryEmbedding, modeling_utils.py:369-376).  Otherwise the workspace holds
