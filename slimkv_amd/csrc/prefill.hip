@@ -323,16 +323,10 @@ prefill_kernel(PrefillParams p) {
                     }
             }
             mx = rows_max(mx);
-            // The column's reference maximum (log2 units) moves only when a
-            // scaled score exceeds it by more than 8, so P stays below 2^8 and
-            // most tiles keep alpha = 1 for every column of the wave (the
-            // rescale below is skipped): the 8-window C3 step's attention
-            // 1.409-1.431 -> 1.380-1.382 ms.
             const float m_new = fmaxf(m[nt], mx * p.scale_log2);
-            const float ref = m_new > m[nt] + 8.f ? m_new : m[nt];
-            const float base = ref == kNegInf ? 0.f : ref;
+            const float base = m_new == kNegInf ? 0.f : m_new;
             const float alpha = fast_exp2(m[nt] - base);
-            m[nt] = ref;
+            m[nt] = m_new;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll

@@ -81,6 +81,29 @@ def test_wide_query_tiles_on_sampled_heads(device, B, Lq, N, Hq, Hk, seqlens):
         assert_lse_close(to_np(lse[b:b + 1, h:h + 1]), l)
 
 
+def test_reference_maximum_moves_mid_sequence(device):
+    """Keys with large norms late in the sequence (rows 100-109 six times, rows
+    600-619 twelve times the others) lift the scores of the queries that see
+    them by far more than 2^8 (log2 units) after many tiles of ordinary keys:
+    the kernel's reference maximum moves mid-sequence and the accumulated
+    output is rescaled; against the oracle."""
+    from slimkv_amd import kernels
+    B, Lq, N, Hq, Hk = 2, 300, 900, 8, 2
+    gen = torch.Generator(device=device).manual_seed(77)
+    q = torch.randn(B, Lq, Hq, 128, generator=gen, device=device)
+    k = torch.randn(B, N, Hk, 128, generator=gen, device=device)
+    v = torch.randn(B, N, Hk, 128, generator=gen, device=device)
+    k[:, 100:110] *= 6.0
+    k[:, 600:620] *= 12.0
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    scale = 128 ** -0.5
+    out, lse = kernels.prefill_attention(q, k, v, scale, True)
+    torch.cuda.synchronize()
+    want, want_lse = oa.eager_forward(to_np(q), to_np(k), to_np(v), scale, True)
+    assert_close(to_np(out), want)
+    assert_lse_close(to_np(lse), want_lse)
+
+
 def test_non_causal_and_strided_kv(device):
     _run(device, 2, 90, 250, 8, 2, False, seed=1, strided=True)
 
