@@ -838,16 +838,18 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
             sc1 = mfma16(as_v4s(tile.k[c].z, tile.k[c].w), as_v4s(qv[c].z, qv[c].w), sc1);
         }
         const v4f sc = sc0 + sc1;
+        // raw scores (the scale is positive: it is applied to the maximum
+        // and inside the exponent's FMA)
         float sv[4];
         float tmax = kNegInf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int n = r0 + 4 * grp + i;
-            const float x = n < vis ? sc[i] * scale_log2 : kNegInf;
+            const float x = n < vis ? sc[i] : kNegInf;
             sv[i] = x;
             tmax = fmaxf(tmax, x);
         }
-        tmax = rows_max(tmax);
+        tmax = rows_max(tmax) * scale_log2;
         const float mnew = fmaxf(m, tmax);
         const float mref = mnew == kNegInf ? 0.f : mnew;
         const float alpha = fast_exp2(m - mref);
@@ -855,7 +857,7 @@ __device__ __forceinline__ void split_segment(const Seg& sg, int w, int B, int L
         float psum = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            p[i] = fast_exp2(sv[i] - mref);
+            p[i] = fast_exp2(fmaf(sv[i], scale_log2, -mref));
             psum += p[i];
         }
         lsum = lsum * alpha + psum;
@@ -1343,16 +1345,18 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
                          u32x4{qop[tt + 2].x, qop[tt + 2].y, qop[tt + 3].x, qop[tt + 3].y}, sc1);
         }
         const v4f sc = sc0 + sc1;
+        // raw scores (the scale is positive: it is applied to the maximum
+        // and inside the exponent's FMA)
         float sv[4];
         float tmax = kNegInf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int nn = r0 + 4 * grp + i;
-            const float xv = nn < vis ? sc[i] * scale_log2 : kNegInf;
+            const float xv = nn < vis ? sc[i] : kNegInf;
             sv[i] = xv;
             tmax = fmaxf(tmax, xv);
         }
-        tmax = rows_max(tmax);
+        tmax = rows_max(tmax) * scale_log2;
         const float mnew = fmaxf(m, tmax);
         const float mref = mnew == kNegInf ? 0.f : mnew;
         const float alpha = fast_exp2(m - mref);
@@ -1360,7 +1364,7 @@ __device__ __forceinline__ void recon_segment(const ReconSeg& sg, int w, int Lq,
         float psum = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            pr[i] = fast_exp2(sv[i] - mref);
+            pr[i] = fast_exp2(fmaf(sv[i], scale_log2, -mref));
             psum += pr[i];
         }
         lsum = lsum * alpha + psum;
