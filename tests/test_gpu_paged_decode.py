@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 HQ, HKV, D = 32, 8, 128
 
 
-def _case(device, layout_args, lengths, raw_lengths, seed=0, pool_extra=7, garbage=True):
+def _case(device, layout_args, lengths, raw_lengths, seed=0, pool_extra=7, garbage=True, heads=HQ):
     from slimkv_amd.paged_cache import BeaconPageLayout
     layout = BeaconPageLayout(*layout_args)
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -49,7 +49,7 @@ def _case(device, layout_args, lengths, raw_lengths, seed=0, pool_extra=7, garba
     max_raw = max(raw_lengths)
     raw_k = torch.randn(B, max_raw, HKV, D, generator=gen, device=device).to(torch.bfloat16)
     raw_v = torch.randn(B, max_raw, HKV, D, generator=gen, device=device).to(torch.bfloat16)
-    q = torch.randn(B, 1, HQ, D, generator=gen, device=device).to(torch.bfloat16)
+    q = torch.randn(B, 1, heads, D, generator=gen, device=device).to(torch.bfloat16)
     return dict(layout=layout, pages=pages, tables=tables.to(device), up_k=up_k, up_v=up_v, raw_k=raw_k,
                 raw_v=raw_v, q=q, lengths=torch.tensor(lengths, dtype=torch.int32, device=device),
                 raw_lengths=torch.tensor(raw_lengths, dtype=torch.int32, device=device), lat_keys=max(lengths))
@@ -109,6 +109,32 @@ def test_compact_schedule_matches_oracle(device, rows_total, layout_args):
     lat_k, lat_v = _dense(c)
     torch.cuda.synchronize()
     q = to_np(c['q'].transpose(1, 2))                                  # [B, H, 1, D]
+    raw_k, raw_v = to_np(c['raw_k'].transpose(1, 2)), to_np(c['raw_v'].transpose(1, 2))
+    up_k, up_v = to_np(c['up_k']), to_np(c['up_v'])
+    for b, (n, nr) in enumerate(zip(lengths, raw_lengths)):
+        ref, ref_lse = oa.latent_layer(q[b:b + 1], raw_k[b:b + 1, :, :nr], raw_v[b:b + 1, :, :nr],
+                                       to_np(lat_k)[b:b + 1, None, :n], to_np(lat_v)[b:b + 1, None, :n],
+                                       up_k, up_v, scale, HKV)
+        assert_close(to_np(got.transpose(1, 2))[b:b + 1], ref, what=f'sequence {b}')
+        np.testing.assert_allclose(to_np(lse)[b:b + 1], ref_lse, atol=2e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize('heads', [40, 64, 16])
+def test_compact_schedule_other_gqa_groups(device, heads):
+    """Query heads 40, 64 and 16 on the 8 KV heads of the page layout (GQA
+    groups of five, eight and two: the latent tiles hold whole KV heads),
+    beacon and raw rows from their pages' dense gather, against the oracle."""
+    from slimkv_amd import kernels
+    lengths = [3000, 1, 0, 2047, 777]
+    raw_lengths = [133, 1, 7, 64, 100]
+    c = _case(device, (16, 8, 256, 256, 1024), lengths, raw_lengths, seed=heads, heads=heads)
+    scale = D ** -0.5
+    got, lse = kernels.paged_latent_decode(c['q'], c['raw_k'], c['raw_v'], c['pages'], c['tables'], c['lengths'],
+                                           c['lat_keys'], c['layout'], c['up_k'], c['up_v'], scale,
+                                           rows_total=sum(lengths), block_diagonal=True, raw_lengths=c['raw_lengths'])
+    lat_k, lat_v = _dense(c)
+    torch.cuda.synchronize()
+    q = to_np(c['q'].transpose(1, 2))
     raw_k, raw_v = to_np(c['raw_k'].transpose(1, 2)), to_np(c['raw_v'].transpose(1, 2))
     up_k, up_v = to_np(c['up_k']), to_np(c['up_v'])
     for b, (n, nr) in enumerate(zip(lengths, raw_lengths)):
